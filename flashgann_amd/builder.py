@@ -1,0 +1,304 @@
+"""Codebook builder: graph construction and per-edge RaBitQ encoding.
+
+The reference consumes a prebuilt SymphonyQG-style codebook and ships no
+builder (README.md:12, include/qg.hpp:16).  This module writes one in the
+reference's layout (include/qg.hpp:66-73).  It runs on whatever torch device
+it is handed: the GPU for million-point indexes, the CPU for test fixtures.
+
+Graph.  Exactly `degree` out-edges per node:
+  * local edges (degree - degree/4 slots): exact k-nearest candidates
+    (k = 2*degree) pruned with the relative-neighbourhood rule (drop v if a
+    kept w has d(w,v) < d(u,v)), backfilled from the candidates in distance
+    order;
+  * long links (degree/4 slots): seeded uniform-random targets.  Mixture data
+    with well-separated components has no between-component edges in a k-NN
+    graph; random links make every component reachable and let the beam
+    search sample other components cheaply through RaBitQ estimates.
+Neighbour lists are sorted by (distance, id); short lists (tiny N) are padded
+with 0xFFFFFFFF, which the search treats as "no neighbour".
+
+Encoding (per edge u -> v, residual r = v - u zero-padded to B, P = H_B diag(s)
+the unnormalised Walsh-Hadamard rotation the search applies to the query,
+include/utils.cuh:790-821):
+    y = P r,  b_i = [y_i > 0],  s_i = 2 b_i - 1
+  L2:  f = -2 |r|^2 / sum|y|;  factor_dq = f;  factor_vq = f * sum(s);
+       triple_x = |r|^2 - f * <s, P u>
+  IP:  f = -|r|^2 / sum|y|;    factor_dq = f;  factor_vq = f * sum(s);
+       triple_x = 0
+so that the search's estimate (include/utils.cuh:989-993)
+    triple_x + d(q,u) + factor_dq*width*(2*raw - sum_q) + factor_vq*low
+is the RaBitQ estimate of d(q,v) with P q ~ low + width*q_i.  Factors are
+computed in float64 and rounded to float32.  A zero residual (duplicate point)
+gets f = 0 and triple_x = 0.  Edges to padding get triple_x = FLT_MAX.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from .codebook import MAX_INDEX, Codebook, Layout, code_bit_positions
+
+FLT_MAX = float(np.finfo(np.float32).max)
+
+
+def _sqnorm(x: torch.Tensor) -> torch.Tensor:
+    return (x * x).sum(-1)
+
+
+def knn(base: torch.Tensor, k: int, queries: torch.Tensor | None = None,
+        exclude_self: bool = True, chunk_elems: int = 1 << 28):
+    """Exact k nearest neighbours by L2 (or of `queries` against `base`).
+
+    Returns (ids int64 [m,k], sqdist float32 [m,k]) ordered by (dist, id).
+    Squared distances are |x|^2 + |y|^2 - 2 x.y in float32, exact for
+    integer-valued data with |.|^2 < 2^24."""
+    q = base if queries is None else queries
+    n = base.shape[0]
+    m = q.shape[0]
+    kk = min(k, n - (1 if exclude_self and queries is None else 0))
+    extra = min(16, n - kk)
+    bn = _sqnorm(base)
+    rows = max(1, min(m, chunk_elems // max(1, n)))
+    ids_out = torch.empty((m, kk), dtype=torch.int64, device=base.device)
+    d_out = torch.empty((m, kk), dtype=torch.float32, device=base.device)
+    for s in range(0, m, rows):
+        e = min(m, s + rows)
+        qs = q[s:e]
+        d = _sqnorm(qs)[:, None] + bn[None, :] - 2.0 * (qs @ base.T)
+        d.clamp_(min=0.0)
+        if exclude_self and queries is None:
+            r = torch.arange(s, e, device=base.device)
+            d[r - s, r] = float("inf")
+        kc = min(n, kk + extra)
+        dv, di = torch.topk(d, kc, dim=1, largest=False, sorted=True)
+        # order by (dist, id): sort by id, then stable sort by dist
+        o = torch.argsort(di, dim=1)
+        di = torch.gather(di, 1, o)
+        dv = torch.gather(dv, 1, o)
+        o = torch.argsort(dv, dim=1, stable=True)
+        ids_out[s:e] = torch.gather(di, 1, o)[:, :kk]
+        d_out[s:e] = torch.gather(dv, 1, o)[:, :kk]
+    return ids_out, d_out
+
+
+def _pairwise_sq(v: torch.Tensor) -> torch.Tensor:
+    """v: (m, c, d) -> (m, c, c) squared distances."""
+    nv = _sqnorm(v)
+    g = torch.bmm(v, v.transpose(1, 2).contiguous())
+    return (nv[:, :, None] + nv[:, None, :] - 2.0 * g).clamp_(min=0.0)
+
+
+def _prune(cand: torch.Tensor, cd: torch.Tensor, x: torch.Tensor, limit: int,
+           alpha2: float = 1.0, chunk: int = 4096) -> torch.Tensor:
+    """Greedy (alpha-)RNG pruning of ordered candidate lists.
+
+    cand (n, c) int64 (-1 = none), cd (n, c) squared distances to the owner.
+    Keeps candidate i unless an earlier kept w has alpha2 * d(w, v_i) < d(u, v_i)
+    (alpha2 = 1: relative neighbourhood rule), at most `limit` kept.
+    Returns a bool mask (n, c)."""
+    n, c = cand.shape
+    out = torch.zeros((n, c), dtype=torch.bool, device=cand.device)
+    for s in range(0, n, chunk):
+        e = min(n, s + chunk)
+        cc = cand[s:e]
+        valid = cc >= 0
+        v = x[cc.clamp(min=0)]
+        pd = _pairwise_sq(v)
+        du = cd[s:e]
+        kept = torch.zeros((e - s, c), dtype=torch.bool, device=cand.device)
+        count = torch.zeros((e - s,), dtype=torch.int64, device=cand.device)
+        for i in range(c):
+            ok = valid[:, i] & (count < limit)
+            if i > 0:
+                bad = ((alpha2 * pd[:, i, :i] < du[:, i : i + 1]) & kept[:, :i]).any(1)
+                ok &= ~bad
+            kept[:, i] = ok
+            count += ok.to(torch.int64)
+        out[s:e] = kept
+    return out
+
+
+def _first_unique(m: torch.Tensor, width: int) -> torch.Tensor:
+    """Row-wise: first `width` distinct non-negative entries of m in order,
+    padded with -1."""
+    rows, L = m.shape
+    pos = torch.arange(L, device=m.device).expand(rows, L)
+    key = torch.where(m >= 0, m, torch.full_like(m, -1))
+    o = torch.argsort(key, dim=1, stable=True)
+    sk = torch.gather(key, 1, o)
+    dup_sorted = torch.zeros_like(sk, dtype=torch.bool)
+    dup_sorted[:, 1:] = sk[:, 1:] == sk[:, :-1]
+    dup = torch.zeros_like(dup_sorted)
+    dup.scatter_(1, o, dup_sorted)
+    drop = dup | (m < 0)
+    rank = drop.to(torch.int64) * L + pos
+    o2 = torch.argsort(rank, dim=1)[:, :width]
+    sel = torch.gather(m, 1, o2)
+    sel_drop = torch.gather(drop, 1, o2)
+    sel = torch.where(sel_drop, torch.full_like(sel, -1), sel)
+    if sel.shape[1] < width:
+        pad = torch.full((rows, width - sel.shape[1]), -1, dtype=sel.dtype, device=sel.device)
+        sel = torch.cat([sel, pad], 1)
+    return sel
+
+
+def hadamard_rotation(signs: np.ndarray, device) -> torch.Tensor:
+    """P = H_B diag(signs) as float64 (B x B), H_B the Sylvester matrix."""
+    b = signs.shape[0]
+    idx = torch.arange(b, dtype=torch.int64)
+    parity = torch.zeros((b, b), dtype=torch.int64)
+    a = idx[:, None] & idx[None, :]
+    while bool((a != 0).any()):
+        parity ^= a & 1
+        a = a >> 1
+    h = (1 - 2 * parity).to(torch.float64)
+    return (h * torch.as_tensor(signs, dtype=torch.float64)[None, :]).to(device)
+
+
+def build_graph(x: torch.Tensor, degree: int, random_links: int | None = None,
+                seed: int = 0x5EED, verbose: bool = False) -> torch.Tensor:
+    """Returns (n, degree) int64 neighbour ids (-1 = padding)."""
+    n = x.shape[0]
+    dev = x.device
+    kc = min(2 * degree, n - 1)
+    cand, cd = knn(x, kc)
+    if verbose:
+        print(f"[builder] knn done k={kc}", flush=True)
+    nr = degree // 4 if random_links is None else random_links
+    nr = min(nr, max(0, n - 1 - degree)) if n > 2 * degree else 0
+    local_cap = degree - nr
+    local_keep = _prune(cand, cd, x, local_cap)
+    ar = torch.arange(kc, device=dev)[None, :]
+    o = torch.argsort(torch.where(local_keep, ar, kc + ar), dim=1)
+    local = torch.where(torch.gather(local_keep, 1, o), torch.gather(cand, 1, o),
+                        torch.full_like(cand, -1))[:, :local_cap]
+    parts = [local]
+    if nr:
+        g = torch.Generator().manual_seed(seed)
+        # uniform targets != self: draw in [0, n-1) and skip over the owner
+        r = torch.randint(0, n - 1, (n, 2 * nr), generator=g).to(dev)
+        own = torch.arange(n, device=dev)[:, None]
+        r = r + (r >= own).to(r.dtype)
+        parts.append(_first_unique(r, nr))
+    parts.append(cand)
+    merged = _first_unique(torch.cat(parts, 1), degree)
+    # sort each list by (distance, id)
+    big = torch.iinfo(torch.int64).max
+    valid = merged >= 0
+    mv = x[merged.clamp(min=0)]
+    dist = _sqnorm(mv - x[:, None, :]).to(torch.float64)
+    dist = torch.where(valid, dist, torch.full_like(dist, float("inf")))
+    o = torch.argsort(torch.where(valid, merged, torch.full_like(merged, big)), dim=1)
+    merged = torch.gather(merged, 1, o)
+    dist = torch.gather(dist, 1, o)
+    o = torch.argsort(dist, dim=1, stable=True)
+    return torch.gather(merged, 1, o)
+
+
+def encode(x: torch.Tensor, nbrs: torch.Tensor, signs: np.ndarray, use_ip: bool = False,
+           chunk_edges: int = 1 << 20):
+    """Per-edge codes (n, deg, B/8) uint8 and factors (n, 3, deg) float32."""
+    n, dim = x.shape
+    deg = nbrs.shape[1]
+    b = signs.shape[0]
+    dev = x.device
+    p = hadamard_rotation(signs, dev)
+    pos = torch.as_tensor(code_bit_positions(b), device=dev)
+    weights = (2 ** torch.arange(8, device=dev, dtype=torch.int64))
+    codes = torch.zeros((n, deg, b // 8), dtype=torch.uint8, device=dev)
+    factors = torch.zeros((n, 3, deg), dtype=torch.float32, device=dev)
+    rows = max(1, chunk_edges // max(1, deg * b // 128))
+    for s in range(0, n, rows):
+        e = min(n, s + rows)
+        c = torch.zeros((e - s, b), dtype=torch.float64, device=dev)
+        c[:, :dim] = x[s:e].to(torch.float64)
+        nb = nbrs[s:e]
+        valid = nb >= 0
+        v = torch.zeros((e - s, deg, b), dtype=torch.float64, device=dev)
+        v[:, :, :dim] = x[nb.clamp(min=0)].to(torch.float64)
+        r = v - c[:, None, :]
+        y = r @ p.T
+        bits = (y > 0)
+        sgn = bits.to(torch.float64) * 2.0 - 1.0
+        nr = (r * r).sum(-1)
+        sabs = y.abs().sum(-1)
+        ssum = sgn.sum(-1)
+        zero = sabs <= 0
+        if use_ip:
+            f = torch.where(zero, torch.zeros_like(nr), -nr / torch.where(zero, torch.ones_like(sabs), sabs))
+            tx = torch.zeros_like(f)
+        else:
+            f = torch.where(zero, torch.zeros_like(nr), -2.0 * nr / torch.where(zero, torch.ones_like(sabs), sabs))
+            pc = c @ p.T
+            spc = (sgn * pc[:, None, :]).sum(-1)
+            tx = torch.where(zero, torch.zeros_like(nr), nr - f * spc)
+        fvq = f * ssum
+        tx = torch.where(valid, tx, torch.full_like(tx, FLT_MAX))
+        f = torch.where(valid, f, torch.zeros_like(f))
+        fvq = torch.where(valid, fvq, torch.zeros_like(fvq))
+        factors[s:e, 0] = tx.to(torch.float32)
+        factors[s:e, 1] = f.to(torch.float32)
+        factors[s:e, 2] = fvq.to(torch.float32)
+        ordered = torch.zeros((e - s, deg, b), dtype=torch.int64, device=dev)
+        ordered[:, :, pos] = (bits & valid[:, :, None]).to(torch.int64)
+        packed = (ordered.view(e - s, deg, b // 8, 8) * weights).sum(-1)
+        codes[s:e] = packed.to(torch.uint8)
+    return codes, factors
+
+
+def entry_point(x: torch.Tensor) -> int:
+    """The node nearest the mean vector (float64)."""
+    xd = x.to(torch.float64)
+    mu = xd.mean(0, keepdim=True)
+    return int(torch.argmin(_sqnorm(xd - mu)).item())
+
+
+def build_codebook(base: np.ndarray, degree: int, signs: np.ndarray, use_ip: bool = False,
+                   device: str | torch.device = "cpu", random_links: int | None = None,
+                   store_entry: bool = True, verbose: bool = False) -> Codebook:
+    """Builds a complete codebook in the reference layout."""
+    n, dim = base.shape
+    lay = Layout.make(dim, degree)
+    if signs.shape[0] != lay.padded_dim:
+        raise ValueError("signs must have padded_dim entries")
+    x = torch.as_tensor(np.ascontiguousarray(base, dtype=np.float32), device=device)
+    nbrs = build_graph(x, degree, random_links=random_links, verbose=verbose)
+    codes, factors = encode(x, nbrs, signs, use_ip=use_ip)
+    rows = np.zeros((n, lay.row_offset), dtype=np.float32)
+    rows[:, :dim] = base
+    code_bytes = rows[:, lay.code_offset : lay.factor_offset].view(np.uint8)
+    code_bytes[:] = codes.cpu().numpy().reshape(n, -1)
+    rows[:, lay.factor_offset : lay.neighbor_offset] = factors.cpu().numpy().reshape(n, -1)
+    ids = nbrs.cpu().numpy()
+    ids = np.where(ids < 0, MAX_INDEX, ids).astype(np.uint32)
+    rows[:, lay.neighbor_offset : lay.row_offset].view(np.uint32)[:] = ids
+    entry = entry_point(x) if store_entry else MAX_INDEX
+    return Codebook(rows, np.asarray(signs, dtype=np.float32), entry, lay)
+
+
+def ground_truth(base: np.ndarray, queries: np.ndarray, k: int,
+                 device: str | torch.device = "cpu", use_ip: bool = False) -> np.ndarray:
+    """Exact top-k ids (int32) by L2 (or by -<q,x> for IP), ties by id."""
+    b = torch.as_tensor(np.ascontiguousarray(base, dtype=np.float32), device=device)
+    q = torch.as_tensor(np.ascontiguousarray(queries, dtype=np.float32), device=device)
+    if not use_ip:
+        ids, _ = knn(b, k, queries=q, exclude_self=False)
+        return ids.cpu().numpy().astype(np.int32)
+    out = []
+    for s in range(0, q.shape[0], 1024):
+        d = -(q[s : s + 1024] @ b.T)
+        dv, di = torch.topk(d, min(b.shape[0], k + 16), dim=1, largest=False)
+        o = torch.argsort(di, 1)
+        di, dv = torch.gather(di, 1, o), torch.gather(dv, 1, o)
+        o = torch.argsort(dv, 1, stable=True)
+        out.append(torch.gather(di, 1, o)[:, :k].cpu().numpy())
+    return np.concatenate(out).astype(np.int32)
+
+
+def graph_stats(nbrs: np.ndarray) -> dict:
+    valid = nbrs != MAX_INDEX
+    return {"mean_degree": float(valid.sum(1).mean()), "min_degree": int(valid.sum(1).min())}
+
+
+__all__ = ["knn", "build_graph", "encode", "build_codebook", "ground_truth", "entry_point",
+           "hadamard_rotation", "graph_stats"]

@@ -1,0 +1,1421 @@
+// fg_search.hip -- adaptive graph beam search for MI355X (gfx950, wave64).
+//
+// The search path of the reference (src/adaptive_search.cuh:5-466 with the
+// primitives of include/utils.cuh and src/adaptive_search_utils.cuh) rebuilt
+// around one 64-lane wavefront per query:
+//   * one workgroup = one wave = one query; the reference's 256-thread block
+//     barriers become wave-ordered LDS traffic, so the beam, candidate buffer,
+//     visited table and controller state never leave the CU's LDS/registers;
+//   * the reference's 32-lane sorting networks are data-oblivious, so the
+//     same compare-exchange sequence is replayed on the wave (two 32-lane
+//     halves, or 1-2 positions per lane) and ties resolve identically;
+//   * RaBitQ scores come from 7 popcount bit-planes of the quantized query
+//     held in LDS (raw = sum_p 2^p popcount(code & plane_p)), corrected for the
+//     reference's uint8 LUT wrap, instead of per-nibble LUT gathers;
+//   * exact distances keep the reference's per-lane accumulation order and
+//     reduction tree, so results are bitwise equal to the 32-lane original.
+// Determinism: where the reference races (concurrent inserts of one child by
+// two warps in the speculative path), this kernel fixes "every task of a round
+// sees the visited set as of the round's start; the lowest (task, lane) wins".
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cfloat>
+#include <chrono>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/flashgann.h"
+
+namespace {
+
+constexpr uint32_t kMaxIndex = 0xFFFFFFFFu;
+constexpr uint32_t kMsb = 0x80000000u;
+constexpr int kSearchWidth = 8;       // THETA_MAX = WARPS_PER_BLOCK (adaptive_search_config.cuh:32)
+constexpr int kBufferBound = 32;      // BUFFER_BOUND (adaptive_search_config.cuh:54)
+constexpr int kMaxIterations = 1024;  // MAX_ITERATIONS (adaptive_search_config.cuh:12)
+constexpr int kHashReset = 16;        // SMALL_HASH_RESET_INTERVAL (utils.cuh:683)
+constexpr int kRefBlock = 256;        // reference block size: fixes merge-path segmentation
+constexpr int kMaxBeam = 1024;
+constexpr int kMaxDegree = 64;
+constexpr int kMaxPaddedDim = 2048;
+constexpr float kPhase1Rho = 0.25f;   // PHASE1_RHO
+constexpr float kRhoMax = 0.99f;      // RHO_MAX
+constexpr int kStallIters = 4;        // TOP1_WARMUP_STALL_ITERS
+constexpr int kPlanes = 7;            // q in [1, 64] needs 7 bit-planes
+
+// ------------------------------------------------------------ host+device
+
+__host__ __device__ inline uint32_t round_up_pow2(uint32_t x) {
+    if (x <= 1) return 1;
+    --x;
+    x |= x >> 1; x |= x >> 2; x |= x >> 4; x |= x >> 8; x |= x >> 16;
+    return x + 1;
+}
+
+// utils.cuh:119-127
+__host__ __device__ inline uint32_t effective_sort_beam(uint32_t beam) {
+    uint32_t r = round_up_pow2(beam);
+    if (r <= 128) return r < 32 ? 32 : r;
+    return beam;
+}
+
+__host__ __device__ inline int clamp_i(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+__host__ __device__ inline float clamp_f(float v, float lo, float hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+// utils.cuh:104-117
+__host__ __device__ inline int keep_count_per_parent(uint32_t max_degree, float rho) {
+    float kf = 1.0f - rho;
+    if (kf < 0.0f) kf = 0.0f;
+    if (kf > 1.0f) kf = 1.0f;
+    uint32_t k = static_cast<uint32_t>(ceilf(static_cast<float>(max_degree) * kf));
+    if (k < 1) k = 1;
+    if (k > max_degree) k = max_degree;
+    return static_cast<int>(k);
+}
+
+// adaptive_search_utils.cuh:121-135
+__host__ __device__ inline int keep_count_for_expander(uint32_t active, int theta, float rho,
+                                                       bool kth_valid, uint32_t near) {
+    const int active_count = static_cast<int>(active);
+    const int rho_keep = keep_count_per_parent(active, rho);
+    const int budget = clamp_i(static_cast<int>(static_cast<uint32_t>(kBufferBound) / static_cast<uint32_t>(theta)), 1,
+                               active_count);
+    int max_keep = rho_keep < budget ? rho_keep : budget;
+    if (kth_valid) max_keep = clamp_i(static_cast<int>(near), 1, max_keep);
+    return clamp_i(max_keep, 1, active_count);
+}
+
+// Visited-table size.  Between two resets the table receives at most
+// beam + 16 * 32 * tiles distinct keys (restore + one reset interval of
+// inserts, <= 32 per 8-task round), so any table that stays below 75% load
+// behaves as an exact set, as the reference's 2^11-entry table does
+// (utils.cuh:137-151).  Membership answers are therefore identical.
+__host__ __device__ inline uint32_t visited_bitlen(uint32_t beam, uint32_t degree) {
+    const uint32_t tiles = (degree + 31) / 32;
+    const uint32_t need = beam + 16u * 32u * tiles + 1u;
+    const uint32_t target = (need * 4u + 2u) / 3u;
+    uint32_t bitlen = 8;
+    while ((1u << bitlen) < target) ++bitlen;
+    return bitlen;
+}
+
+struct LdsLayout {
+    uint32_t hash_off, beam_off, cand_off, query_off, plane_off, scratch_off, total;
+};
+
+// Per-query LDS: visited table (aliased by the rotated query during
+// preparation), two beam buffers (ping-pong for the merge-path variant), the
+// 32-entry candidate buffer, the raw query, 8 x B/32 plane words and a small
+// scratch area (speculative round: 256 child ids + 32-entry accepted list +
+// parent lists).
+__host__ __device__ inline LdsLayout lds_layout(uint32_t dim, uint32_t padded_dim, uint32_t pbeam,
+                                                uint32_t bitlen) {
+    LdsLayout L;
+    uint32_t off = 0;
+    L.hash_off = off;
+    uint32_t hash_bytes = (1u << bitlen) * 4u;
+    if (hash_bytes < padded_dim * 4u) hash_bytes = padded_dim * 4u;
+    off += hash_bytes;
+    L.beam_off = off;
+    off += (pbeam > 128 ? 2u : 1u) * pbeam * 8u;
+    L.cand_off = off;
+    off += 32u * 8u;
+    L.query_off = off;
+    off += ((dim + 3u) & ~3u) * 4u;
+    L.plane_off = off;
+    off += 8u * (padded_dim / 32u) * 4u;
+    L.scratch_off = off;
+    off += (256u + 32u + 3u * 8u) * 4u;
+    L.total = (off + 15u) & ~15u;
+    return L;
+}
+
+struct SearchParams {
+    const float *data;
+    const float *signs;
+    const float *queries;
+    uint32_t *results;
+    uint32_t *counters;
+    uint64_t npoints;
+    uint64_t row_offset, code_offset, factor_offset, neighbor_offset;
+    int dim, padded_dim, degree;
+    int K, beam, pbeam, cbs, collect_cap;
+    int bitlen, max_iter;
+    float phase2_rho;
+    int use_ip;
+    int dup_free;
+    uint32_t entry;
+    int nq;
+    LdsLayout lds;
+};
+
+// ------------------------------------------------------------ device helpers
+
+__device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & 63; }
+
+__device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
+
+__device__ __forceinline__ uint32_t half_bits(uint64_t m, int h) {
+    return static_cast<uint32_t>(m >> (32 * h));
+}
+
+__device__ __forceinline__ float wave_min(float v) {
+    for (int m = 32; m >= 1; m >>= 1) v = fminf(v, __shfl_xor(v, m));
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
+    return v;
+}
+__device__ __forceinline__ int wave_sum(int v) {
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    return v;
+}
+
+// uniform value -> scalar register
+__device__ __forceinline__ uint32_t uni(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ float uni(float v) {
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+
+__device__ __forceinline__ bool finite_below_max(float x) { return isfinite(x) && x < FLT_MAX; }
+
+// ------------------------------------------------------------ query preparation
+
+// utils.cuh:790-939 for one wave: rotate (x*signs, pad, FWHT len = 1..B/2 with
+// butterflies (u+v, u-v)), min/max, width = (hi-lo)*fl(1/63), q = round(fma(
+// y-lo, 1/width, 0.5)) (NaN -> 0), then the 7 popcount planes and the chunks
+// whose uint8 LUT entry would wrap.  Writes planes (8 x W words) and returns
+// low, width, sum_q.  `rot` is LDS scratch of B floats.
+__device__ void prepare_query(const float *__restrict__ query, const float *__restrict__ signs, int dim,
+                              int B, float *rot, float *qv, uint32_t *planes, float &low_out,
+                              float &high_out, float &width_out, int &sumq_out, uint8_t *qdump) {
+    const int lane = lane_id();
+    for (int i = lane; i < B; i += 64) {
+        float x = 0.0f;
+        if (i < dim) {
+            const float v = query[i];
+            if (qv) qv[i] = v;
+            x = v * signs[i];
+        }
+        rot[i] = x;
+    }
+    __syncthreads();
+    for (int len = 1; len < B; len <<= 1) {
+        for (int p = lane; p < (B >> 1); p += 64) {
+            const int blk = p / len, j = p - blk * len;
+            const int i1 = blk * (len << 1) + j, i2 = i1 + len;
+            const float u = rot[i1], v = rot[i2];
+            rot[i1] = u + v;
+            rot[i2] = u - v;
+        }
+        __syncthreads();
+    }
+    float lo = FLT_MAX, hi = -FLT_MAX;
+    for (int i = lane; i < B; i += 64) {
+        lo = fminf(lo, rot[i]);
+        hi = fmaxf(hi, rot[i]);
+    }
+    lo = uni(wave_min(lo));
+    hi = uni(wave_max(hi));
+    const float levels_inv = 1.0f / 63.0f;
+    const float width = (hi - lo) * levels_inv;
+    const float inv_width = 1.0f / width;
+    const int W = B >> 5;
+    const int h = lane >> 5, nl = lane & 31;
+    int sum = 0;
+    for (int w0 = 0; w0 < W; w0 += 2) {
+        const int w = w0 + h;  // W is even (B >= 64)
+        const int g = 32 * w + nl;
+        const int i = 4 * (g >> 2) + 3 - (g & 3);
+        const float scaled = fmaf(rot[i] - lo, inv_width, 0.5f);
+        const uint32_t q = isnan(scaled) ? 0u : static_cast<uint32_t>(roundf(scaled));
+        if (qdump) qdump[i] = static_cast<uint8_t>(q);
+        sum += static_cast<int>(q);
+        for (int p = 0; p < kPlanes; ++p) {
+            const uint64_t m = ballot(((q >> p) & 1u) != 0u);
+            if (nl == 0) planes[p * W + w] = half_bits(m, h);
+        }
+        // a chunk's full-nibble LUT entry is (q0+q1+q2+q3) mod 256 (utils.cuh:913-917)
+        uint32_t s = q + static_cast<uint32_t>(__shfl_xor(static_cast<int>(q), 1));
+        s += static_cast<uint32_t>(__shfl_xor(static_cast<int>(s), 2));
+        const uint64_t wm = ballot(s >= 256u);
+        if (nl == 0) planes[kPlanes * W + w] = half_bits(wm, h);
+    }
+    sumq_out = uni(wave_sum(sum));
+    low_out = lo;
+    high_out = hi;
+    width_out = width;
+    __syncthreads();
+}
+
+// raw = sum_cb LUT[cb][nibble] (utils.cuh:976-980) over code words [w0, w1).
+__device__ __forceinline__ int32_t raw_partial(const uint32_t *__restrict__ code, int w0, int w1,
+                                               const uint32_t *planes, int W) {
+    uint32_t acc[kPlanes];
+#pragma unroll
+    for (int p = 0; p < kPlanes; ++p) acc[p] = 0;
+    uint32_t wraps = 0;
+    for (int w = w0; w < w1; ++w) {
+        const uint32_t c = code[w];
+#pragma unroll
+        for (int p = 0; p < kPlanes; ++p) acc[p] += __popc(c & planes[p * W + w]);
+        const uint32_t x = c & planes[kPlanes * W + w];
+        wraps += __popc(x & (x >> 1) & (x >> 2) & (x >> 3) & 0x11111111u);
+    }
+    uint32_t raw = 0;
+#pragma unroll
+    for (int p = 0; p < kPlanes; ++p) raw += acc[p] << p;
+    return static_cast<int32_t>(raw - 256u * wraps);
+}
+
+// utils.cuh:989-993 with nvcc's contraction of the two multiply-adds.
+__device__ __forceinline__ float estimate_formula(int32_t raw, int32_t sum_q, float width, float low,
+                                                  float tx, float fdq, float fvq, float pdist) {
+    const float rf = static_cast<float>((raw << 1) - sum_q);
+    float est = tx + pdist;
+    est = fmaf(fdq * width, rf, est);
+    est = fmaf(fvq, low, est);
+    return est;
+}
+
+// utils.cuh:269-305 for one 32-lane half: lane nl accumulates dims nl, nl+32,
+// ... with a contracted multiply-add, then the xor butterfly 16..1 (lane 0 of
+// the half holds exactly the shfl_down tree's sum; every lane gets the same).
+__device__ __forceinline__ float half_distance(const float *__restrict__ row, const float *qv, int dim,
+                                               int nl, bool use_ip, bool active) {
+    float val = 0.0f;
+    if (active) {
+        if (use_ip) {
+            for (int i = nl; i < dim; i += 32) val = fmaf(qv[i], row[i], val);
+        } else {
+            for (int i = nl; i < dim; i += 32) {
+                const float d = qv[i] - row[i];
+                val = fmaf(d, d, val);
+            }
+        }
+    }
+    val += __shfl_xor(val, 16);
+    val += __shfl_xor(val, 8);
+    val += __shfl_xor(val, 4);
+    val += __shfl_xor(val, 2);
+    val += __shfl_xor(val, 1);
+    return use_ip ? -val : val;
+}
+
+// Exact distances for the children in cd/ci slots listed by `mask` (bit i =
+// slot i), two children per pass (one per half-wave).  Writes cd[slot].
+__device__ void exact_for_slots(const SearchParams &P, uint32_t mask, float *cd, const uint32_t *ci,
+                                const float *qv) {
+    const int lane = lane_id();
+    const int h = lane >> 5, nl = lane & 31;
+    while (mask) {
+        const int s0 = __builtin_ctz(mask);
+        mask &= mask - 1;
+        int s1 = -1;
+        if (mask) {
+            s1 = __builtin_ctz(mask);
+            mask &= mask - 1;
+        }
+        const int slot = h == 0 ? s0 : s1;
+        const bool active = slot >= 0;
+        const uint32_t child = active ? ci[slot] : 0u;
+        const float *row = P.data + static_cast<uint64_t>(child) * P.row_offset;
+        const float d = half_distance(row, qv, P.dim, nl, P.use_ip != 0, active);
+        if (active && nl == 0) cd[slot] = d;
+    }
+}
+
+// ------------------------------------------------------------ sorting networks
+
+// One bitonic stage of block size kk over E positions per lane (position of
+// item e is base + e), compare distance j = jstart .. 1.  Cross-lane steps use
+// the reference's per-lane rule (utils.cuh:309-316, 340-341): lane takes its
+// partner's pair iff the keys differ and (k < pk) != p with
+// p = (pos & kk != 0) == (pos & j != 0).  In-lane steps are utils.cuh:319-328
+// with ascending = (pos_lo & kk) == 0.
+template <int E>
+__device__ __forceinline__ void bitonic_stage(float (&k)[E], uint32_t (&v)[E], int base, int kk, int jstart) {
+    for (int j = jstart; j >= 1; j >>= 1) {
+        if (j >= E) {
+            const int m = j / E;
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                const float pk = __shfl_xor(k[e], m);
+                const uint32_t pv = static_cast<uint32_t>(__shfl_xor(static_cast<int>(v[e]), m));
+                const int pos = base + e;
+                const bool p = ((pos & kk) != 0) == ((pos & j) != 0);
+                if (k[e] != pk && ((k[e] < pk) != p)) {
+                    k[e] = pk;
+                    v[e] = pv;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                if (e & j) continue;
+                const int hi = e | j;
+                const bool asc = ((base + e) & kk) == 0;
+                if (k[e] != k[hi] && ((k[e] < k[hi]) != asc)) {
+                    const float tk = k[e]; k[e] = k[hi]; k[hi] = tk;
+                    const uint32_t tv = v[e]; v[e] = v[hi]; v[hi] = tv;
+                }
+            }
+        }
+    }
+}
+
+// warp_sort<1> on 32 positions (utils.cuh:409-414): position = lane & 31, both
+// halves sort the same data.
+__device__ __forceinline__ void sort32(float &key, uint32_t &val, int nl) {
+    float k[1] = {key};
+    uint32_t v[1] = {val};
+    for (int kk = 2; kk <= 32; kk <<= 1) bitonic_stage<1>(k, v, nl, kk, kk >> 1);
+    key = k[0];
+    val = v[0];
+}
+
+// utils.cuh:588-616
+__device__ __forceinline__ int merge_path_partition(const float *a, int na, const float *b, int nb, int diag) {
+    int low = diag - nb > 0 ? diag - nb : 0;
+    int high = diag < na ? diag : na;
+    while (low <= high) {
+        const int ai = (low + high) >> 1;
+        const int bi = diag - ai;
+        const float al = ai > 0 ? a[ai - 1] : -FLT_MAX;
+        const float ar = ai < na ? a[ai] : FLT_MAX;
+        const float bl = bi > 0 ? b[bi - 1] : -FLT_MAX;
+        const float br = bi < nb ? b[bi] : FLT_MAX;
+        if (al > br) high = ai - 1;
+        else if (bl > ar) low = ai + 1;
+        else return ai;
+    }
+    return low;
+}
+
+// Beam merge (utils.cuh:1369-1399 dispatch for a <= 32-entry buffer).
+// pbeam <= 128: topk_small_by_bitonic_sort<1, pbeam/32> (utils.cuh:490-586).
+// The `first` strided load + sort is skipped: it runs only at iteration 0,
+// when every beam entry is the identical (FLT_MAX, MAX_INDEX) pair, where it
+// is the identity.  pbeam > 128: topk_candidate_sort_and_merge
+// (utils.cuh:618-680) with the reference block's segmentation, writing into
+// the other beam buffer; returns the index of the buffer holding the beam.
+__device__ int merge_beam(const SearchParams &P, float *bd0, uint32_t *bi0, float *bd1, uint32_t *bi1, int cur,
+                          float *cd, uint32_t *ci) {
+    const int lane = lane_id();
+    const int nl = lane & 31, h = lane >> 5;
+    const int cbs = P.cbs, pbeam = P.pbeam;
+    float ck = nl < cbs ? cd[nl] : FLT_MAX;
+    uint32_t cv = nl < cbs ? ci[nl] : kMaxIndex;
+    sort32(ck, cv, nl);
+    float *bd = cur ? bd1 : bd0;
+    uint32_t *bi = cur ? bi1 : bi0;
+    if (pbeam <= 128) {
+        if (pbeam == 128) {
+            float k[2];
+            uint32_t v[2];
+            const int base = 2 * lane;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                k[e] = bd[base + e];
+                v[e] = bi[base + e];
+                const int kc = pbeam - 1 - (base + e);
+                const float kk2 = __shfl(ck, kc & 31);
+                const uint32_t vv2 = static_cast<uint32_t>(__shfl(static_cast<int>(cv), kc & 31));
+                if (kc < cbs && k[e] > kk2) {
+                    k[e] = kk2;
+                    v[e] = vv2;
+                }
+            }
+            bitonic_stage<2>(k, v, base, 128, 64);
+            __syncthreads();
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                bd[base + e] = k[e];
+                bi[base + e] = v[e];
+            }
+        } else {
+            const int pos = pbeam == 64 ? lane : nl;
+            float k[1] = {bd[pos]};
+            uint32_t v[1] = {bi[pos]};
+            const int kc = pbeam - 1 - pos;
+            const float kk2 = __shfl(ck, kc & 31);
+            const uint32_t vv2 = static_cast<uint32_t>(__shfl(static_cast<int>(cv), kc & 31));
+            if (kc < cbs && k[0] > kk2) {
+                k[0] = kk2;
+                v[0] = vv2;
+            }
+            bitonic_stage<1>(k, v, pos, pbeam, pbeam >> 1);
+            __syncthreads();
+            if (pbeam == 64 || h == 0) {
+                bd[pos] = k[0];
+                bi[pos] = v[0];
+            }
+        }
+        __syncthreads();
+        return cur;
+    }
+    // merge-path variant: sorted candidates to LDS, then segments
+    if (h == 0 && nl < cbs) {
+        cd[nl] = ck;
+        ci[nl] = cv;
+    }
+    __syncthreads();
+    float *od = cur ? bd0 : bd1;
+    uint32_t *oi = cur ? bi0 : bi1;
+    int active = (pbeam + 3) / 4;
+    active = ((active + 31) / 32) * 32;
+    if (active > kRefBlock) active = kRefBlock;
+    for (int t = lane; t < active; t += 64) {
+        const uint32_t ub = static_cast<uint32_t>(pbeam);
+        const int ob = static_cast<int>(min(ub, (static_cast<uint32_t>(t) * ub) / static_cast<uint32_t>(active)));
+        const int oe = static_cast<int>(min(ub, (static_cast<uint32_t>(t + 1) * ub) / static_cast<uint32_t>(active)));
+        const int tb = merge_path_partition(bd, pbeam, cd, cbs, ob);
+        const int te = merge_path_partition(bd, pbeam, cd, cbs, oe);
+        int ti = tb, cix = ob - tb;
+        const int cend = oe - te;
+        for (int o = ob; o < oe; ++o) {
+            const bool take_top = (cix >= cend) || (ti < te && bd[ti] <= cd[cix]);
+            if (take_top) {
+                od[o] = bd[ti];
+                oi[o] = bi[ti];
+                ++ti;
+            } else {
+                od[o] = cd[cix];
+                oi[o] = ci[cix];
+                ++cix;
+            }
+        }
+    }
+    __syncthreads();
+    return cur ^ 1;
+}
+
+// ------------------------------------------------------------ visited table
+
+// utils.cuh:697-735 hashing (slot = (k ^ (k >> bitlen)) & mask, linear probe,
+// empty = 0xFFFFFFFF) on an LDS table.
+__device__ __forceinline__ uint32_t hash_insert(uint32_t *t, int bitlen, uint32_t key) {
+    const uint32_t size = 1u << bitlen, mask = size - 1;
+    uint32_t idx = (key ^ (key >> bitlen)) & mask;
+    for (uint32_t i = 0; i < size; ++i) {
+        const uint32_t old = atomicCAS(&t[idx], kMaxIndex, key);
+        if (old == kMaxIndex) return 1;
+        if (old == key) return 0;
+        idx = (idx + 1) & mask;
+    }
+    return 0;
+}
+
+__device__ __forceinline__ bool hash_contains(const uint32_t *t, int bitlen, uint32_t key) {
+    const uint32_t size = 1u << bitlen, mask = size - 1;
+    uint32_t idx = (key ^ (key >> bitlen)) & mask;
+    for (uint32_t i = 0; i < size; ++i) {
+        const uint32_t old = t[idx];
+        if (old == key) return true;
+        if (old == kMaxIndex) return false;
+        idx = (idx + 1) & mask;
+    }
+    return false;
+}
+
+__device__ __forceinline__ void hash_reset(uint32_t *t, int bitlen) {
+    const int n = 1 << bitlen;
+    uint4 *t4 = reinterpret_cast<uint4 *>(t);
+    const uint4 e = make_uint4(kMaxIndex, kMaxIndex, kMaxIndex, kMaxIndex);
+    for (int i = lane_id(); i < (n >> 2); i += 64) t4[i] = e;
+}
+
+// true iff an earlier (lower-lane) member of `members` in this half carries
+// the same key.  Scans lanes of half h in order via readlane.
+__device__ __forceinline__ bool dup_of_earlier(uint32_t key, uint32_t members, int nl, int h) {
+    bool dup = false;
+    uint32_t m = members;
+    while (m) {
+        const int s = __builtin_ctz(m);
+        m &= m - 1;
+        if (s >= 31) break;
+        const uint32_t k0 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(key), s));
+        const uint32_t k1 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(key), s + 32));
+        const uint32_t other = h ? k1 : k0;
+        dup |= (s < nl) && (other == key);
+    }
+    return dup;
+}
+
+// ------------------------------------------------------------ the search kernel
+
+struct Controller {
+    int spec;
+    float rho;
+    int policy_iters;
+    uint32_t top1;
+    int stall;
+    bool warm;
+    float entry_d, last_e, cur_e;
+};
+
+// src/adaptive_search.cuh:166-190 + adaptive_search_utils.cuh:32-39, 51-119
+// (CHECK_INTERVAL = 1): every lane computes the same values.
+__device__ __forceinline__ void controller_step(Controller &c, uint32_t beam0, float phase2_rho) {
+    const uint32_t top = beam0 & 0x7fffffffu;
+    const int stall = (c.policy_iters > 0 && top == c.top1) ? c.stall + 1 : 0;
+    const bool phase_changed = c.warm || stall >= kStallIters;
+    const float entry = c.entry_d;
+    const float last = finite_below_max(c.last_e) ? c.last_e : entry;
+    const float cur = finite_below_max(c.cur_e) ? c.cur_e : last;
+    float rate = 0.0f;
+    const float denom = fabsf(entry);
+    if (isfinite(last) && isfinite(cur) && isfinite(entry) && denom > 1.0e-20f) {
+        const float pr = (last - cur) / denom;
+        if (isfinite(pr) && pr > 0.0f) rate = pr < 1.0f ? pr : 1.0f;
+    }
+    c.top1 = top;
+    c.stall = stall;
+    c.last_e = last;
+    c.cur_e = cur;
+    if (phase_changed) {
+        c.warm = true;
+        c.spec = kSearchWidth;
+        c.rho = phase2_rho;
+    } else {
+        const float span = phase2_rho > kPhase1Rho ? phase2_rho - kPhase1Rho : kRhoMax - 0.0f;
+        const float base = c.policy_iters == 0 ? kPhase1Rho : c.rho;
+        const float cap = phase2_rho > kPhase1Rho ? phase2_rho : kRhoMax;
+        c.warm = false;
+        c.spec = 1;
+        c.rho = clamp_f(fmaf(span, rate, base), 0.0f, cap);
+    }
+    c.policy_iters += 1;
+}
+
+__global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int qid = blockIdx.x;
+    if (qid >= P.nq) return;
+    const int lane = lane_id();
+    const int h = lane >> 5, nl = lane & 31;
+    const int B = P.padded_dim, W = B >> 5;
+    const int deg = P.degree;
+    const int bitlen = P.bitlen;
+
+    uint32_t *H = reinterpret_cast<uint32_t *>(smem + P.lds.hash_off);
+    float *bd0 = reinterpret_cast<float *>(smem + P.lds.beam_off);
+    uint32_t *bi0 = reinterpret_cast<uint32_t *>(bd0 + P.pbeam);
+    float *bd1 = reinterpret_cast<float *>(bi0 + P.pbeam);
+    uint32_t *bi1 = reinterpret_cast<uint32_t *>(bd1 + P.pbeam);
+    float *cd = reinterpret_cast<float *>(smem + P.lds.cand_off);
+    uint32_t *ci = reinterpret_cast<uint32_t *>(cd + 32);
+    float *qv = reinterpret_cast<float *>(smem + P.lds.query_off);
+    uint32_t *planes = reinterpret_cast<uint32_t *>(smem + P.lds.plane_off);
+    uint32_t *rchild = reinterpret_cast<uint32_t *>(smem + P.lds.scratch_off);
+    uint32_t *alist = rchild + 256;
+    uint32_t *plist = alist + 32;
+    uint32_t *pnode = plist + 8;
+    float *pdist = reinterpret_cast<float *>(pnode + 8);
+
+    // ---- query preparation (the visited table's LDS holds the rotation)
+    float qlow, qhigh, qwidth;
+    int sum_q;
+    prepare_query(P.queries + static_cast<uint64_t>(qid) * P.dim, P.signs, P.dim, B, reinterpret_cast<float *>(H),
+                  qv, planes, qlow, qhigh, qwidth, sum_q, nullptr);
+
+    // ---- state (adaptive_search.cuh:67-107)
+    hash_reset(H, bitlen);
+    for (int i = lane; i < P.pbeam; i += 64) {
+        bd0[i] = FLT_MAX;
+        bi0[i] = kMaxIndex;
+    }
+    if (lane < 32) {
+        cd[lane] = FLT_MAX;
+        ci[lane] = kMaxIndex;
+    }
+    __syncthreads();
+    // entry point (adaptive_search.cuh:109-119)
+    const float entry_d = uni(half_distance(P.data + static_cast<uint64_t>(P.entry) * P.row_offset, qv, P.dim, nl,
+                                            P.use_ip != 0, true));
+    if (lane == 0) {
+        cd[0] = entry_d;
+        ci[0] = P.entry;
+        hash_insert(H, bitlen, P.entry);
+    }
+    __syncthreads();
+
+    Controller ctl{1, kPhase1Rho, 0, kMaxIndex, 0, false, entry_d, FLT_MAX, FLT_MAX};
+    uint32_t c_iters = 0, c_exp = 0, c_ids = 0, c_est = 0, c_exact = 1, c_st2 = kMaxIndex;
+    int cur = 0;
+    const int beam_sz = P.beam, pbeam = P.pbeam;
+    const int cbs = P.cbs;
+    const float *data = P.data;
+
+    for (int iter = 0; iter < kMaxIterations; ++iter) {
+        float *bd = cur ? bd1 : bd0;
+        uint32_t *bi = cur ? bi1 : bi0;
+        if (((iter + 1) % kHashReset) == 0) {  // adaptive_search.cuh:128-134
+            hash_reset(H, bitlen);
+            __syncthreads();
+            for (int i = lane; i < beam_sz; i += 64) hash_insert(H, bitlen, bi[i] & ~kMsb);
+            __syncthreads();
+        }
+        if (iter >= P.max_iter) break;
+
+        cur = merge_beam(P, bd0, bi0, bd1, bi1, cur, cd, ci);
+        bd = cur ? bd1 : bd0;
+        bi = cur ? bi1 : bi0;
+        for (int i = beam_sz + lane; i < pbeam; i += 64) {
+            bd[i] = FLT_MAX;
+            bi[i] = kMaxIndex;
+        }
+        if (lane < 32) {
+            cd[lane] = FLT_MAX;
+            ci[lane] = kMaxIndex;
+        }
+        __syncthreads();
+        float kth = FLT_MAX;  // adaptive_search_utils.cuh:25-30
+        if (bi[beam_sz - 1] != kMaxIndex) kth = bd[(P.K < beam_sz ? P.K : beam_sz) - 1];
+        kth = uni(kth);
+        controller_step(ctl, uni(bi[0]), P.phase2_rho);
+        const int theta = ctl.spec;
+
+        // pick_expanders (utils.cuh:752-787): first theta unexpanded entries
+        uint32_t nexp = 0;
+        for (int base = 0; base < beam_sz; base += 64) {
+            const int j = base + lane;
+            bool fresh = false;
+            if (j < beam_sz) fresh = (bi[j] & kMsb) == 0;
+            const uint64_t m = ballot(fresh);
+            if (fresh) {
+                const uint32_t r = static_cast<uint32_t>(__popcll(m & ((1ull << lane) - 1ull))) + nexp;
+                if (r < static_cast<uint32_t>(theta)) {
+                    plist[r] = static_cast<uint32_t>(j);
+                    bi[j] |= kMsb;
+                }
+            }
+            nexp += static_cast<uint32_t>(__popcll(m));
+            if (nexp >= static_cast<uint32_t>(theta)) {
+                nexp = static_cast<uint32_t>(theta);
+                break;
+            }
+        }
+        __syncthreads();
+        if (nexp == 0) break;
+        c_iters++;
+        c_exp += nexp;
+        if (lane < static_cast<int>(nexp)) {
+            const uint32_t pos = plist[lane];
+            pnode[lane] = bi[pos] & 0x7fffffffu;
+            pdist[lane] = bd[pos];
+        }
+        __syncthreads();
+        // adaptive_search_utils.cuh:41-49
+        ctl.last_e = finite_below_max(ctl.cur_e) ? ctl.cur_e : ctl.entry_d;
+        ctl.cur_e = uni(pdist[nexp - 1]);
+        const bool kth_valid = finite_below_max(kth);
+
+        if (theta <= 1) {
+            // ---------------- single expander (adaptive_search.cuh:221-343)
+            const int cwc = deg < cbs ? deg : cbs;
+            const uint32_t parent = uni(pnode[0]);
+            const float pd0 = uni(pdist[0]);
+            const float *prow = data + static_cast<uint64_t>(parent) * P.row_offset;
+            const uint32_t *nbrs = reinterpret_cast<const uint32_t *>(prow + P.neighbor_offset);
+            c_ids += static_cast<uint32_t>(cwc);
+            uint32_t child = kMaxIndex;
+            if (nl < cwc) {
+                child = nbrs[nl];
+                if (child >= P.npoints || hash_contains(H, bitlen, child)) child = kMaxIndex;
+            }
+            const uint32_t vmask = half_bits(ballot(child != kMaxIndex), 0);
+            const int valid_count = __popc(vmask);
+            const int keep = keep_count_for_expander(static_cast<uint32_t>(cwc), 1, ctl.rho, false, 0);
+            const bool keep_all = keep >= valid_count;
+            float dist = child == kMaxIndex ? FLT_MAX : 0.0f;
+            uint32_t admit_mask;
+            if (!keep_all) {
+                c_est += static_cast<uint32_t>(valid_count);
+                const float *factors = prow + P.factor_offset;
+                const uint32_t *codes = reinterpret_cast<const uint32_t *>(prow + P.code_offset);
+                const bool valid = child != kMaxIndex;
+                float tx = 0.0f, fdq = 0.0f, fvq = 0.0f;
+                int32_t part = 0;
+                if (valid) {
+                    tx = factors[nl];
+                    fdq = factors[deg + nl];
+                    fvq = factors[2 * deg + nl];
+                    const int hw = W >> 1;
+                    part = raw_partial(codes + static_cast<uint64_t>(nl) * W, h * hw, (h + 1) * hw, planes, W);
+                }
+                const int32_t raw = part + __shfl_xor(part, 32);
+                float est = FLT_MAX;
+                if (valid) {
+                    est = tx == FLT_MAX ? 0.0f : estimate_formula(raw, sum_q, qwidth, qlow, tx, fdq, fvq, pd0);
+                    if (!isfinite(est)) {
+                        child = kMaxIndex;
+                        est = FLT_MAX;
+                    }
+                    dist = est;
+                }
+                uint32_t near = 0;
+                if (kth_valid)
+                    near = __popc(half_bits(ballot(child != kMaxIndex && isfinite(dist) && dist <= kth), 0));
+                const int eff = keep_count_for_expander(static_cast<uint32_t>(cwc), 1, ctl.rho, kth_valid, near);
+                // dispatch_candidate_bitonic_sort over the cbs-entry buffer (padding beyond it)
+                float sk = nl < cbs ? dist : FLT_MAX;
+                uint32_t sv = nl < cbs ? child : kMaxIndex;
+                sort32(sk, sv, nl);
+                dist = sk;
+                child = sv;
+                if (nl >= eff) {
+                    child = kMaxIndex;
+                    dist = FLT_MAX;
+                }
+                admit_mask = eff >= 32 ? 0xFFFFFFFFu : ((1u << eff) - 1u);
+            } else {
+                admit_mask = cwc >= 32 ? 0xFFFFFFFFu : ((1u << cwc) - 1u);
+            }
+            // admit in slot order: insert, drop repeats (lowest slot wins)
+            const bool want = ((admit_mask >> nl) & 1u) && child != kMaxIndex && dist < FLT_MAX;
+            const uint32_t want_mask = half_bits(ballot(want), 0);
+            bool ins = want;
+            if (!P.dup_free) ins = want && !dup_of_earlier(child, want_mask, nl, 0);
+            if (h == 0 && ins) hash_insert(H, bitlen, child);
+            if (!ins) {
+                if ((admit_mask >> nl) & 1u) {
+                    child = kMaxIndex;
+                    dist = FLT_MAX;
+                }
+            }
+            if (h == 0) {
+                cd[nl] = dist;
+                ci[nl] = child;
+            }
+            __syncthreads();
+            const uint32_t ins_mask = half_bits(ballot(ins), 0);
+            c_exact += static_cast<uint32_t>(__popc(ins_mask));
+            exact_for_slots(P, ins_mask, cd, ci, qv);
+        } else {
+            // ---------------- speculative expansion (adaptive_search.cuh:344-444)
+            if (c_st2 == kMaxIndex) c_st2 = static_cast<uint32_t>(iter);
+            const int tiles = (deg + 31) / 32;
+            const int tasks = static_cast<int>(nexp) * tiles;
+            uint32_t compact = 0;
+            for (int rbase = 0; rbase < tasks; rbase += kSearchWidth) {
+                uint32_t kept_masks[kSearchWidth];
+                for (int sr = 0; sr < kSearchWidth / 2; ++sr) {
+                    const int wslot = 2 * sr + h;
+                    const int task = rbase + wslot;
+                    const bool tact = task < tasks;
+                    const int pidx = tact ? task / tiles : 0;
+                    const int tile = tact ? task - pidx * tiles : 0;
+                    const int nidx = tile * 32 + nl;
+                    const uint32_t parent = pnode[pidx];
+                    const float *prow = data + static_cast<uint64_t>(parent) * P.row_offset;
+                    uint32_t child = kMaxIndex;
+                    bool valid = false;
+                    if (tact && nidx < deg) {
+                        child = reinterpret_cast<const uint32_t *>(prow + P.neighbor_offset)[nidx];
+                        valid = child != kMaxIndex && child < P.npoints && !hash_contains(H, bitlen, child);
+                    }
+                    const uint64_t idsm = ballot(tact && nidx < deg);
+                    c_ids += static_cast<uint32_t>(__popcll(idsm));
+                    int an = tact ? deg - tile * 32 : 0;
+                    if (an > 32) an = 32;
+                    const int keep = tact ? keep_count_for_expander(static_cast<uint32_t>(an), theta, ctl.rho, false, 0) : 0;
+                    const uint64_t vm = ballot(valid);
+                    const int rvc = __popc(half_bits(vm, h));
+                    const bool keep_all = keep >= rvc;
+                    float est = FLT_MAX;
+                    const uint64_t estm = ballot(!keep_all && valid);
+                    c_est += static_cast<uint32_t>(__popcll(estm));
+                    if (!keep_all && valid) {
+                        const float *factors = prow + P.factor_offset;
+                        const float tx = factors[nidx];
+                        if (tx != FLT_MAX) {
+                            const float fdq = factors[deg + nidx];
+                            const float fvq = factors[2 * deg + nidx];
+                            const uint32_t *code =
+                                reinterpret_cast<const uint32_t *>(prow + P.code_offset) + static_cast<uint64_t>(nidx) * W;
+                            const int32_t raw = raw_partial(code, 0, W, planes, W);
+                            est = estimate_formula(raw, sum_q, qwidth, qlow, tx, fdq, fvq, pdist[pidx]);
+                        }
+                        valid = isfinite(est);
+                    }
+                    bool keep_lane = valid;
+                    if (!keep_all) {
+                        const uint32_t near =
+                            __popc(half_bits(ballot(valid && kth_valid && est <= kth), h));
+                        const int eff = keep_count_for_expander(static_cast<uint32_t>(an), theta, ctl.rho, kth_valid, near);
+                        // warp_keep_topk_smallest_f32 (utils.cuh:251-267) within the half
+                        const float mine = valid ? est : FLT_MAX;
+                        const uint32_t vmh = half_bits(ballot(valid), h);
+                        int rank = 0;
+                        for (int s = 0; s < 32; ++s) {
+                            const float o0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), s));
+                            const float o1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), s + 32));
+                            const float other = h ? o1 : o0;
+                            const bool ov = (vmh >> s) & 1u;
+                            rank += (ov && (other < mine || (other == mine && s < nl))) ? 1 : 0;
+                        }
+                        keep_lane = valid && eff > 0 && rank < eff;
+                    }
+                    const uint64_t km = ballot(keep_lane);
+                    kept_masks[2 * sr] = uni(half_bits(km, 0));
+                    kept_masks[2 * sr + 1] = uni(half_bits(km, 1));
+                    rchild[wslot * 32 + nl] = child;
+                }
+                __syncthreads();
+                // list kept children in (task, lane) order
+                uint32_t total = 0;
+                for (int t = 0; t < kSearchWidth; ++t) {
+                    const uint32_t m = kept_masks[t];
+                    if (lane < 32 && ((m >> lane) & 1u)) {
+                        const uint32_t e = total + static_cast<uint32_t>(__popc(m & ((1u << lane) - 1u)));
+                        if (e < 32) alist[e] = rchild[t * 32 + lane];
+                    }
+                    total += static_cast<uint32_t>(__popc(m));
+                }
+                __syncthreads();
+                if (total > 32) total = 32;  // <= 4 kept per task at theta = 8
+                const bool mine = lane < static_cast<int>(total);
+                const uint32_t key = mine ? alist[lane] : kMaxIndex;
+                const uint32_t members = half_bits(ballot(mine), 0);
+                const bool acc = mine && !dup_of_earlier(key, members, nl, 0);
+                if (acc) hash_insert(H, bitlen, key);
+                const uint32_t accm = half_bits(ballot(acc), 0);
+                if (acc) {
+                    const uint32_t slot = compact + static_cast<uint32_t>(__popc(accm & ((1u << lane) - 1u)));
+                    if (slot < static_cast<uint32_t>(P.collect_cap)) {
+                        ci[slot] = key;
+                        cd[slot] = FLT_MAX;
+                    }
+                }
+                compact += static_cast<uint32_t>(__popc(accm));
+                __syncthreads();
+            }
+            if (compact > static_cast<uint32_t>(P.collect_cap)) compact = static_cast<uint32_t>(P.collect_cap);
+            const uint32_t emask = compact >= 32 ? 0xFFFFFFFFu : ((1u << compact) - 1u);
+            c_exact += compact;
+            exact_for_slots(P, emask, cd, ci, qv);
+        }
+        __syncthreads();
+    }
+
+    cur = merge_beam(P, bd0, bi0, bd1, bi1, cur, cd, ci);
+    const uint32_t *bi = cur ? bi1 : bi0;
+    // result writer (adaptive_search.cuh:455-464)
+    for (int i = lane; i < P.K; i += 64) {
+        const uint32_t r = i < beam_sz ? (bi[i] & 0x7fffffffu) : (bi[beam_sz - 1] & 0x7fffffffu);
+        P.results[static_cast<uint64_t>(qid) * P.K + i] = r;
+    }
+    if (P.counters && lane == 0) {
+        uint32_t *c = P.counters + static_cast<uint64_t>(qid) * FG_COUNTERS_PER_QUERY;
+        c[0] = c_iters;
+        c[1] = c_exp;
+        c[2] = c_ids;
+        c[3] = c_est;
+        c[4] = c_exact;
+        c[5] = c_st2;
+    }
+}
+
+// ------------------------------------------------------------ test-hook kernels
+
+__global__ __launch_bounds__(64) void fg_prepare_kernel(const float *queries, const float *signs, int dim, int B,
+                                                        int nq, float *rotated, uint8_t *quant, float *lhw,
+                                                        int32_t *sumq, uint32_t scratch_off) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int qid = blockIdx.x;
+    if (qid >= nq) return;
+    float *rot = reinterpret_cast<float *>(smem);
+    uint32_t *planes = reinterpret_cast<uint32_t *>(smem + scratch_off);
+    float lo, hi, w;
+    int s;
+    prepare_query(queries + static_cast<uint64_t>(qid) * dim, signs, dim, B, rot, nullptr, planes, lo, hi, w, s,
+                  quant + static_cast<uint64_t>(qid) * B);
+    for (int i = lane_id(); i < B; i += 64) rotated[static_cast<uint64_t>(qid) * B + i] = rot[i];
+    if (lane_id() == 0) {
+        lhw[3 * qid] = lo;
+        lhw[3 * qid + 1] = hi;
+        lhw[3 * qid + 2] = w;
+        sumq[qid] = s;
+    }
+}
+
+struct ScoreParams {
+    const float *data, *signs, *queries;
+    const uint32_t *qix, *parents, *slots;
+    float *est_lanes, *est_seq, *exact;
+    uint64_t row_offset, code_offset, factor_offset, npoints;
+    int dim, B, deg, use_ip;
+    uint32_t n;
+    uint32_t plane_off, query_off;
+};
+
+// One workgroup per scored edge: prepares the query, then evaluates both
+// estimator variants and the exact distance of the neighbour in `slot`.
+__global__ __launch_bounds__(64) void fg_score_kernel(ScoreParams S) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const uint32_t e = blockIdx.x;
+    if (e >= S.n) return;
+    const int lane = lane_id();
+    const int nl = lane & 31, h = lane >> 5;
+    float *rot = reinterpret_cast<float *>(smem);
+    float *qv = reinterpret_cast<float *>(smem + S.query_off);
+    uint32_t *planes = reinterpret_cast<uint32_t *>(smem + S.plane_off);
+    float lo, hi, w;
+    int sq;
+    prepare_query(S.queries + static_cast<uint64_t>(S.qix[e]) * S.dim, S.signs, S.dim, S.B, rot, qv, planes, lo, hi,
+                  w, sq, nullptr);
+    const uint32_t parent = S.parents[e];
+    const int slot = static_cast<int>(S.slots[e]);
+    const float *prow = S.data + static_cast<uint64_t>(parent) * S.row_offset;
+    const float pd = uni(half_distance(prow, qv, S.dim, nl, S.use_ip != 0, true));
+    const int W = S.B >> 5;
+    const uint32_t *code = reinterpret_cast<const uint32_t *>(prow + S.code_offset) + static_cast<uint64_t>(slot) * W;
+    const float *f = prow + S.factor_offset;
+    const float tx = f[slot], fdq = f[S.deg + slot], fvq = f[2 * S.deg + slot];
+    // both halves split the words (theta == 1 layout) and one lane does all
+    // words (theta > 1 layout): the integer sums must agree.
+    const int hw = W >> 1;
+    const int32_t part = raw_partial(code, h * hw, (h + 1) * hw, planes, W);
+    const int32_t raw_split = part + __shfl_xor(part, 32);
+    const int32_t raw_full = raw_partial(code, 0, W, planes, W);
+    const float el = tx == FLT_MAX ? 0.0f : estimate_formula(raw_split, sq, w, lo, tx, fdq, fvq, pd);
+    const float es = tx == FLT_MAX ? FLT_MAX : estimate_formula(raw_full, sq, w, lo, tx, fdq, fvq, pd);
+    const uint32_t child = reinterpret_cast<const uint32_t *>(prow + (S.factor_offset + 3 * S.deg))[slot];
+    const bool child_ok = child < S.npoints;
+    const float ex = uni(half_distance(S.data + static_cast<uint64_t>(child_ok ? child : 0u) * S.row_offset, qv,
+                                       S.dim, nl, S.use_ip != 0, child_ok));
+    if (lane == 0) {
+        if (S.est_lanes) S.est_lanes[e] = el;
+        if (S.est_seq) S.est_seq[e] = es;
+        if (S.exact) S.exact[e] = ex;
+    }
+}
+
+}  // namespace
+
+// ================================================================== host side
+
+struct fg_index {
+    int device = 0;
+    float *d_rows = nullptr;
+    float *d_signs = nullptr;
+    uint64_t npoints = 0;
+    uint32_t dim = 0, padded_dim = 0, degree = 0, entry = 0;
+    uint64_t code_offset = 0, factor_offset = 0, neighbor_offset = 0, row_offset = 0;
+    int metric = FG_METRIC_L2;
+    int dup_free = 0;
+    float *d_q = nullptr;
+    size_t q_cap = 0;
+    uint32_t *d_res = nullptr;
+    size_t res_cap = 0;
+    uint32_t *d_cnt = nullptr;
+    size_t cnt_cap = 0;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string &msg) {
+    g_err = msg;
+    return code;
+}
+
+#define FG_HIP(call, what)                                                                          \
+    do {                                                                                            \
+        hipError_t _e = (call);                                                                     \
+        if (_e != hipSuccess) return fail(FG_EDEVICE, std::string(what) + ": " + hipGetErrorString(_e)); \
+    } while (0)
+
+void compute_offsets(fg_index *ix) {
+    uint32_t b = 1;
+    while (b < ix->dim) b <<= 1;
+    ix->padded_dim = b;
+    ix->code_offset = ix->dim;
+    ix->factor_offset = ix->code_offset + static_cast<uint64_t>(b / 64) * 2u * ix->degree;
+    ix->neighbor_offset = ix->factor_offset + 3ull * ix->degree;
+    ix->row_offset = ix->neighbor_offset + ix->degree;
+}
+
+int check_shape(uint32_t dim, uint32_t degree) {
+    if (dim < 33 || dim > static_cast<uint32_t>(kMaxPaddedDim))
+        return fail(FG_EINVAL, "dim must be in [33, 2048] (the code layout needs padded_dim >= 64)");
+    if (degree < 1 || degree > static_cast<uint32_t>(kMaxDegree)) return fail(FG_EINVAL, "degree must be in [1, 64]");
+    return FG_OK;
+}
+
+// include/common.hpp:26-47 + distance.hpp:14-29 (scalar loops, no contraction)
+uint32_t host_entry_point(const float *rows, uint64_t n, uint32_t dim, uint64_t row_offset, int metric) {
+    std::vector<float> c(dim, 0.0f);
+    const float inv = 1.0f / static_cast<float>(n);
+    for (uint64_t i = 0; i < n; ++i) {
+        const float *r = rows + i * row_offset;
+        for (uint32_t d = 0; d < dim; ++d) {
+            volatile float t = r[d] * inv;
+            c[d] += t;
+        }
+    }
+    uint32_t best = 0;
+    float best_d = FLT_MAX;
+    for (uint64_t i = 0; i < n; ++i) {
+        const float *r = rows + i * row_offset;
+        float s = 0.0f;
+        for (uint32_t d = 0; d < dim; ++d) {
+            if (metric == FG_METRIC_IP) {
+                volatile float p = r[d] * c[d];
+                s += p;
+            } else {
+                const float df = r[d] - c[d];
+                volatile float p = df * df;
+                s += p;
+            }
+        }
+        if (metric == FG_METRIC_IP) s = -s;
+        if (s < best_d) {
+            best_d = s;
+            best = static_cast<uint32_t>(i);
+        }
+    }
+    return best;
+}
+
+int ensure(void **p, size_t *cap, size_t need) {
+    if (*cap >= need) return FG_OK;
+    if (*p) (void)hipFree(*p);
+    *p = nullptr;
+    *cap = 0;
+    if (hipMalloc(p, need) != hipSuccess) return fail(FG_ENOMEM, "hipMalloc of search buffers failed");
+    *cap = need;
+    return FG_OK;
+}
+
+int make_params(fg_index *ix, uint32_t nq, uint32_t K, uint32_t beam, SearchParams &P) {
+    if (K < 1) return fail(FG_EINVAL, "K must be >= 1");
+    if (beam < 1 || beam > static_cast<uint32_t>(kMaxBeam))
+        return fail(FG_EINVAL, "beam must be in [1, 1024]");
+    P.data = ix->d_rows;
+    P.signs = ix->d_signs;
+    P.npoints = ix->npoints;
+    P.row_offset = ix->row_offset;
+    P.code_offset = ix->code_offset;
+    P.factor_offset = ix->factor_offset;
+    P.neighbor_offset = ix->neighbor_offset;
+    P.dim = static_cast<int>(ix->dim);
+    P.padded_dim = static_cast<int>(ix->padded_dim);
+    P.degree = static_cast<int>(ix->degree);
+    P.K = static_cast<int>(K);
+    P.beam = static_cast<int>(beam);
+    P.pbeam = static_cast<int>(effective_sort_beam(beam));
+    uint32_t cap = static_cast<uint32_t>(kSearchWidth) * ix->degree;
+    if (cap > static_cast<uint32_t>(kBufferBound)) cap = kBufferBound;
+    P.cbs = static_cast<int>(round_up_pow2(cap));
+    P.collect_cap = P.cbs < kBufferBound ? P.cbs : kBufferBound;
+    P.bitlen = static_cast<int>(visited_bitlen(beam, ix->degree));
+    P.max_iter = static_cast<int>((beam * 11 + 9) / 10);  // gpu_search_adaptive.cu:96
+    P.phase2_rho = ix->degree <= 4u ? 0.0f : 1.0f - 4.0f / static_cast<float>(ix->degree);  // utils 20-23
+    P.use_ip = ix->metric == FG_METRIC_IP ? 1 : 0;
+    P.dup_free = ix->dup_free;
+    P.entry = ix->entry;
+    P.nq = static_cast<int>(nq);
+    P.lds = lds_layout(ix->dim, ix->padded_dim, static_cast<uint32_t>(P.pbeam), static_cast<uint32_t>(P.bitlen));
+    return FG_OK;
+}
+
+int launch(fg_index *ix, const SearchParams &P, hipStream_t stream) {
+    if (P.nq == 0) return FG_OK;
+    hipLaunchKernelGGL(fg_search_kernel, dim3(P.nq), dim3(64), P.lds.total, stream, P);
+    FG_HIP(hipGetLastError(), "search kernel launch");
+    (void)ix;
+    return FG_OK;
+}
+
+bool rows_dup_free(const float *rows, uint64_t n, uint32_t degree, uint64_t nbr_off, uint64_t row_off) {
+    std::vector<uint32_t> tmp(degree);
+    for (uint64_t i = 0; i < n; ++i) {
+        const uint32_t *nb = reinterpret_cast<const uint32_t *>(rows + i * row_off + nbr_off);
+        std::copy(nb, nb + degree, tmp.begin());
+        std::sort(tmp.begin(), tmp.end());
+        for (uint32_t j = 1; j < degree; ++j)
+            if (tmp[j] == tmp[j - 1] && tmp[j] != kMaxIndex) return false;
+    }
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *fg_last_error(void) { return g_err.c_str(); }
+const char *fg_version(void) { return "flashgann-amd 0.1 (gfx950, wave64)"; }
+
+uint32_t fg_lds_bytes(uint32_t dim, uint32_t beam, uint32_t degree) {
+    uint32_t b = 1;
+    while (b < dim) b <<= 1;
+    return lds_layout(dim, b, effective_sort_beam(beam), visited_bitlen(beam, degree)).total;
+}
+
+int fg_index_create(const float *rows, uint64_t npoints, uint32_t dim, uint32_t degree, const float *signs,
+                    uint32_t entry, int metric, fg_index **out) {
+    if (!out) return fail(FG_EINVAL, "out is NULL");
+    *out = nullptr;
+    if (!rows || !signs || npoints == 0) return fail(FG_EINVAL, "rows/signs must be non-NULL and npoints > 0");
+    if (int rc = check_shape(dim, degree)) return rc;
+    if (metric != FG_METRIC_L2 && metric != FG_METRIC_IP) return fail(FG_EINVAL, "unknown metric");
+    fg_index *ix = new (std::nothrow) fg_index();
+    if (!ix) return fail(FG_ENOMEM, "host allocation failed");
+    ix->npoints = npoints;
+    ix->dim = dim;
+    ix->degree = degree;
+    ix->metric = metric;
+    compute_offsets(ix);
+    if (entry == FG_ENTRY_AUTO) entry = host_entry_point(rows, npoints, dim, ix->row_offset, metric);
+    if (entry >= npoints) {
+        delete ix;
+        return fail(FG_EINVAL, "entry point out of range");
+    }
+    ix->entry = entry;
+    ix->dup_free = rows_dup_free(rows, npoints, degree, ix->neighbor_offset, ix->row_offset) ? 1 : 0;
+    const size_t bytes = static_cast<size_t>(npoints) * ix->row_offset * sizeof(float);
+    size_t free_b = 0, total_b = 0;
+    if (hipGetDevice(&ix->device) != hipSuccess || hipMemGetInfo(&free_b, &total_b) != hipSuccess) {
+        delete ix;
+        return fail(FG_EDEVICE, "no HIP device available");
+    }
+    if (bytes + ix->padded_dim * sizeof(float) > free_b) {  // gpu_search_adaptive.cu:61-63
+        delete ix;
+        return fail(FG_ENOMEM, "QG upload exceeds currently available GPU memory");
+    }
+    if (hipMalloc(&ix->d_rows, bytes) != hipSuccess || hipMalloc(&ix->d_signs, ix->padded_dim * sizeof(float)) != hipSuccess) {
+        fg_index_destroy(ix);
+        return fail(FG_ENOMEM, "hipMalloc of the codebook failed");
+    }
+    if (hipMemcpy(ix->d_rows, rows, bytes, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(ix->d_signs, signs, ix->padded_dim * sizeof(float), hipMemcpyHostToDevice) != hipSuccess ||
+        hipEventCreate(&ix->ev0) != hipSuccess || hipEventCreate(&ix->ev1) != hipSuccess) {
+        fg_index_destroy(ix);
+        return fail(FG_EDEVICE, "codebook upload failed");
+    }
+    *out = ix;
+    return FG_OK;
+}
+
+int fg_index_load(const char *path, uint64_t npoints, uint32_t dim, uint32_t degree, int metric, fg_index **out) {
+    if (!out || !path) return fail(FG_EINVAL, "NULL argument");
+    *out = nullptr;
+    if (int rc = check_shape(dim, degree)) return rc;
+    fg_index tmp;
+    tmp.dim = dim;
+    tmp.degree = degree;
+    compute_offsets(&tmp);
+    std::ifstream f(path, std::ios::binary);
+    if (!f) return fail(FG_EIO, std::string("Cannot open codebook file: ") + path);
+    uint32_t entry = 0;
+    const size_t nfl = static_cast<size_t>(npoints) * tmp.row_offset;
+    std::vector<float> rows;
+    std::vector<float> signs(tmp.padded_dim);
+    try {
+        rows.resize(nfl);
+    } catch (...) {
+        return fail(FG_ENOMEM, "host allocation for the codebook failed");
+    }
+    f.read(reinterpret_cast<char *>(&entry), sizeof(entry));
+    f.read(reinterpret_cast<char *>(rows.data()), static_cast<std::streamsize>(nfl * sizeof(float)));
+    f.read(reinterpret_cast<char *>(signs.data()), static_cast<std::streamsize>(signs.size() * sizeof(float)));
+    if (!f) return fail(FG_EIO, std::string("codebook file is truncated: ") + path);
+    return fg_index_create(rows.data(), npoints, dim, degree, signs.data(), entry, metric, out);
+}
+
+void fg_index_destroy(fg_index *ix) {
+    if (!ix) return;
+    if (ix->d_rows) (void)hipFree(ix->d_rows);
+    if (ix->d_signs) (void)hipFree(ix->d_signs);
+    if (ix->d_q) (void)hipFree(ix->d_q);
+    if (ix->d_res) (void)hipFree(ix->d_res);
+    if (ix->d_cnt) (void)hipFree(ix->d_cnt);
+    if (ix->ev0) (void)hipEventDestroy(ix->ev0);
+    if (ix->ev1) (void)hipEventDestroy(ix->ev1);
+    delete ix;
+}
+
+int fg_index_get_info(const fg_index *ix, fg_index_info *info) {
+    if (!ix || !info) return fail(FG_EINVAL, "NULL argument");
+    info->dim = ix->dim;
+    info->padded_dim = ix->padded_dim;
+    info->degree = ix->degree;
+    info->entry = ix->entry;
+    info->npoints = ix->npoints;
+    info->code_offset = ix->code_offset;
+    info->factor_offset = ix->factor_offset;
+    info->neighbor_offset = ix->neighbor_offset;
+    info->row_offset = ix->row_offset;
+    info->metric = ix->metric;
+    return FG_OK;
+}
+
+int fg_search_device(fg_index *ix, const float *d_queries, uint32_t nq, uint32_t K, uint32_t beam,
+                     uint32_t *d_results, uint32_t *d_counters, void *stream) {
+    if (!ix) return fail(FG_EINVAL, "index is NULL");
+    if (nq && (!d_queries || !d_results)) return fail(FG_EINVAL, "NULL device buffer");
+    SearchParams P;
+    if (int rc = make_params(ix, nq, K, beam, P)) return rc;
+    P.queries = d_queries;
+    P.results = d_results;
+    P.counters = d_counters;
+    return launch(ix, P, reinterpret_cast<hipStream_t>(stream));
+}
+
+int fg_search(fg_index *ix, const float *queries, uint32_t nq, uint32_t K, uint32_t beam, uint32_t *result_ids,
+              uint32_t *counters, fg_stats *stats) {
+    if (!ix) return fail(FG_EINVAL, "index is NULL");
+    if (nq && (!queries || !result_ids)) return fail(FG_EINVAL, "NULL host buffer");
+    SearchParams P;
+    if (int rc = make_params(ix, nq, K, beam, P)) return rc;
+    if (stats) {
+        stats->elapsed_s = 0.0;
+        stats->kernel_ms = 0.0f;
+        stats->lds_bytes = P.lds.total;
+        stats->hash_bitlen = static_cast<uint32_t>(P.bitlen);
+    }
+    if (nq == 0) return FG_OK;
+    const size_t qb = static_cast<size_t>(nq) * ix->dim * sizeof(float);
+    const size_t rb = static_cast<size_t>(nq) * K * sizeof(uint32_t);
+    const size_t cb = static_cast<size_t>(nq) * FG_COUNTERS_PER_QUERY * sizeof(uint32_t);
+    if (int rc = ensure(reinterpret_cast<void **>(&ix->d_q), &ix->q_cap, qb)) return rc;
+    if (int rc = ensure(reinterpret_cast<void **>(&ix->d_res), &ix->res_cap, rb)) return rc;
+    if (counters)
+        if (int rc = ensure(reinterpret_cast<void **>(&ix->d_cnt), &ix->cnt_cap, cb)) return rc;
+    FG_HIP(hipMemcpy(ix->d_q, queries, qb, hipMemcpyHostToDevice), "query upload");
+    FG_HIP(hipDeviceSynchronize(), "sync before search");
+    P.queries = ix->d_q;
+    P.results = ix->d_res;
+    P.counters = counters ? ix->d_cnt : nullptr;
+    const auto t0 = std::chrono::high_resolution_clock::now();
+    FG_HIP(hipEventRecord(ix->ev0, nullptr), "event record");
+    if (int rc = launch(ix, P, nullptr)) return rc;
+    FG_HIP(hipEventRecord(ix->ev1, nullptr), "event record");
+    FG_HIP(hipDeviceSynchronize(), "search kernel");
+    const auto t1 = std::chrono::high_resolution_clock::now();
+    if (stats) {
+        stats->elapsed_s = std::chrono::duration<double>(t1 - t0).count();
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, ix->ev0, ix->ev1) == hipSuccess) stats->kernel_ms = ms;
+    }
+    FG_HIP(hipMemcpy(result_ids, ix->d_res, rb, hipMemcpyDeviceToHost), "result download");
+    if (counters) FG_HIP(hipMemcpy(counters, ix->d_cnt, cb, hipMemcpyDeviceToHost), "counter download");
+    return FG_OK;
+}
+
+int fg_query_prepare(fg_index *ix, const float *queries, uint32_t nq, float *rotated, uint8_t *quantized,
+                     float *lhw, int32_t *sum_q) {
+    if (!ix || !queries || !rotated || !quantized || !lhw || !sum_q) return fail(FG_EINVAL, "NULL argument");
+    if (nq == 0) return FG_OK;
+    const uint32_t B = ix->padded_dim;
+    float *dq = nullptr, *drot = nullptr, *dl = nullptr;
+    uint8_t *dqt = nullptr;
+    int32_t *ds = nullptr;
+    int rc = FG_OK;
+    const size_t qb = static_cast<size_t>(nq) * ix->dim * 4;
+    if (hipMalloc(&dq, qb) != hipSuccess || hipMalloc(&drot, static_cast<size_t>(nq) * B * 4) != hipSuccess ||
+        hipMalloc(&dqt, static_cast<size_t>(nq) * B) != hipSuccess || hipMalloc(&dl, nq * 12ull) != hipSuccess ||
+        hipMalloc(&ds, nq * 4ull) != hipSuccess) {
+        rc = fail(FG_ENOMEM, "hipMalloc failed");
+    }
+    if (rc == FG_OK && hipMemcpy(dq, queries, qb, hipMemcpyHostToDevice) != hipSuccess) rc = fail(FG_EDEVICE, "upload");
+    if (rc == FG_OK) {
+        const uint32_t scratch = B * 4;
+        const uint32_t lds = scratch + 8 * (B / 32) * 4;
+        hipLaunchKernelGGL(fg_prepare_kernel, dim3(nq), dim3(64), lds, nullptr, dq, ix->d_signs,
+                           static_cast<int>(ix->dim), static_cast<int>(B), static_cast<int>(nq), drot, dqt, dl, ds,
+                           scratch);
+        if (hipGetLastError() != hipSuccess || hipDeviceSynchronize() != hipSuccess) rc = fail(FG_EDEVICE, "prepare kernel");
+    }
+    if (rc == FG_OK && (hipMemcpy(rotated, drot, static_cast<size_t>(nq) * B * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+                        hipMemcpy(quantized, dqt, static_cast<size_t>(nq) * B, hipMemcpyDeviceToHost) != hipSuccess ||
+                        hipMemcpy(lhw, dl, nq * 12ull, hipMemcpyDeviceToHost) != hipSuccess ||
+                        hipMemcpy(sum_q, ds, nq * 4ull, hipMemcpyDeviceToHost) != hipSuccess))
+        rc = fail(FG_EDEVICE, "download");
+    (void)hipFree(dq);
+    (void)hipFree(drot);
+    (void)hipFree(dqt);
+    (void)hipFree(dl);
+    (void)hipFree(ds);
+    return rc;
+}
+
+int fg_score_edges(fg_index *ix, const float *queries, uint32_t nq, const uint32_t *query_ix, const uint32_t *parents,
+                   const uint32_t *slots, uint32_t n, float *est_lanes, float *est_seq, float *exact) {
+    if (!ix || !queries || !query_ix || !parents || !slots) return fail(FG_EINVAL, "NULL argument");
+    if (n == 0) return FG_OK;
+    for (uint32_t i = 0; i < n; ++i) {
+        if (query_ix[i] >= nq || parents[i] >= ix->npoints || slots[i] >= ix->degree)
+            return fail(FG_EINVAL, "score triple out of range");
+    }
+    const uint32_t B = ix->padded_dim;
+    ScoreParams S{};
+    S.data = ix->d_rows;
+    S.signs = ix->d_signs;
+    S.row_offset = ix->row_offset;
+    S.code_offset = ix->code_offset;
+    S.factor_offset = ix->factor_offset;
+    S.npoints = ix->npoints;
+    S.dim = static_cast<int>(ix->dim);
+    S.B = static_cast<int>(B);
+    S.deg = static_cast<int>(ix->degree);
+    S.use_ip = ix->metric == FG_METRIC_IP;
+    S.n = n;
+    S.query_off = B * 4;
+    S.plane_off = S.query_off + ((ix->dim + 3) & ~3u) * 4;
+    const uint32_t lds = S.plane_off + 8 * (B / 32) * 4;
+    float *dq = nullptr, *o1 = nullptr, *o2 = nullptr, *o3 = nullptr;
+    uint32_t *t1 = nullptr, *t2 = nullptr, *t3 = nullptr;
+    int rc = FG_OK;
+    const size_t qb = static_cast<size_t>(nq) * ix->dim * 4;
+    if (hipMalloc(&dq, qb) != hipSuccess || hipMalloc(&o1, n * 4ull) != hipSuccess || hipMalloc(&o2, n * 4ull) != hipSuccess ||
+        hipMalloc(&o3, n * 4ull) != hipSuccess || hipMalloc(&t1, n * 4ull) != hipSuccess ||
+        hipMalloc(&t2, n * 4ull) != hipSuccess || hipMalloc(&t3, n * 4ull) != hipSuccess)
+        rc = fail(FG_ENOMEM, "hipMalloc failed");
+    if (rc == FG_OK && (hipMemcpy(dq, queries, qb, hipMemcpyHostToDevice) != hipSuccess ||
+                        hipMemcpy(t1, query_ix, n * 4ull, hipMemcpyHostToDevice) != hipSuccess ||
+                        hipMemcpy(t2, parents, n * 4ull, hipMemcpyHostToDevice) != hipSuccess ||
+                        hipMemcpy(t3, slots, n * 4ull, hipMemcpyHostToDevice) != hipSuccess))
+        rc = fail(FG_EDEVICE, "upload");
+    if (rc == FG_OK) {
+        S.queries = dq;
+        S.qix = t1;
+        S.parents = t2;
+        S.slots = t3;
+        S.est_lanes = o1;
+        S.est_seq = o2;
+        S.exact = o3;
+        hipLaunchKernelGGL(fg_score_kernel, dim3(n), dim3(64), lds, nullptr, S);
+        if (hipGetLastError() != hipSuccess || hipDeviceSynchronize() != hipSuccess) rc = fail(FG_EDEVICE, "score kernel");
+    }
+    if (rc == FG_OK) {
+        if ((est_lanes && hipMemcpy(est_lanes, o1, n * 4ull, hipMemcpyDeviceToHost) != hipSuccess) ||
+            (est_seq && hipMemcpy(est_seq, o2, n * 4ull, hipMemcpyDeviceToHost) != hipSuccess) ||
+            (exact && hipMemcpy(exact, o3, n * 4ull, hipMemcpyDeviceToHost) != hipSuccess))
+            rc = fail(FG_EDEVICE, "download");
+    }
+    (void)hipFree(dq);
+    (void)hipFree(o1);
+    (void)hipFree(o2);
+    (void)hipFree(o3);
+    (void)hipFree(t1);
+    (void)hipFree(t2);
+    (void)hipFree(t3);
+    return rc;
+}
+
+}  // extern "C"

@@ -1,0 +1,74 @@
+"""Seeded synthetic datasets for the benchmark configurations.
+
+All draws use numpy's PCG64 with fixed seeds (stable for a given numpy
+version), seeded as 0xF1A50000 + 16*config + stream with streams
+0 = means, 1 = base, 2 = queries, 3 = signs.
+
+  C1  N x 128 integer Gaussian mixture, 64 components: means ~ U[0,100]^d,
+      x = max(0, rint(mu + 10 z)); queries from the same mixture.
+  C2  as C1 with 1024 components (the headline configuration, N = 1M).
+  C3  N x 96 unit vectors: 1024 components, means ~ N(0,1), x = mu + 0.3 z,
+      normalised; queries = base point + N(0, 0.05), renormalised.
+  C4  N x 960 in [0,1]: 256 components, means ~ U[0,1], x = clip(mu+0.1 z).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+SEED_BASE = 0xF1A50000
+
+
+def _rng(config: int, stream: int) -> np.random.Generator:
+    return np.random.Generator(np.random.PCG64(SEED_BASE + 16 * config + stream))
+
+
+def integer_mixture(n: int, nq: int, dim: int = 128, components: int = 64, config: int = 1,
+                    sigma: float = 10.0):
+    """C1/C2 generator: returns (base, queries) as float32 with integer values."""
+    means = _rng(config, 0).uniform(0.0, 100.0, size=(components, dim)).astype(np.float32)
+
+    def draw(count: int, stream: int) -> np.ndarray:
+        r = _rng(config, stream)
+        comp = r.integers(0, components, size=count)
+        out = np.empty((count, dim), dtype=np.float32)
+        step = 1 << 16
+        for s in range(0, count, step):
+            e = min(count, s + step)
+            z = r.standard_normal(size=(e - s, dim), dtype=np.float32)
+            out[s:e] = np.maximum(0.0, np.rint(means[comp[s:e]] + sigma * z))
+        return out
+
+    return draw(n, 1), draw(nq, 2)
+
+
+def normalized_mixture(n: int, nq: int, dim: int = 96, components: int = 1024, config: int = 3):
+    """C3 generator: unit-normalised mixture, queries perturbed from base points."""
+    means = _rng(config, 0).standard_normal(size=(components, dim)).astype(np.float32)
+    r = _rng(config, 1)
+    comp = r.integers(0, components, size=n)
+    base = means[comp] + 0.3 * r.standard_normal(size=(n, dim), dtype=np.float32)
+    base /= np.linalg.norm(base, axis=1, keepdims=True)
+    rq = _rng(config, 2)
+    pick = rq.integers(0, n, size=nq)
+    q = base[pick] + 0.05 * rq.standard_normal(size=(nq, dim), dtype=np.float32)
+    q /= np.linalg.norm(q, axis=1, keepdims=True)
+    return base.astype(np.float32), q.astype(np.float32)
+
+
+def unit_box_mixture(n: int, nq: int, dim: int = 960, components: int = 256, config: int = 4):
+    """C4 generator: values in [0,1]."""
+    means = _rng(config, 0).uniform(0.0, 1.0, size=(components, dim)).astype(np.float32)
+
+    def draw(count: int, stream: int) -> np.ndarray:
+        r = _rng(config, stream)
+        comp = r.integers(0, components, size=count)
+        z = r.standard_normal(size=(count, dim), dtype=np.float32)
+        return np.clip(means[comp] + 0.1 * z, 0.0, 1.0).astype(np.float32)
+
+    return draw(n, 1), draw(nq, 2)
+
+
+def signs_for(padded_dim: int, config: int = 1) -> np.ndarray:
+    """The +-1 diagonal of the rotation P = H_B * diag(signs)."""
+    r = _rng(config, 3)
+    return np.where(r.integers(0, 2, size=padded_dim) == 1, 1.0, -1.0).astype(np.float32)

@@ -1,0 +1,126 @@
+/*
+ * flashgann.h -- C ABI of the MI355X (gfx950) adaptive graph beam search.
+ *
+ * Drop-in boundary for the reference's search path.  The reference exposes it
+ * as a C++ member function, not a plugin:
+ *   QuantizationGraph::QuantizationGraph(num_node, dim, degree, codebook_path)
+ *       include/qg.hpp:17-42
+ *   void QuantizationGraph::gpu_search_adaptive(int nq, const float *queries,
+ *       int K, vidType *result_idx, int beam_sz, double &elapsed)
+ *       include/qg.hpp:62-63, gpu_search_adaptive.cu:12-114
+ *   __global__ QuantizedPrunedBeamSearch(...)   src/adaptive_search.cuh:5-11
+ * The entry points below carry the same arguments with the same meaning, as
+ * plain pointers and sizes.  Buffers are caller-owned; the index owns its
+ * device copy of the codebook (uploaded once, instead of once per call as
+ * gpu_search_adaptive.cu:65-71 does).
+ *
+ * Every function returns 0 on success and a negative FG_E* code on failure;
+ * fg_last_error() then describes the failure (thread-local string).
+ */
+#ifndef FLASHGANN_H
+#define FLASHGANN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FG_OK 0
+#define FG_EINVAL -1     /* argument outside the supported range */
+#define FG_ENOMEM -2     /* device allocation failed / not enough free memory */
+#define FG_EDEVICE -3    /* HIP runtime error */
+#define FG_EIO -4        /* file missing or truncated */
+
+#define FG_METRIC_L2 0   /* include/metric.hpp:9 METRIC_L2 */
+#define FG_METRIC_IP 1   /* include/metric.hpp:9 METRIC_IP */
+
+#define FG_ENTRY_AUTO 0xFFFFFFFFu  /* qg.hpp entry field == UINT32_MAX */
+
+typedef struct fg_index fg_index;
+
+/* Codebook geometry in float units (include/qg.hpp:66-73). */
+typedef struct {
+    uint32_t dim;
+    uint32_t padded_dim;
+    uint32_t degree;
+    uint32_t entry;
+    uint64_t npoints;
+    uint64_t code_offset;
+    uint64_t factor_offset;
+    uint64_t neighbor_offset;
+    uint64_t row_offset;
+    int metric;
+} fg_index_info;
+
+/* Per-call statistics. */
+typedef struct {
+    double elapsed_s;        /* host wall clock around launch + sync
+                                (gpu_search_adaptive.cu:98-107) */
+    float kernel_ms;         /* HIP-event time of the search kernel */
+    uint32_t lds_bytes;      /* dynamic LDS per workgroup (one query) */
+    uint32_t hash_bitlen;    /* visited-table size used by the kernel */
+} fg_stats;
+
+/* Per-query work counters (6 x uint32 per query when requested):
+ * iterations, expansions, ids_read, estimates, exact, stage2_iter. */
+#define FG_COUNTERS_PER_QUERY 6
+
+/* Replaces the QuantizationGraph constructor's upload half
+ * (include/qg.hpp:17-42 + gpu_search_adaptive.cu:65-71): copies npoints rows
+ * of the codebook (row layout of fg_index_info) and padded_dim signs to the
+ * current device.  entry == FG_ENTRY_AUTO picks the node nearest the float
+ * centroid with the reference's host routine semantics
+ * (include/common.hpp:26-47, gpu_search_adaptive.cu:74-77). */
+int fg_index_create(const float *rows, uint64_t npoints, uint32_t dim, uint32_t degree,
+                    const float *signs, uint32_t entry, int metric, fg_index **out);
+
+/* Same as fg_index_create but reads the reference's codebook file
+ * (include/qg.hpp:17-42); a truncated file is FG_EIO instead of being read
+ * short. */
+int fg_index_load(const char *codebook_path, uint64_t npoints, uint32_t dim, uint32_t degree,
+                  int metric, fg_index **out);
+
+void fg_index_destroy(fg_index *index);
+
+int fg_index_get_info(const fg_index *index, fg_index_info *info);
+
+/* Replaces QuantizationGraph::gpu_search_adaptive (gpu_search_adaptive.cu:12-114):
+ * host queries (nq x dim float32, row-major) in, host result ids
+ * (nq x K uint32) out.  stats->elapsed_s is the kernel-only time the reference
+ * reports as `elapsed`.  counters may be NULL, else nq*6 uint32 (host). */
+int fg_search(fg_index *index, const float *queries, uint32_t nq, uint32_t K, uint32_t beam,
+              uint32_t *result_ids, uint32_t *counters, fg_stats *stats);
+
+/* Device-resident variant: d_queries, d_results (and d_counters, may be NULL)
+ * are device pointers; the kernel is enqueued on `stream` (a hipStream_t, NULL
+ * = default stream) and the call returns without synchronising.  This is the
+ * kernel launch of gpu_search_adaptive.cu:99-103 on its own. */
+int fg_search_device(fg_index *index, const float *d_queries, uint32_t nq, uint32_t K,
+                     uint32_t beam, uint32_t *d_results, uint32_t *d_counters, void *stream);
+
+/* Dynamic LDS bytes one query's workgroup needs (the analogue of
+ * calculate_shared_mem_size, src/adaptive_search_utils.cuh:152-176). */
+uint32_t fg_lds_bytes(uint32_t dim, uint32_t beam, uint32_t degree);
+
+/* Query preparation only (utils.cuh:840-939): rotated query (padded_dim
+ * float32), quantized levels (padded_dim uint8), and {low, high, width} plus
+ * sum_q, for nq host queries.  Test hook for the preparation stage. */
+int fg_query_prepare(fg_index *index, const float *queries, uint32_t nq, float *rotated,
+                     uint8_t *quantized, float *low_high_width, int32_t *sum_q);
+
+/* Estimates and exact distances for explicit (query, parent, neighbour slot)
+ * triples, with both estimator variants (utils.cuh:941-1027) and the exact
+ * distance (utils.cuh:269-305).  Test hook for the scoring stages.
+ * est_lanes/est_seq/exact are n floats each; any may be NULL. */
+int fg_score_edges(fg_index *index, const float *queries, uint32_t nq, const uint32_t *query_ix,
+                   const uint32_t *parents, const uint32_t *slots, uint32_t n, float *est_lanes,
+                   float *est_seq, float *exact);
+
+const char *fg_last_error(void);
+const char *fg_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FLASHGANN_H */

@@ -1,0 +1,937 @@
+/*
+ * fg_oracle.c -- CPU restatement of FlashGANN's adaptive graph beam search
+ * (reference: src/adaptive_search.cuh, src/adaptive_search_utils.cuh,
+ * src/adaptive_search_config.cuh, include/utils.cuh, include/qg.hpp,
+ * include/common.hpp, gpu_search_adaptive.cu).
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker for the HIP path, never the product.
+ *
+ * Build: oracle/Makefile, with -ffp-contract=off so that the only fused
+ * multiply-adds are the explicit fmaf() calls placed where nvcc's default
+ * --fmad=true contracts the reference's expressions.
+ *
+ * How each piece is pinned (tests/test_oracle_*.py):
+ *   layout / sizing helpers      hand-computed values for the configs
+ *   FWHT (fgo_rotate)            O(B^2) Sylvester-Hadamard product, exact on
+ *                                integer inputs
+ *   quantizer / LUT              closed form: LUT[m] = sum of q over bits of m
+ *                                (mod 256); q in [1, 64]; sum_q = sum q
+ *   estimators                   closed form vs the bit-plane identity
+ *                                raw = sum_i b_i q_i (minus the u8 wrap), and a
+ *                                statistical check against exact L2
+ *   warp distances               float64 textbook sum within 1e-5 relative;
+ *                                exact on integer data
+ *   bitonic network              sortedness + permutation vs sorted() on
+ *                                distinct keys; tie behaviour by brute force
+ *                                of compare-exchange on tiny inputs
+ *   merges                       vs heapq.merge / sorted() on distinct keys
+ *   hash                         set semantics vs a Python set
+ *   pick / keep / controller     hand-computed cases
+ *   entry point / recall / I/O   the reference's own host headers compiled
+ *                                from /root/reference (oracle/_ref)
+ *   whole search                 recall vs brute-force ground truth, plus
+ *                                internal invariants (sorted beam, unique
+ *                                expansions, counters)
+ * The speculative-round visibility rule and the fp-contraction sites cannot be
+ * pinned without running the reference (no CUDA toolchain here): they are the
+ * oracle's stated choices, recorded as "parity unpinned" in the design notes.
+ */
+#include "fg_oracle.h"
+
+#include <float.h>
+#include <math.h>
+#include <pthread.h>
+#include <stdatomic.h>
+#include <stdlib.h>
+#include <string.h>
+
+static inline uint32_t umin32(uint32_t a, uint32_t b) { return a < b ? a : b; }
+static inline int clamp_int(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+static inline float clamp_float(float v, float lo, float hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+/* ------------------------------------------------------------------ sizing */
+
+/* qg.hpp:66-73 (padded_dim via an integer power-of-two round-up, equal to
+ * 1 << ceil(log2(dim)) for every dim used here). */
+int fgo_compute_layout(uint32_t dim, uint32_t degree, fgo_layout *out) {
+    if (dim == 0 || degree == 0) return -1;
+    uint32_t b = 1;
+    while (b < dim) b <<= 1;
+    out->dim = dim;
+    out->padded_dim = b;
+    out->degree = degree;
+    out->code_offset = dim;
+    out->factor_offset = out->code_offset + (uint64_t)(b / 64) * 2u * degree;
+    out->neighbor_offset = out->factor_offset + 3u * (uint64_t)degree;
+    out->row_offset = out->neighbor_offset + degree;
+    return 0;
+}
+
+/* utils.cuh:68-78 */
+uint32_t fgo_round_up_pow2(uint32_t x) {
+    if (x <= 1) return 1;
+    --x;
+    x |= x >> 1; x |= x >> 2; x |= x >> 4; x |= x >> 8; x |= x >> 16;
+    return x + 1;
+}
+
+/* utils.cuh:119-127 (GPU_FAST_BITONIC_TOPK_CAP = 128, WARP_SIZE = 32) */
+uint32_t fgo_effective_sort_beam_size(uint32_t beam) {
+    if (beam == 0) return 0;
+    uint32_t r = fgo_round_up_pow2(beam);
+    if (r <= 128) return r < 32 ? 32 : r;
+    return beam;
+}
+
+/* utils.cuh:137-151 (GPU_HASH_BASE_BITLEN = 11) */
+uint32_t fgo_hash_bitlen(uint32_t pbeam, uint32_t cbs, uint32_t reset_interval) {
+    uint64_t req64 = (uint64_t)pbeam + (uint64_t)cbs * reset_interval;
+    uint32_t req = req64 > 0xffffffffull ? 0xffffffffu : (uint32_t)req64;
+    uint32_t target = (req * 4u + 2u) / 3u;
+    uint32_t cap = 1u << 11;
+    while (cap < target) cap <<= 1;
+    uint32_t bitlen = 0;
+    while ((1u << bitlen) < cap) ++bitlen;
+    return bitlen;
+}
+
+/* adaptive_search_utils.cuh:145-150 (THETA_MAX = 8, BUFFER_BOUND = 32) */
+uint32_t fgo_candidate_buffer_capacity(uint32_t degree) {
+    uint32_t maxc = (uint32_t)FGO_SEARCH_WIDTH * degree;
+    uint32_t c = FGO_BUFFER_BOUND;
+    return c > maxc ? maxc : c;
+}
+
+/* adaptive_search_utils.cuh:20-23 (MIN_PHASE2_KEEP = 4, RHO_MIN = 0) */
+float fgo_max_rho_bound(uint32_t degree) {
+    if (degree <= 4u) return 0.0f;
+    return 1.0f - 4.0f / (float)degree;
+}
+
+/* utils.cuh:104-117 */
+uint32_t fgo_keep_count_per_parent(uint32_t max_degree, float rho) {
+    float kf = 1.0f - rho;
+    if (kf < 0.0f) kf = 0.0f;
+    if (kf > 1.0f) kf = 1.0f;
+    uint32_t k = (uint32_t)ceilf((float)max_degree * kf);
+    if (k < 1) k = 1;
+    if (k > max_degree) k = max_degree;
+    return k;
+}
+
+/* adaptive_search_utils.cuh:121-135 */
+int fgo_keep_count_for_expander(uint32_t active, int theta, float rho, int kth_valid, uint32_t near) {
+    const int active_count = (int)active;
+    const int rho_keep = (int)fgo_keep_count_per_parent(active, rho);
+    const uint32_t per_parent_bound = (uint32_t)FGO_BUFFER_BOUND / (uint32_t)theta;
+    const int budget_keep = clamp_int((int)per_parent_bound, 1, active_count);
+    int max_keep = rho_keep < budget_keep ? rho_keep : budget_keep;
+    if (kth_valid) max_keep = clamp_int((int)near, 1, max_keep);
+    return clamp_int(max_keep, 1, active_count);
+}
+
+/* ------------------------------------------------------- query preparation */
+
+/* utils.cuh:790-821: x*signs, zero pad, unnormalised radix-2 FWHT with
+ * len = 1, 2, ..., B/2 and butterflies (u+v, u-v). */
+void fgo_rotate(const float *src, const float *signs, int dim, int padded_dim, float *dst) {
+    for (int i = 0; i < dim; ++i) dst[i] = src[i] * signs[i];
+    for (int i = dim; i < padded_dim; ++i) dst[i] = 0.0f;
+    for (int len = 1; len < padded_dim; len <<= 1) {
+        int pairs = padded_dim >> 1;
+        for (int p = 0; p < pairs; ++p) {
+            int block = p / len, j = p % len;
+            int i1 = block * (len << 1) + j, i2 = i1 + len;
+            float u = dst[i1], v = dst[i2];
+            dst[i1] = u + v;
+            dst[i2] = u - v;
+        }
+    }
+}
+
+/* utils.cuh:840-939.  width = (high-low) * fl(1/63); q = lroundf(fma(y-low,
+ * 1/width, 0.5)) (contracted as nvcc does); u8 LUT of the 16 subset sums per
+ * 4-dim chunk, bit 3 <-> dim 4cb+0 ... bit 0 <-> dim 4cb+3, wrapping mod 256.
+ * A NaN scale (constant rotated query, width 0) quantizes to 0: the reference
+ * leaves that case undefined (lroundf of NaN); 0 is what a saturating
+ * float-to-integer conversion gives. */
+void fgo_query_prepare(const float *query, const float *signs, int dim, int padded_dim,
+                       fgo_query_factors *qf) {
+    const float levels_inv = 1.0f / 63.0f;
+    fgo_rotate(query, signs, dim, padded_dim, qf->rotated);
+    float lo = FLT_MAX, hi = -FLT_MAX;
+    for (int i = 0; i < padded_dim; ++i) {
+        lo = fminf(lo, qf->rotated[i]);
+        hi = fmaxf(hi, qf->rotated[i]);
+    }
+    qf->low = lo;
+    qf->high = hi;
+    qf->width = (hi - lo) * levels_inv;
+    const float inv_width = 1.0f / qf->width;
+    int32_t sum = 0;
+    const int ncb = padded_dim >> 2;
+    for (int cb = 0; cb < ncb; ++cb) {
+        uint8_t q[4];
+        for (int j = 0; j < 4; ++j) {
+            const int idx = (cb << 2) + j;
+            const float scaled = fmaf(qf->rotated[idx] - lo, inv_width, 0.5f);
+            q[j] = isnan(scaled) ? 0 : (uint8_t)lroundf(scaled);
+            qf->q[idx] = q[j];
+            sum += q[j];
+        }
+        uint8_t *lut = qf->lut + (cb << 4);
+        lut[0] = 0;
+        for (int mask = 1; mask < 16; ++mask) {
+            const int lowbit = mask & -mask;
+            const int pos = lowbit == 8 ? 0 : (lowbit == 4 ? 1 : (lowbit == 2 ? 2 : 3));
+            lut[mask] = (uint8_t)(lut[mask - lowbit] + q[pos]);
+        }
+    }
+    qf->sum_q = sum;
+}
+
+/* utils.cuh:823-838 (LUT_LAYOUT_LANES = 32): chunk cb of one neighbour's code is
+ * the low nibble of byte cb>>1 when cb is even, the high nibble when odd. */
+static inline uint32_t code_nibble(const uint8_t *code, int cb) {
+    const uint8_t packed = code[cb >> 1];
+    return (cb & 1) ? (uint32_t)(packed >> 4) : (uint32_t)(packed & 0x0f);
+}
+
+/* utils.cuh:976-980 / 1016-1020: raw = sum over chunks of LUT[cb][nibble]. */
+uint32_t fgo_raw_lut(const fgo_query_factors *qf, const uint8_t *code, int padded_dim) {
+    uint32_t raw = 0;
+    const int ncb = padded_dim >> 2;
+    for (int cb = 0; cb < ncb; ++cb) raw += qf->lut[(cb << 4) + code_nibble(code, cb)];
+    return raw;
+}
+
+static inline float estimate_formula(const fgo_query_factors *qf, uint32_t raw, float tx,
+                                     float fdq, float fvq, float pdist) {
+    /* utils.cuh:989-993 / 1022-1026, with the two multiply-adds contracted. */
+    const float rf = (float)(((int32_t)raw << 1) - qf->sum_q);
+    float est = tx + pdist;
+    est = fmaf(fdq * qf->width, rf, est);
+    est = fmaf(fvq, qf->low, est);
+    return est;
+}
+
+/* utils.cuh:941-994 (theta == 1 path): triple_x == FLT_MAX gives 0.0f. */
+float fgo_estimate_lanes(const fgo_query_factors *qf, const uint8_t *code, float triple_x,
+                         float factor_dq, float factor_vq, float parent_dist, int padded_dim) {
+    if (triple_x == FLT_MAX) return 0.0f;
+    return estimate_formula(qf, fgo_raw_lut(qf, code, padded_dim), triple_x, factor_dq,
+                            factor_vq, parent_dist);
+}
+
+/* utils.cuh:996-1027 (theta > 1 path): triple_x == FLT_MAX gives FLT_MAX. */
+float fgo_estimate_seq(const fgo_query_factors *qf, const uint8_t *code, float triple_x,
+                       float factor_dq, float factor_vq, float parent_dist, int padded_dim) {
+    if (triple_x == FLT_MAX) return FLT_MAX;
+    return estimate_formula(qf, fgo_raw_lut(qf, code, padded_dim), triple_x, factor_dq,
+                            factor_vq, parent_dist);
+}
+
+/* --------------------------------------------------------------- distances */
+
+/* utils.cuh:269-284: lane l (of 32) accumulates dims l, l+32, ... with a
+ * contracted val += d*d, then a shfl_down tree 16, 8, 4, 2, 1 read at lane 0. */
+float fgo_warp_l2(int dim, const float *a, const float *b) {
+    float v[32];
+    for (int l = 0; l < 32; ++l) {
+        float val = 0.0f;
+        for (int i = l; i < dim; i += 32) {
+            const float d = a[i] - b[i];
+            val = fmaf(d, d, val);
+        }
+        v[l] = val;
+    }
+    for (int off = 16; off >= 1; off >>= 1)
+        for (int l = 0; l < off; ++l) v[l] = v[l] + v[l + off];
+    return v[0];
+}
+
+/* utils.cuh:286-300 */
+float fgo_warp_ip(int dim, const float *a, const float *b) {
+    float v[32];
+    for (int l = 0; l < 32; ++l) {
+        float val = 0.0f;
+        for (int i = l; i < dim; i += 32) val = fmaf(a[i], b[i], val);
+        v[l] = val;
+    }
+    for (int off = 16; off >= 1; off >>= 1)
+        for (int l = 0; l < off; ++l) v[l] = v[l] + v[l + off];
+    return -v[0];
+}
+
+/* distance.hpp:14-29: the scalar loops the reference's Makefile compiles in
+ * (no -march, so neither AVX path is taken); plain multiply then add. */
+float fgo_scalar_l2(int dim, const float *a, const float *b) {
+    float sum = 0.0f;
+    for (int i = 0; i < dim; ++i) {
+        float d = a[i] - b[i];
+        float sq = d * d;
+        sum += sq;
+    }
+    return sum;
+}
+
+float fgo_scalar_ip(int dim, const float *a, const float *b) {
+    float sum = 0.0f;
+    for (int i = 0; i < dim; ++i) {
+        float p = a[i] * b[i];
+        sum += p;
+    }
+    return -sum;
+}
+
+static inline float index_distance(const fgo_index *ix, const float *query, uint32_t node) {
+    const float *row = ix->data + (uint64_t)node * ix->lay.row_offset;
+    return ix->use_ip ? fgo_warp_ip((int)ix->lay.dim, query, row)
+                      : fgo_warp_l2((int)ix->lay.dim, query, row);
+}
+
+/* ---------------------------------------------------------------- networks */
+
+/* utils.cuh:309-328: swap only if the keys differ and are out of order. */
+static inline void cex(float *k, uint32_t *v, uint32_t lo, uint32_t hi, int asc) {
+    if (k[lo] != k[hi] && ((k[lo] < k[hi]) != asc)) {
+        float tk = k[lo]; k[lo] = k[hi]; k[hi] = tk;
+        uint32_t tv = v[lo]; v[lo] = v[hi]; v[hi] = tv;
+    }
+}
+
+/* One stage (block size kk) of the bitonic network.  utils.cuh:330-414 with N
+ * items per lane in the blocked layout (position = N*lane + i): warp_merge at
+ * range r is exactly this stage with kk = N*r (kk = 2..N for range 1), all
+ * compare-exchanges at distance j = kk/2 .. 1, ascending iff (pos & kk) == 0
+ * at the lower position. */
+void fgo_bitonic_stage(float *keys, uint32_t *vals, uint32_t n, uint32_t kk) {
+    for (uint32_t j = kk >> 1; j >= 1; j >>= 1)
+        for (uint32_t lo = 0; lo < n; ++lo) {
+            const uint32_t hi = lo ^ j;
+            if (hi <= lo || hi >= n) continue;
+            cex(keys, vals, lo, hi, (lo & kk) == 0);
+        }
+}
+
+/* utils.cuh:409-414 (warp_sort: ranges 1..32 = stages 2..n). */
+void fgo_bitonic_sort(float *keys, uint32_t *vals, uint32_t n) {
+    for (uint32_t kk = 2; kk <= n; kk <<= 1) fgo_bitonic_stage(keys, vals, n, kk);
+}
+
+/* utils.cuh:417-457 candidate_by_bitonic_sort<1,0>: one warp, positions =
+ * lanes, entries past the buffer padded with (FLT_MAX, MAX_INDEX). */
+static void candidate_sort32(float *cd, uint32_t *ci, uint32_t cbs) {
+    float k[32];
+    uint32_t v[32];
+    for (uint32_t l = 0; l < 32; ++l) {
+        k[l] = l < cbs ? cd[l] : FLT_MAX;
+        v[l] = l < cbs ? ci[l] : FGO_MAX_INDEX;
+    }
+    fgo_bitonic_sort(k, v, 32);
+    for (uint32_t l = 0; l < cbs && l < 32; ++l) {
+        cd[l] = k[l];
+        ci[l] = v[l];
+    }
+}
+
+/* utils.cuh:588-616 */
+int fgo_merge_path_partition(const float *a, int na, const float *b, int nb, int diag) {
+    int low = diag - nb > 0 ? diag - nb : 0;
+    int high = diag < na ? diag : na;
+    while (low <= high) {
+        const int ai = (low + high) >> 1;
+        const int bi = diag - ai;
+        const float al = ai > 0 ? a[ai - 1] : -FLT_MAX;
+        const float ar = ai < na ? a[ai] : FLT_MAX;
+        const float bl = bi > 0 ? b[bi - 1] : -FLT_MAX;
+        const float br = bi < nb ? b[bi] : FLT_MAX;
+        if (al > br) high = ai - 1;
+        else if (bl > ar) low = ai + 1;
+        else return ai;
+    }
+    return low;
+}
+
+/* Beam merge, dispatched as utils.cuh:1369-1399 does for a 32-entry (or
+ * smaller) candidate buffer:
+ *  - pbeam <= 128 (always a power of two >= 32): topk_small_by_bitonic_sort
+ *    <1, pbeam/32> (utils.cuh:490-586);
+ *  - pbeam > 128: topk_candidate_sort_and_merge (utils.cuh:618-680), with the
+ *    reference's 256-thread block fixing the merge-path segmentation. */
+void fgo_merge_candidates(float *beam_d, uint32_t *beam_i, float *cand_d, uint32_t *cand_i,
+                          uint32_t cbs, uint32_t pbeam, int first, float *scratch_d,
+                          uint32_t *scratch_i) {
+    if (pbeam <= 128) {
+        const uint32_t n2 = pbeam / 32;
+        float k1[32];
+        uint32_t v1[32];
+        for (uint32_t l = 0; l < 32; ++l) {
+            k1[l] = l < cbs ? cand_d[l] : FLT_MAX;
+            v1[l] = l < cbs ? cand_i[l] : FGO_MAX_INDEX;
+        }
+        fgo_bitonic_sort(k1, v1, 32);
+        for (uint32_t l = 0; l < 32; ++l)
+            if (l < cbs && l < pbeam) {
+                cand_d[l] = k1[l];
+                cand_i[l] = v1[l];
+            }
+        float k2[128];
+        uint32_t v2[128];
+        if (first) {
+            /* strided load (element lane + 32*i lands at position n2*lane + i) */
+            for (uint32_t l = 0; l < 32; ++l)
+                for (uint32_t i = 0; i < n2; ++i) {
+                    const uint32_t j = l + 32 * i;
+                    k2[n2 * l + i] = j < pbeam ? beam_d[j] : FLT_MAX;
+                    v2[n2 * l + i] = j < pbeam ? beam_i[j] : FGO_MAX_INDEX;
+                }
+            fgo_bitonic_sort(k2, v2, pbeam);
+        } else {
+            for (uint32_t p = 0; p < pbeam; ++p) {
+                k2[p] = beam_d[p];
+                v2[p] = beam_i[p];
+            }
+        }
+        for (uint32_t p = 0; p < pbeam; ++p) {
+            const uint32_t k = pbeam - 1 - p;
+            if (k >= pbeam || k >= cbs) continue;
+            if (k2[p] > cand_d[k]) {
+                k2[p] = cand_d[k];
+                v2[p] = cand_i[k];
+            }
+        }
+        fgo_bitonic_stage(k2, v2, pbeam, pbeam);
+        for (uint32_t p = 0; p < pbeam; ++p) {
+            beam_d[p] = k2[p];
+            beam_i[p] = v2[p];
+        }
+        return;
+    }
+    candidate_sort32(cand_d, cand_i, cbs);
+    int active = (int)((pbeam + 3) / 4);
+    active = ((active + 31) / 32) * 32;
+    if (active > 256) active = 256;
+    for (int t = 0; t < active; ++t) {
+        const uint32_t ob = umin32(pbeam, ((uint32_t)t * pbeam) / (uint32_t)active);
+        const uint32_t oe = umin32(pbeam, ((uint32_t)(t + 1) * pbeam) / (uint32_t)active);
+        const int out_begin = (int)ob, out_end = (int)oe;
+        const int top_begin = fgo_merge_path_partition(beam_d, (int)pbeam, cand_d, (int)cbs, out_begin);
+        const int top_end = fgo_merge_path_partition(beam_d, (int)pbeam, cand_d, (int)cbs, out_end);
+        int ti = top_begin, ci = out_begin - top_begin;
+        const int cand_end = out_end - top_end;
+        for (int o = out_begin; o < out_end; ++o) {
+            const int take_top = (ci >= cand_end) || (ti < top_end && beam_d[ti] <= cand_d[ci]);
+            if (take_top) {
+                scratch_d[o] = beam_d[ti];
+                scratch_i[o] = beam_i[ti];
+                ++ti;
+            } else {
+                scratch_d[o] = cand_d[ci];
+                scratch_i[o] = cand_i[ci];
+                ++ci;
+            }
+        }
+    }
+    memcpy(beam_d, scratch_d, pbeam * sizeof(float));
+    memcpy(beam_i, scratch_i, pbeam * sizeof(uint32_t));
+}
+
+/* -------------------------------------------------------------------- hash */
+
+/* utils.cuh:697-716: open addressing, slot = (k ^ (k >> bitlen)) & mask,
+ * linear probing, empty = 0xFFFFFFFF; returns 1 iff newly inserted. */
+uint32_t fgo_hash_insert(uint32_t *table, unsigned bitlen, uint32_t key) {
+    const uint32_t size = 1u << bitlen, mask = size - 1;
+    uint32_t idx = (key ^ (key >> bitlen)) & mask;
+    for (uint32_t i = 0; i < size; ++i) {
+        const uint32_t old = table[idx];
+        if (old == 0xFFFFFFFFu) {
+            table[idx] = key;
+            return 1;
+        }
+        if (old == key) return 0;
+        idx = (idx + 1) & mask;
+    }
+    return 0;
+}
+
+/* utils.cuh:718-735 */
+uint32_t fgo_hash_contains(const uint32_t *table, unsigned bitlen, uint32_t key) {
+    const uint32_t size = 1u << bitlen, mask = size - 1;
+    uint32_t idx = (key ^ (key >> bitlen)) & mask;
+    for (uint32_t i = 0; i < size; ++i) {
+        const uint32_t old = table[idx];
+        if (old == key) return 1;
+        if (old == 0xFFFFFFFFu) return 0;
+        idx = (idx + 1) & mask;
+    }
+    return 0;
+}
+
+/* utils.cuh:752-787: warp 0 scans the beam in 32-entry chunks and takes the
+ * first n entries whose MSB ("expanded") is clear, marking them.  MAX_INDEX
+ * slots carry the MSB and are never picked. */
+uint32_t fgo_pick_expanders(int n, uint32_t *out, int m, uint32_t *beam_idx) {
+    uint32_t num = 0;
+    uint32_t itopk_max = (uint32_t)m;
+    if (itopk_max % 32) itopk_max += 32 - (itopk_max % 32);
+    for (uint32_t base = 0; base < itopk_max; base += 32) {
+        uint32_t ballot = 0;
+        for (uint32_t l = 0; l < 32; ++l) {
+            const uint32_t j = base + l;
+            if (j < (uint32_t)m && (beam_idx[j] & FGO_MSB) == 0) ballot |= 1u << l;
+        }
+        for (uint32_t l = 0; l < 32; ++l) {
+            if (!(ballot & (1u << l))) continue;
+            const uint32_t i = (uint32_t)__builtin_popcount(ballot & ((1u << l) - 1u)) + num;
+            if (i < (uint32_t)n) {
+                out[i] = base + l;
+                beam_idx[base + l] |= FGO_MSB;
+            }
+        }
+        num += (uint32_t)__builtin_popcount(ballot);
+        if (num > (uint32_t)n) num = (uint32_t)n;
+        if (num >= (uint32_t)n) break;
+    }
+    return num;
+}
+
+/* utils.cuh:251-267: a lane is kept iff it is valid and fewer than keep_k
+ * valid lanes precede it in (value, lane) order. */
+int fgo_warp_keep_topk(const float *values, const int *valid, int keep_k, int *keep_out) {
+    int kept = 0;
+    for (int l = 0; l < 32; ++l) {
+        const float mine = valid[l] ? values[l] : FLT_MAX;
+        int rank = 0;
+        for (int s = 0; s < 32; ++s) {
+            const float other = valid[s] ? values[s] : FLT_MAX;
+            if (valid[s] && (other < mine || (other == mine && s < l))) rank++;
+        }
+        keep_out[l] = valid[l] && keep_k > 0 && rank < keep_k;
+        kept += keep_out[l];
+    }
+    return kept;
+}
+
+/* -------------------------------------------------------------- controller */
+
+/* adaptive_search_utils.cuh:8-18 */
+typedef struct {
+    int spec_degree;
+    float rho;
+    int policy_iters;
+    uint32_t top1_node;
+    int top1_stall_iters;
+    int warmup_done;
+    float entry_distance;
+    float last_expander_distance;
+    float current_expander_distance;
+} ctl_state;
+
+static inline int finite_below_max(float x) { return isfinite(x) && x < FLT_MAX; }
+
+/* adaptive_search_utils.cuh:51-72 */
+static float expander_progress(const ctl_state *prev, float *last, float *cur) {
+    const float entry = prev->entry_distance;
+    *last = finite_below_max(prev->last_expander_distance) ? prev->last_expander_distance : entry;
+    *cur = finite_below_max(prev->current_expander_distance) ? prev->current_expander_distance : *last;
+    const float denom = fabsf(entry);
+    if (!isfinite(*last) || !isfinite(*cur) || !isfinite(entry) || denom <= 1.0e-20f) return 0.0f;
+    const float progress = (*last - *cur) / denom;
+    if (!isfinite(progress) || progress <= 0.0f) return 0.0f;
+    return progress < 1.0f ? progress : 1.0f;
+}
+
+/* adaptive_search.cuh:166-190 with adaptive_search_utils.cuh:32-39, 74-119
+ * (CHECK_INTERVAL = 1, so every non-stage-II iteration re-tunes rho). */
+static void controller_step(ctl_state *st, uint32_t beam0, float phase2_rho) {
+    const uint32_t cur_top1 = beam0 & 0x7fffffffu;
+    const int stall = (st->policy_iters > 0 && cur_top1 == st->top1_node) ? st->top1_stall_iters + 1 : 0;
+    const int phase_changed = st->warmup_done || stall >= 4;
+    float last, cur;
+    const float rate = expander_progress(st, &last, &cur);
+    st->top1_node = cur_top1;
+    st->top1_stall_iters = stall;
+    st->last_expander_distance = last;
+    st->current_expander_distance = cur;
+    if (phase_changed) {
+        st->warmup_done = 1;
+        st->spec_degree = FGO_SEARCH_WIDTH;
+        st->rho = phase2_rho;
+    } else {
+        const float span = phase2_rho > 0.25f ? phase2_rho - 0.25f : 0.99f - 0.0f;
+        const float base = st->policy_iters == 0 ? 0.25f : st->rho;
+        const float cap = phase2_rho > 0.25f ? phase2_rho : 0.99f;
+        st->warmup_done = 0;
+        st->spec_degree = 1;
+        st->rho = clamp_float(fmaf(span, rate, base), 0.0f, cap);
+    }
+    st->policy_iters += 1;
+}
+
+/* ------------------------------------------------------------------ search */
+
+typedef struct {
+    float beam_d[FGO_MAX_BEAM];
+    uint32_t beam_i[FGO_MAX_BEAM];
+    float scratch_d[FGO_MAX_BEAM];
+    uint32_t scratch_i[FGO_MAX_BEAM];
+    float cand_d[32];
+    uint32_t cand_i[32];
+    uint32_t hash[1u << 12];
+    fgo_query_factors qf;
+} search_ws;
+
+static void hash_reset(uint32_t *t, unsigned bitlen) {
+    memset(t, 0xff, (size_t)(1u << bitlen) * sizeof(uint32_t));
+}
+
+static int validate(const fgo_index *ix, int K, int beam) {
+    if (!ix || !ix->data || !ix->signs) return -1;
+    if (K < 1 || beam < 1 || beam > FGO_MAX_BEAM) return -2;
+    if (ix->lay.degree < 1 || ix->lay.degree > FGO_MAX_DEGREE) return -3;
+    if (ix->lay.padded_dim < 64 || ix->lay.padded_dim > FGO_MAX_PADDED_DIM) return -4;
+    if (ix->entry >= ix->npoints) return -5;
+    return 0;
+}
+
+/* src/adaptive_search.cuh:5-466 for one query (one thread block). */
+static int search_one_ws(const fgo_index *ix, const float *query, int K, int beam_sz,
+                         uint32_t *out, fgo_counters *cnt, fgo_trace_rec *trace,
+                         uint32_t trace_cap, uint32_t *trace_len, search_ws *ws) {
+    int rc = validate(ix, K, beam_sz);
+    if (rc) return rc;
+    const fgo_layout *L = &ix->lay;
+    const int dim = (int)L->dim, B = (int)L->padded_dim;
+    const uint32_t deg = L->degree;
+    const uint32_t pbeam = fgo_effective_sort_beam_size((uint32_t)beam_sz);
+    const uint32_t cbs = fgo_round_up_pow2(fgo_candidate_buffer_capacity(deg));
+    const uint32_t collect_cap = umin32(FGO_BUFFER_BOUND, cbs);
+    const unsigned bitlen = fgo_hash_bitlen(pbeam, cbs, FGO_HASH_RESET);
+    const int max_iter = (beam_sz * 11 + 9) / 10;               /* gpu_search_adaptive.cu:96 */
+    const float phase2_rho = fgo_max_rho_bound(deg);            /* gpu_search_adaptive.cu:28 */
+    const int bytes_per_nbr = B >> 3;
+    fgo_counters c = {0, 0, 0, 0, 0, 0xFFFFFFFFu};
+    uint32_t tl = 0;
+    if (bitlen > 12) return -6;
+
+    uint32_t *hash = ws->hash;
+    float *bd = ws->beam_d, *cd = ws->cand_d;
+    uint32_t *bi = ws->beam_i, *ci = ws->cand_i;
+    uint32_t plist[FGO_SEARCH_WIDTH], pnode[FGO_SEARCH_WIDTH];
+    float pdist[FGO_SEARCH_WIDTH];
+
+    ctl_state st = {1, 0.25f, 0, FGO_MAX_INDEX, 0, 0, FLT_MAX, FLT_MAX, FLT_MAX};
+    hash_reset(hash, bitlen);
+    for (uint32_t i = 0; i < pbeam; ++i) { bd[i] = FLT_MAX; bi[i] = FGO_MAX_INDEX; }
+    for (uint32_t i = 0; i < cbs; ++i) { cd[i] = FLT_MAX; ci[i] = FGO_MAX_INDEX; }
+
+    /* adaptive_search.cuh:109-119 */
+    const float entry_dist = index_distance(ix, query, ix->entry);
+    c.exact++;
+    ci[0] = ix->entry;
+    cd[0] = entry_dist;
+    st.entry_distance = entry_dist;
+    fgo_hash_insert(hash, bitlen, ix->entry);
+
+    fgo_query_prepare(query, ix->signs, dim, B, &ws->qf);          /* :121-123 */
+    const fgo_query_factors *qf = &ws->qf;
+
+    for (int iter = 0; iter < FGO_MAX_ITERATIONS; ++iter) {
+        if ((iter + 1) % FGO_HASH_RESET == 0) {                       /* :128-134 */
+            hash_reset(hash, bitlen);
+            for (int i = 0; i < beam_sz; ++i) fgo_hash_insert(hash, bitlen, bi[i] & ~FGO_MSB);
+        }
+        if (iter >= max_iter) break;                                  /* :136-138 */
+
+        fgo_merge_candidates(bd, bi, cd, ci, cbs, pbeam, iter == 0, ws->scratch_d, ws->scratch_i);
+        for (uint32_t i = (uint32_t)beam_sz; i < pbeam; ++i) { bd[i] = FLT_MAX; bi[i] = FGO_MAX_INDEX; }
+        for (uint32_t i = 0; i < cbs; ++i) { cd[i] = FLT_MAX; ci[i] = FGO_MAX_INDEX; }
+        for (int i = 0; i < FGO_SEARCH_WIDTH; ++i) { pnode[i] = FGO_MAX_INDEX; pdist[i] = FLT_MAX; }
+        uint32_t compact_count = 0;
+        /* adaptive_search_utils.cuh:25-30 */
+        float kth_cutoff = FLT_MAX;
+        if (bi[beam_sz - 1] != FGO_MAX_INDEX)
+            kth_cutoff = bd[(K < beam_sz ? K : beam_sz) - 1];
+
+        controller_step(&st, bi[0], phase2_rho);                     /* :166-191 */
+
+        const uint32_t nexp = fgo_pick_expanders(st.spec_degree, plist, beam_sz, bi);  /* :193-197 */
+        if (!nexp) break;
+        c.iterations++;
+        c.expansions += nexp;
+        for (uint32_t p = 0; p < nexp; ++p) {                         /* :203-212 */
+            pnode[p] = bi[plist[p]] & 0x7fffffffu;
+            pdist[p] = bd[plist[p]];
+        }
+        /* adaptive_search_utils.cuh:41-49 */
+        st.last_expander_distance = finite_below_max(st.current_expander_distance)
+                                        ? st.current_expander_distance : st.entry_distance;
+        st.current_expander_distance = pdist[nexp - 1];
+
+        fgo_trace_rec *tr = (trace && tl < trace_cap) ? &trace[tl] : NULL;
+        if (tr) {
+            memset(tr, 0, sizeof(*tr));
+            tr->iter = (uint32_t)iter;
+            tr->theta = (uint32_t)st.spec_degree;
+            tr->rho = st.rho;
+            tr->n_parents = nexp;
+            for (uint32_t p = 0; p < nexp; ++p) tr->parents[p] = pnode[p];
+            tr->top1 = bi[0];
+            tr->top1_dist = bd[0];
+            tr->kth_cutoff = kth_cutoff;
+        }
+
+        const int kth_valid = finite_below_max(kth_cutoff);
+        if (st.spec_degree <= 1) {
+            /* single-expander path, adaptive_search.cuh:221-343 */
+            const uint32_t cwc = umin32(deg, cbs);
+            const uint32_t parent = pnode[0];
+            const float *prow = ix->data + (uint64_t)parent * L->row_offset;
+            const uint32_t *nbrs = (const uint32_t *)(prow + L->neighbor_offset);
+            c.ids_read += cwc;
+            for (uint32_t i = 0; i < cbs; ++i) {
+                uint32_t child = FGO_MAX_INDEX;
+                if (i < cwc) {
+                    child = nbrs[i];
+                    if (child >= ix->npoints || fgo_hash_contains(hash, bitlen, child)) child = FGO_MAX_INDEX;
+                }
+                ci[i] = child;
+                cd[i] = child == FGO_MAX_INDEX ? FLT_MAX : 0.0f;
+            }
+            const int keep = fgo_keep_count_for_expander(cwc, st.spec_degree, st.rho, 0, 0);
+            uint32_t valid = 0;
+            for (uint32_t i = 0; i < cwc; ++i) valid += (ci[i] != FGO_MAX_INDEX && cd[i] < FLT_MAX);
+            const int keep_all = keep >= (int)valid;
+            int eff = keep;
+            if (!keep_all) {
+                const float *factors = prow + L->factor_offset;
+                const uint8_t *codes = (const uint8_t *)(prow + L->code_offset);
+                for (uint32_t i = 0; i < cwc; ++i) {
+                    if (ci[i] == FGO_MAX_INDEX) continue;
+                    const float est = fgo_estimate_lanes(qf, codes + (size_t)i * bytes_per_nbr, factors[i],
+                                                         factors[deg + i], factors[2 * deg + i], pdist[0], B);
+                    c.estimates++;
+                    const int fin = isfinite(est);
+                    cd[i] = fin ? est : FLT_MAX;
+                    if (!fin) ci[i] = FGO_MAX_INDEX;
+                }
+                uint32_t near = 0;
+                if (kth_valid)
+                    for (uint32_t i = 0; i < cwc; ++i)
+                        near += (ci[i] != FGO_MAX_INDEX && isfinite(cd[i]) && cd[i] <= kth_cutoff);
+                eff = fgo_keep_count_for_expander(cwc, st.spec_degree, st.rho, kth_valid, near);
+                candidate_sort32(cd, ci, cbs);
+                for (uint32_t i = 0; i < cbs; ++i)
+                    if ((int)i >= eff) { ci[i] = FGO_MAX_INDEX; cd[i] = FLT_MAX; }
+            }
+            const int admit = keep_all ? (int)cwc : eff;
+            for (int i = 0; i < admit; ++i) {
+                const uint32_t child = ci[i];
+                uint32_t ins = 0;
+                if (child != FGO_MAX_INDEX && cd[i] < FLT_MAX) ins = fgo_hash_insert(hash, bitlen, child);
+                if (!ins) { ci[i] = FGO_MAX_INDEX; cd[i] = FLT_MAX; continue; }
+                cd[i] = index_distance(ix, query, child);
+                c.exact++;
+            }
+        } else {
+            /* speculative multi-expander path, adaptive_search.cuh:344-444 */
+            if (c.stage2_iter == 0xFFFFFFFFu) c.stage2_iter = (uint32_t)iter;
+            const int tiles = (int)((deg + 31) / 32);
+            const int tasks = (int)nexp * tiles;
+            for (int base = 0; base < tasks; base += FGO_SEARCH_WIDTH) {
+                uint32_t child[FGO_SEARCH_WIDTH][32];
+                int keepl[FGO_SEARCH_WIDTH][32];
+                for (int w = 0; w < FGO_SEARCH_WIDTH; ++w) {
+                    const int task = base + w;
+                    const int active = task < tasks;
+                    const uint32_t pidx = active ? (uint32_t)(task / tiles) : 0u;
+                    const int tile = active ? task - (int)pidx * tiles : 0;
+                    const uint32_t parent = pnode[pidx];
+                    float est[32], tx[32], fdq[32], fvq[32];
+                    int valid[32];
+                    const float *prow = NULL;
+                    uint32_t raw_valid = 0;
+                    for (int l = 0; l < 32; ++l) {
+                        const uint32_t nidx = (uint32_t)(tile * 32 + l);
+                        child[w][l] = FGO_MAX_INDEX;
+                        tx[l] = FLT_MAX; fdq[l] = 0.0f; fvq[l] = 0.0f;
+                        valid[l] = 0;
+                        est[l] = FLT_MAX;
+                        if (active && nidx < deg) {
+                            prow = ix->data + (uint64_t)parent * L->row_offset;
+                            const uint32_t *nbrs = (const uint32_t *)(prow + L->neighbor_offset);
+                            const float *factors = prow + L->factor_offset;
+                            child[w][l] = nbrs[nidx];
+                            c.ids_read++;
+                            valid[l] = child[w][l] != FGO_MAX_INDEX && child[w][l] < ix->npoints &&
+                                       !fgo_hash_contains(hash, bitlen, child[w][l]);
+                            if (valid[l]) {
+                                tx[l] = factors[nidx];
+                                fdq[l] = factors[deg + nidx];
+                                fvq[l] = factors[2 * deg + nidx];
+                            }
+                        }
+                        raw_valid += (uint32_t)valid[l];
+                    }
+                    uint32_t an = active ? deg - (uint32_t)tile * 32u : 0u;
+                    if (an > 32) an = 32;
+                    const int keep = active ? fgo_keep_count_for_expander(an, st.spec_degree, st.rho, 0, 0) : 0;
+                    const int keep_all = keep >= (int)raw_valid;
+                    if (!keep_all) {
+                        const uint8_t *codes = (const uint8_t *)(prow + L->code_offset);
+                        for (int l = 0; l < 32; ++l) {
+                            if (!valid[l]) continue;
+                            const uint32_t nidx = (uint32_t)(tile * 32 + l);
+                            est[l] = fgo_estimate_seq(qf, codes + (size_t)nidx * bytes_per_nbr, tx[l], fdq[l],
+                                                      fvq[l], pdist[pidx], B);
+                            c.estimates++;
+                            valid[l] = isfinite(est[l]);
+                        }
+                    }
+                    int eff = keep;
+                    if (!keep_all) {
+                        uint32_t near = 0;
+                        for (int l = 0; l < 32; ++l) near += (valid[l] && kth_valid && est[l] <= kth_cutoff);
+                        eff = fgo_keep_count_for_expander(an, st.spec_degree, st.rho, kth_valid, near);
+                    }
+                    if (keep_all) {
+                        for (int l = 0; l < 32; ++l) keepl[w][l] = valid[l];
+                    } else {
+                        fgo_warp_keep_topk(est, valid, eff, keepl[w]);
+                    }
+                }
+                /* inserts and compaction in (task, lane) order (allocate_warp_compact_slots,
+                 * utils.cuh:187-214; adaptive_search.cuh:405-424) */
+                for (int w = 0; w < FGO_SEARCH_WIDTH; ++w)
+                    for (int l = 0; l < 32; ++l) {
+                        if (!keepl[w][l]) continue;
+                        if (!fgo_hash_insert(hash, bitlen, child[w][l])) continue;
+                        const uint32_t slot = compact_count++;
+                        if (slot < collect_cap) {
+                            ci[slot] = child[w][l];
+                            cd[slot] = FLT_MAX;
+                        }
+                    }
+            }
+            if (compact_count > collect_cap) compact_count = collect_cap;   /* :428-430 */
+            for (uint32_t i = 0; i < compact_count; ++i) {                  /* :433-442 */
+                cd[i] = index_distance(ix, query, ci[i]);
+                c.exact++;
+            }
+        }
+        if (tr) {
+            tr->n_cand = cbs;
+            for (uint32_t i = 0; i < cbs && i < 32; ++i) { tr->cand_idx[i] = ci[i]; tr->cand_dist[i] = cd[i]; }
+            tl++;
+        }
+    }
+
+    fgo_merge_candidates(bd, bi, cd, ci, cbs, pbeam, 0, ws->scratch_d, ws->scratch_i);  /* :449-451 */
+    /* adaptive_search.cuh:455-464 */
+    uint32_t last = 0;
+    for (int i = 0; i < K; ++i) {
+        const uint32_t r = i < beam_sz ? (bi[i] & 0x7fffffffu) : FGO_MAX_INDEX;
+        if (r != FGO_MAX_INDEX) last = r;
+        out[i] = r == FGO_MAX_INDEX ? last : r;
+    }
+    if (cnt) *cnt = c;
+    if (trace_len) *trace_len = tl;
+    return 0;
+}
+
+int fgo_search_one(const fgo_index *ix, const float *query, int K, int beam, uint32_t *out,
+                   fgo_counters *cnt, fgo_trace_rec *trace, uint32_t trace_cap,
+                   uint32_t *trace_len) {
+    search_ws *ws = (search_ws *)malloc(sizeof(search_ws));
+    if (!ws) return -10;
+    int rc = search_one_ws(ix, query, K, beam, out, cnt, trace, trace_cap, trace_len, ws);
+    free(ws);
+    return rc;
+}
+
+typedef struct {
+    const fgo_index *ix;
+    const float *queries;
+    uint64_t nq;
+    int K, beam;
+    uint32_t *out;
+    fgo_counters *cnt;
+    atomic_ullong next;
+    atomic_int err;
+} batch_job;
+
+static void *batch_worker(void *arg) {
+    batch_job *job = (batch_job *)arg;
+    search_ws *ws = (search_ws *)malloc(sizeof(search_ws));
+    if (!ws) { atomic_store(&job->err, -10); return NULL; }
+    for (;;) {
+        const unsigned long long q = atomic_fetch_add(&job->next, 1ull);
+        if (q >= job->nq) break;
+        int rc = search_one_ws(job->ix, job->queries + q * job->ix->lay.dim, job->K, job->beam,
+                               job->out + q * (uint64_t)job->K, job->cnt ? &job->cnt[q] : NULL,
+                               NULL, 0, NULL, ws);
+        if (rc) atomic_store(&job->err, rc);
+    }
+    free(ws);
+    return NULL;
+}
+
+/* One query per task over nthreads host threads (the CPU baseline). */
+int fgo_search_batch(const fgo_index *ix, const float *queries, uint64_t nq, int K, int beam,
+                     uint32_t *out, fgo_counters *cnt, int nthreads) {
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > 256) nthreads = 256;
+    batch_job job;
+    job.ix = ix; job.queries = queries; job.nq = nq; job.K = K; job.beam = beam;
+    job.out = out; job.cnt = cnt;
+    atomic_init(&job.next, 0ull);
+    atomic_init(&job.err, 0);
+    pthread_t th[256];
+    int started = 0;
+    for (int t = 0; t < nthreads; ++t)
+        if (pthread_create(&th[t], NULL, batch_worker, &job) == 0) started++;
+        else break;
+    if (started == 0) batch_worker(&job);
+    for (int t = 0; t < started; ++t) pthread_join(th[t], NULL);
+    return atomic_load(&job.err);
+}
+
+/* common.hpp:26-47: float centroid accumulated in row order as row*(1/N), then
+ * argmin of the metric's scalar distance (distance.hpp:133-154). */
+uint32_t fgo_entry_point(const float *data, uint64_t npoints, uint32_t dim, uint64_t row_offset,
+                         int use_ip) {
+    float *centroid = (float *)calloc(dim, sizeof(float));
+    if (!centroid) return FGO_MAX_INDEX;
+    const float inv = 1.0f / (float)npoints;
+    for (uint64_t i = 0; i < npoints; ++i) {
+        const float *row = data + i * row_offset;
+        for (uint32_t d = 0; d < dim; ++d) {
+            float t = row[d] * inv;
+            centroid[d] += t;
+        }
+    }
+    uint32_t best = 0;
+    float best_dist = FLT_MAX;
+    for (uint64_t i = 0; i < npoints; ++i) {
+        const float *row = data + i * row_offset;
+        const float dd = use_ip ? fgo_scalar_ip((int)dim, row, centroid) : fgo_scalar_l2((int)dim, row, centroid);
+        if (dd < best_dist) { best_dist = dd; best = (uint32_t)i; }
+    }
+    free(centroid);
+    return best;
+}
+
+/* common.hpp:49-66: duplicates in a prediction row count separately. */
+float fgo_recall(const uint32_t *pred, const int32_t *gt, uint64_t nq, int topk, int gt_k) {
+    size_t correct = 0;
+    const int eval_k = topk < gt_k ? topk : gt_k;
+    for (uint64_t i = 0; i < nq; ++i)
+        for (int j = 0; j < topk; ++j) {
+            const int p = (int)pred[i * (uint64_t)topk + j];
+            for (int k = 0; k < eval_k; ++k)
+                if (p == gt[i * (uint64_t)gt_k + k]) { ++correct; break; }
+        }
+    return (float)correct / (float)(nq * (uint64_t)topk);
+}

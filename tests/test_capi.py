@@ -1,0 +1,48 @@
+"""The C-ABI library loads and exports every symbol include/flashgann.h
+declares; argument checks fail before any device call."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    text = open(os.path.join(ROOT, "include", "flashgann.h")).read()
+    return sorted(set(re.findall(r"^\w[\w\s\*]*?\b(fg_\w+)\s*\(", text, re.M)))
+
+
+def test_header_symbols_exported():
+    from flashgann_amd import _lib
+    L = C.CDLL(_lib.LIB_PATH)
+    syms = declared_symbols()
+    assert len(syms) >= 10, syms
+    for s in syms:
+        assert hasattr(L, s), f"{s} declared in include/flashgann.h but not exported"
+    assert set(syms) == set(_lib.EXPORTED)
+
+
+def test_shape_checks_before_device_use():
+    from flashgann_amd import _lib
+    L = _lib.lib()
+    rows = np.zeros((4, 400), dtype=np.float32)
+    signs = np.ones(32, dtype=np.float32)
+    h = C.c_void_p()
+    rc = L.fg_index_create(rows.ctypes.data_as(C.POINTER(C.c_float)), 4, 16, 4,
+                           signs.ctypes.data_as(C.POINTER(C.c_float)), 0, 0, C.byref(h))
+    assert rc == _lib.FG_EINVAL
+    assert b"dim" in L.fg_last_error()
+    rc = L.fg_index_create(rows.ctypes.data_as(C.POINTER(C.c_float)), 4, 128, 65,
+                           signs.ctypes.data_as(C.POINTER(C.c_float)), 0, 0, C.byref(h))
+    assert rc == _lib.FG_EINVAL and b"degree" in L.fg_last_error()
+
+
+def test_lds_bytes_host_only():
+    from flashgann_amd import lds_bytes
+    small = lds_bytes(128, 128, 32)
+    big = lds_bytes(128, 1024, 32)
+    assert 4096 < small < big < 64 * 1024

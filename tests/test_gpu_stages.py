@@ -1,0 +1,63 @@
+"""Stage-level parity: query preparation, RaBitQ estimates and exact
+distances from the HIP kernels against the oracle, bit for bit."""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from conftest import small_index
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("kind,dim", [("int", 128), ("unit", 96), ("box", 960)])
+def test_query_prepare_matches_oracle(gpu_available, kind, dim):
+    from flashgann_amd import Index
+    from oracle import oracle as O
+    cb, q, _ = small_index(n=1500, nq=8, dim=dim, comps=8, kind=kind)
+    ix = Index.from_codebook(cb)
+    rot, qt, lhw, sq = ix.query_prepare(q)
+    B = cb.layout.padded_dim
+    for i in range(q.shape[0]):
+        qf = O.query_prepare(q[i], cb.signs, dim, B)
+        assert np.array_equal(rot[i], np.ctypeslib.as_array(qf.rotated)[:B])
+        assert np.array_equal(qt[i], np.ctypeslib.as_array(qf.q)[:B])
+        assert (lhw[i, 0], lhw[i, 1], lhw[i, 2]) == (np.float32(qf.low), np.float32(qf.high), np.float32(qf.width))
+        assert sq[i] == qf.sum_q
+    ix.close()
+
+
+@pytest.mark.parametrize("kind,dim", [("int", 128), ("unit", 96), ("box", 960)])
+def test_scores_match_oracle(gpu_available, kind, dim):
+    from flashgann_amd import Index
+    from oracle import oracle as O
+    cb, q, _ = small_index(n=1500, nq=8, dim=dim, comps=8, kind=kind)
+    ix = Index.from_codebook(cb)
+    rng = np.random.default_rng(5)
+    n = 300
+    qi = rng.integers(0, q.shape[0], n).astype(np.uint32)
+    pa = rng.integers(0, cb.npoints, n).astype(np.uint32)
+    sl = rng.integers(0, cb.layout.degree, n).astype(np.uint32)
+    el, es, ex = ix.score_edges(q, qi, pa, sl)
+    lay = cb.layout
+    L = O.lib()
+    codes = cb.codes()
+    fac = cb.factors()
+    nb = cb.neighbors()
+    for t in range(n):
+        qf = O.query_prepare(q[qi[t]], cb.signs, dim, lay.padded_dim)
+        prow = cb.rows[pa[t]]
+        pd = L.fgo_warp_l2(dim, O.ptr(np.ascontiguousarray(q[qi[t]]), C.c_float), O.ptr(np.ascontiguousarray(prow[:dim]), C.c_float))
+        code = np.ascontiguousarray(codes[pa[t], sl[t]])
+        tx, fdq, fvq = (float(fac[pa[t], j, sl[t]]) for j in range(3))
+        ref_l = L.fgo_estimate_lanes(C.byref(qf), O.ptr(code, C.c_uint8), tx, fdq, fvq, pd, lay.padded_dim)
+        ref_s = L.fgo_estimate_seq(C.byref(qf), O.ptr(code, C.c_uint8), tx, fdq, fvq, pd, lay.padded_dim)
+        child = int(nb[pa[t], sl[t]])
+        ref_x = L.fgo_warp_l2(dim, O.ptr(np.ascontiguousarray(q[qi[t]]), C.c_float),
+                              O.ptr(np.ascontiguousarray(cb.rows[child, :dim]), C.c_float))
+        assert np.float32(el[t]) == np.float32(ref_l), t
+        assert np.float32(es[t]) == np.float32(ref_s), t
+        assert np.float32(ex[t]) == np.float32(ref_x), t
+    ix.close()

@@ -1,0 +1,270 @@
+"""Pins the oracle's sorting networks and merges.
+
+The oracle states the reference's warp networks (include/utils.cuh:307-414) as
+standard bitonic stages over positions.  Here the reference's own lane-level
+procedure is replayed literally (32 lanes, per-lane shuffle rule, blocked
+layout position = N*lane + i) and compared on inputs with many tied keys, so a
+wrong direction bit, distance or tie rule in the restatement fails."""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+FLT_MAX = np.float32(np.finfo(np.float32).max)
+MAXI = 0xFFFFFFFF
+
+
+def _shfl_swap(k, v, i, off, p):
+    """swap_if_needed (utils.cuh:309-316) on item i of all 32 lanes at once."""
+    nk = [row[:] for row in k]
+    nv = [row[:] for row in v]
+    for lane in range(32):
+        k0, k1 = k[lane][i], k[lane ^ off][i]
+        if k0 != k1 and ((k0 < k1) != p[lane]):
+            nk[lane][i] = k1
+            nv[lane][i] = v[lane ^ off][i]
+    return nk, nv
+
+
+def _reg_swap(k, v, lane, i, j, p):
+    """swap_if_needed (utils.cuh:319-328) between items i < j of one lane."""
+    if k[lane][i] != k[lane][j] and ((k[lane][i] < k[lane][j]) != p):
+        k[lane][i], k[lane][j] = k[lane][j], k[lane][i]
+        v[lane][i], v[lane][j] = v[lane][j], v[lane][i]
+
+
+def ref_warp_merge(k, v, N, rng):
+    """warp_merge_core<N> (utils.cuh:330-402), literally."""
+    if N == 1:
+        if rng == 1:
+            return k, v
+        b = rng
+        c = b // 2
+        while c >= 1:
+            p = [bool(l & b) == bool(l & c) for l in range(32)]
+            k, v = _shfl_swap(k, v, 0, c, p)
+            c //= 2
+        return k, v
+    if N == 2:
+        if rng == 1:
+            for l in range(32):
+                _reg_swap(k, v, l, 0, 1, (l & 1) == 0)
+            return k, v
+        b = rng
+        c = b // 2
+        while c >= 1:
+            p = [bool(l & b) == bool(l & c) for l in range(32)]
+            for i in range(2):
+                k, v = _shfl_swap(k, v, i, c, p)
+            c //= 2
+        for l in range(32):
+            _reg_swap(k, v, l, 0, 1, (l & b) == 0)
+        return k, v
+    if rng == 1:
+        b = 2
+        while b <= N:
+            c = b // 2
+            while c >= 1:
+                for l in range(32):
+                    for i in range(N):
+                        j = i ^ c
+                        if i >= j:
+                            continue
+                        line = i + N * l
+                        _reg_swap(k, v, l, i, j, bool(line & b) == bool(line & c))
+                c //= 2
+            b *= 2
+        return k, v
+    b = rng
+    c = b // 2
+    while c >= 1:
+        p = [bool(l & b) == bool(l & c) for l in range(32)]
+        for i in range(N):
+            k, v = _shfl_swap(k, v, i, c, p)
+        c //= 2
+    c = N // 2
+    while c >= 1:
+        for l in range(32):
+            for i in range(N):
+                j = i ^ c
+                if i >= j:
+                    continue
+                _reg_swap(k, v, l, i, j, (l & b) == 0)
+        c //= 2
+    return k, v
+
+
+def ref_warp_sort(k, v, N):
+    rng = 1
+    while rng <= 32:
+        k, v = ref_warp_merge(k, v, N, rng)
+        rng *= 2
+    return k, v
+
+
+def _blocked(keys, vals, N):
+    k = [[keys[N * l + i] for i in range(N)] for l in range(32)]
+    v = [[vals[N * l + i] for i in range(N)] for l in range(32)]
+    return k, v
+
+
+def _flat(k, v, N):
+    return (np.array([k[l][i] for l in range(32) for i in range(N)], dtype=np.float32),
+            np.array([v[l][i] for l in range(32) for i in range(N)], dtype=np.uint32))
+
+
+def _oracle_sort(keys, vals):
+    k = np.ascontiguousarray(keys, dtype=np.float32).copy()
+    v = np.ascontiguousarray(vals, dtype=np.uint32).copy()
+    O.lib().fgo_bitonic_sort(O.ptr(k, C.c_float), O.ptr(v, C.c_uint32), k.size)
+    return k, v
+
+
+@pytest.mark.parametrize("N", [1, 2, 4, 8])
+@pytest.mark.parametrize("seed", range(6))
+def test_warp_sort_matches_lane_replay(N, seed):
+    rng = np.random.default_rng(100 * N + seed)
+    n = 32 * N
+    keys = rng.integers(0, 6, n).astype(np.float32)       # heavy ties
+    keys[rng.random(n) < 0.2] = FLT_MAX
+    vals = rng.permutation(n).astype(np.uint32)
+    rk, rv = _flat(*ref_warp_sort(*_blocked(list(keys), list(vals), N), N), N)
+    ok, ov = _oracle_sort(keys, vals)
+    assert np.array_equal(rk, ok) and np.array_equal(rv, ov)
+    assert np.all(np.diff(ok) >= 0)
+
+
+@pytest.mark.parametrize("N", [1, 2, 4])
+def test_final_merge_stage_matches_lane_replay(N):
+    rng = np.random.default_rng(7 + N)
+    n = 32 * N
+    for _ in range(5):
+        half = n // 2
+        a = np.sort(rng.integers(0, 8, half)).astype(np.float32)
+        b = np.sort(rng.integers(0, 8, n - half))[::-1].astype(np.float32)
+        keys = np.concatenate([a, b])
+        vals = rng.permutation(n).astype(np.uint32)
+        rk, rv = _flat(*ref_warp_merge(*_blocked(list(keys), list(vals), N), N, 32), N)
+        k = keys.copy()
+        v = vals.copy()
+        O.lib().fgo_bitonic_stage(O.ptr(k, C.c_float), O.ptr(v, C.c_uint32), n, n)
+        assert np.array_equal(rk, k) and np.array_equal(rv, v)
+
+
+def _ref_small_merge(beam_d, beam_i, cand_d, cand_i, cbs, pbeam, first):
+    """topk_small_by_bitonic_sort<1, pbeam/32> (utils.cuh:490-586), literally."""
+    N2 = pbeam // 32
+    k1 = [[float(cand_d[l]) if l < cbs else FLT_MAX] for l in range(32)]
+    v1 = [[int(cand_i[l]) if l < cbs else MAXI] for l in range(32)]
+    k1, v1 = ref_warp_sort(k1, v1, 1)
+    cd, ci = list(cand_d), list(cand_i)
+    for l in range(32):
+        if l < cbs and l < pbeam:
+            cd[l], ci[l] = k1[l][0], v1[l][0]
+    if first:
+        k2 = [[float(beam_d[l + 32 * i]) for i in range(N2)] for l in range(32)]
+        v2 = [[int(beam_i[l + 32 * i]) for i in range(N2)] for l in range(32)]
+        k2, v2 = ref_warp_sort(k2, v2, N2)
+    else:
+        k2 = [[float(beam_d[N2 * l + i]) for i in range(N2)] for l in range(32)]
+        v2 = [[int(beam_i[N2 * l + i]) for i in range(N2)] for l in range(32)]
+    for l in range(32):
+        for i in range(N2):
+            j = N2 * l + i
+            kk = pbeam - 1 - j
+            if kk >= pbeam or kk >= cbs:
+                continue
+            if k2[l][i] > cd[kk]:
+                k2[l][i], v2[l][i] = cd[kk], ci[kk]
+    k2, v2 = ref_warp_merge(k2, v2, N2, 32)
+    return _flat(k2, v2, N2)
+
+
+@pytest.mark.parametrize("pbeam", [32, 64, 128])
+@pytest.mark.parametrize("first", [0, 1])
+@pytest.mark.parametrize("cbs", [32, 16])
+def test_small_merge_matches_lane_replay(pbeam, first, cbs):
+    rng = np.random.default_rng(pbeam + 3 * first + cbs)
+    L = O.lib()
+    for _ in range(4):
+        bd = np.sort(rng.integers(0, 10, pbeam)).astype(np.float32)
+        bd[rng.random(pbeam) < 0.2] = FLT_MAX
+        bd = np.sort(bd)
+        if first:
+            rng.shuffle(bd)
+        bi = rng.permutation(1000)[:pbeam].astype(np.uint32)
+        cd = rng.integers(0, 10, 32).astype(np.float32)
+        ci = (1000 + rng.permutation(100)[:32]).astype(np.uint32)
+        rk, rv = _ref_small_merge(bd, bi, cd, ci, cbs, pbeam, first)
+        b1, b2, c1, c2 = bd.copy(), bi.copy(), cd.copy(), ci.copy()
+        sd = np.zeros(1024, np.float32)
+        si = np.zeros(1024, np.uint32)
+        L.fgo_merge_candidates(O.ptr(b1, C.c_float), O.ptr(b2, C.c_uint32), O.ptr(c1, C.c_float),
+                               O.ptr(c2, C.c_uint32), cbs, pbeam, first, O.ptr(sd, C.c_float),
+                               O.ptr(si, C.c_uint32))
+        assert np.array_equal(b1, rk) and np.array_equal(b2, rv)
+
+
+def test_merge_path_distinct_keys_is_sorted_union():
+    """Distinct keys: the merge-path variant returns the pbeam smallest of
+    beam U candidates in order, for every reference segmentation."""
+    rng = np.random.default_rng(3)
+    L = O.lib()
+    for pbeam in (129, 200, 256, 384, 640, 1000, 1024):
+        allk = rng.permutation(5000).astype(np.float32)
+        bd = np.sort(allk[:pbeam])
+        cd = allk[pbeam : pbeam + 32].copy()
+        bi = np.arange(pbeam, dtype=np.uint32)
+        ci = np.arange(10000, 10032, dtype=np.uint32)
+        ref = np.sort(np.concatenate([bd, cd]))[:pbeam]
+        b1, b2 = bd.copy(), bi.copy()
+        sd = np.zeros(1024, np.float32)
+        si = np.zeros(1024, np.uint32)
+        L.fgo_merge_candidates(O.ptr(b1, C.c_float), O.ptr(b2, C.c_uint32), O.ptr(cd, C.c_float),
+                               O.ptr(ci, C.c_uint32), 32, pbeam, 0, O.ptr(sd, C.c_float),
+                               O.ptr(si, C.c_uint32))
+        assert np.array_equal(b1, ref)
+        key_of = {**{int(i): float(k) for i, k in zip(bi, bd)}, **{int(i): float(k) for i, k in zip(ci, np.sort(cd))}}
+        assert all(key_of[int(i)] == float(k) for i, k in zip(b2, b1))
+
+
+def _ref_partition(a, b, diag):
+    """Brute force: the binary search of utils.cuh:588-616, unrolled."""
+    na, nb = len(a), len(b)
+    low, high = max(0, diag - nb), min(diag, na)
+    while low <= high:
+        ai = (low + high) >> 1
+        bi = diag - ai
+        al = a[ai - 1] if ai > 0 else -FLT_MAX
+        ar = a[ai] if ai < na else FLT_MAX
+        bl = b[bi - 1] if bi > 0 else -FLT_MAX
+        br = b[bi] if bi < nb else FLT_MAX
+        if al > br:
+            high = ai - 1
+        elif bl > ar:
+            low = ai + 1
+        else:
+            return ai
+    return low
+
+
+def test_merge_path_partition_valid_split():
+    rng = np.random.default_rng(11)
+    L = O.lib()
+    for _ in range(200):
+        na = int(rng.integers(1, 300))
+        a = np.sort(rng.integers(0, 20, na)).astype(np.float32)
+        b = np.sort(rng.integers(0, 20, 32)).astype(np.float32)
+        diag = int(rng.integers(0, na + 33))
+        got = L.fgo_merge_path_partition(O.ptr(a, C.c_float), na, O.ptr(b, C.c_float), 32, diag)
+        assert got == _ref_partition(list(a), list(b), diag)
+        bi = diag - got
+        # a valid merge split: everything left of it <= everything right of it
+        left = np.concatenate([a[:got], b[:bi]])
+        right = np.concatenate([a[got:], b[bi:]])
+        if left.size and right.size:
+            assert left.max() <= right.min()
