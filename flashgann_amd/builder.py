@@ -156,18 +156,20 @@ def hadamard_rotation(signs: np.ndarray, device) -> torch.Tensor:
 
 
 def build_graph(x: torch.Tensor, degree: int, random_links: int | None = None,
-                seed: int = 0x5EED, verbose: bool = False) -> torch.Tensor:
+                seed: int = 0x5EED, alpha: float = 1.0, candidates: int | None = None,
+                verbose: bool = False) -> torch.Tensor:
     """Returns (n, degree) int64 neighbour ids (-1 = padding)."""
     n = x.shape[0]
     dev = x.device
-    kc = min(2 * degree, n - 1)
-    cand, cd = knn(x, kc)
+    kc = min(candidates or 2 * degree, n - 1)
+    on_gpu = x.device.type == "cuda"
+    cand, cd = knn(x, kc, chunk_elems=(1 << 30) if on_gpu else (1 << 28))
     if verbose:
         print(f"[builder] knn done k={kc}", flush=True)
     nr = degree // 4 if random_links is None else random_links
     nr = min(nr, max(0, n - 1 - degree)) if n > 2 * degree else 0
     local_cap = degree - nr
-    local_keep = _prune(cand, cd, x, local_cap)
+    local_keep = _prune(cand, cd, x, local_cap, alpha2=alpha * alpha, chunk=32768 if on_gpu else 4096)
     ar = torch.arange(kc, device=dev)[None, :]
     o = torch.argsort(torch.where(local_keep, ar, kc + ar), dim=1)
     local = torch.where(torch.gather(local_keep, 1, o), torch.gather(cand, 1, o),
@@ -255,6 +257,7 @@ def entry_point(x: torch.Tensor) -> int:
 
 def build_codebook(base: np.ndarray, degree: int, signs: np.ndarray, use_ip: bool = False,
                    device: str | torch.device = "cpu", random_links: int | None = None,
+                   alpha: float = 1.0, candidates: int | None = None,
                    store_entry: bool = True, verbose: bool = False) -> Codebook:
     """Builds a complete codebook in the reference layout."""
     n, dim = base.shape
@@ -262,8 +265,10 @@ def build_codebook(base: np.ndarray, degree: int, signs: np.ndarray, use_ip: boo
     if signs.shape[0] != lay.padded_dim:
         raise ValueError("signs must have padded_dim entries")
     x = torch.as_tensor(np.ascontiguousarray(base, dtype=np.float32), device=device)
-    nbrs = build_graph(x, degree, random_links=random_links, verbose=verbose)
-    codes, factors = encode(x, nbrs, signs, use_ip=use_ip)
+    nbrs = build_graph(x, degree, random_links=random_links, alpha=alpha, candidates=candidates,
+                       verbose=verbose)
+    codes, factors = encode(x, nbrs, signs, use_ip=use_ip,
+                            chunk_edges=(1 << 22) if x.device.type == "cuda" else (1 << 20))
     rows = np.zeros((n, lay.row_offset), dtype=np.float32)
     rows[:, :dim] = base
     code_bytes = rows[:, lay.code_offset : lay.factor_offset].view(np.uint8)
@@ -282,7 +287,8 @@ def ground_truth(base: np.ndarray, queries: np.ndarray, k: int,
     b = torch.as_tensor(np.ascontiguousarray(base, dtype=np.float32), device=device)
     q = torch.as_tensor(np.ascontiguousarray(queries, dtype=np.float32), device=device)
     if not use_ip:
-        ids, _ = knn(b, k, queries=q, exclude_self=False)
+        ids, _ = knn(b, k, queries=q, exclude_self=False,
+                     chunk_elems=(1 << 30) if b.device.type == "cuda" else (1 << 28))
         return ids.cpu().numpy().astype(np.int32)
     out = []
     for s in range(0, q.shape[0], 1024):

@@ -114,8 +114,7 @@ struct LdsLayout {
 // Per-query LDS: visited table (aliased by the rotated query during
 // preparation), two beam buffers (ping-pong for the merge-path variant), the
 // 32-entry candidate buffer, the raw query, 8 x B/32 plane words and a small
-// scratch area (speculative round: 256 child ids + 32-entry accepted list +
-// parent lists).
+// scratch area (32-entry child list + parent lists).
 __host__ __device__ inline LdsLayout lds_layout(uint32_t dim, uint32_t padded_dim, uint32_t pbeam,
                                                 uint32_t bitlen) {
     LdsLayout L;
@@ -133,7 +132,7 @@ __host__ __device__ inline LdsLayout lds_layout(uint32_t dim, uint32_t padded_di
     L.plane_off = off;
     off += 8u * (padded_dim / 32u) * 4u;
     L.scratch_off = off;
-    off += (256u + 32u + 3u * 8u) * 4u;
+    off += (32u + 3u * 8u) * 4u;
     L.total = (off + 15u) & ~15u;
     return L;
 }
@@ -152,6 +151,7 @@ struct SearchParams {
     float phase2_rho;
     int use_ip;
     int dup_free;
+    int vec_ok;
     uint32_t entry;
     int nq;
     LdsLayout lds;
@@ -310,29 +310,6 @@ __device__ __forceinline__ float half_distance(const float *__restrict__ row, co
     val += __shfl_xor(val, 2);
     val += __shfl_xor(val, 1);
     return use_ip ? -val : val;
-}
-
-// Exact distances for the children in cd/ci slots listed by `mask` (bit i =
-// slot i), two children per pass (one per half-wave).  Writes cd[slot].
-__device__ void exact_for_slots(const SearchParams &P, uint32_t mask, float *cd, const uint32_t *ci,
-                                const float *qv) {
-    const int lane = lane_id();
-    const int h = lane >> 5, nl = lane & 31;
-    while (mask) {
-        const int s0 = __builtin_ctz(mask);
-        mask &= mask - 1;
-        int s1 = -1;
-        if (mask) {
-            s1 = __builtin_ctz(mask);
-            mask &= mask - 1;
-        }
-        const int slot = h == 0 ? s0 : s1;
-        const bool active = slot >= 0;
-        const uint32_t child = active ? ci[slot] : 0u;
-        const float *row = P.data + static_cast<uint64_t>(child) * P.row_offset;
-        const float d = half_distance(row, qv, P.dim, nl, P.use_ip != 0, active);
-        if (active && nl == 0) cd[slot] = d;
-    }
 }
 
 // ------------------------------------------------------------ sorting networks
@@ -598,6 +575,168 @@ __device__ __forceinline__ void controller_step(Controller &c, uint32_t beam0, f
     c.policy_iters += 1;
 }
 
+// Loads one neighbour's B/8-byte code as WT words (16-byte vector load when
+// the row layout keeps the code block 16-byte aligned).
+template <int WT>
+__device__ __forceinline__ void load_code(const uint32_t *__restrict__ code, bool vec_ok, uint32_t (&c)[WT]) {
+    if constexpr (WT == 4) {
+        if (vec_ok) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(code);
+            c[0] = v.x; c[1] = v.y; c[2] = v.z; c[3] = v.w;
+            return;
+        }
+    }
+#pragma unroll
+    for (int w = 0; w < WT; ++w) c[w] = code[w];
+}
+
+// raw = sum_cb LUT[cb][nibble] from register-held planes (see raw_partial).
+template <int WT>
+__device__ __forceinline__ int32_t raw_regs(const uint32_t (&c)[WT], const uint32_t (&pl)[kPlanes + 1][WT],
+                                            bool any_wrap) {
+    uint32_t acc[kPlanes];
+#pragma unroll
+    for (int p = 0; p < kPlanes; ++p) acc[p] = 0;
+#pragma unroll
+    for (int w = 0; w < WT; ++w)
+#pragma unroll
+        for (int p = 0; p < kPlanes; ++p) acc[p] += __popc(c[w] & pl[p][w]);
+    uint32_t raw = 0;
+#pragma unroll
+    for (int p = 0; p < kPlanes; ++p) raw += acc[p] << p;
+    if (any_wrap) {
+        uint32_t wraps = 0;
+#pragma unroll
+        for (int w = 0; w < WT; ++w) {
+            const uint32_t x = c[w] & pl[kPlanes][w];
+            wraps += __popc(x & (x >> 1) & (x >> 2) & (x >> 3) & 0x11111111u);
+        }
+        raw -= 256u * wraps;
+    }
+    return static_cast<int32_t>(raw);
+}
+
+// Exact distances for n children held in cd/ci at slots slot_list[0..n)
+// (or 0..n when slot_list is null): two children per pass, PB passes with
+// their row loads issued together (DPL > 0: dims per lane known at compile
+// time; DPL == 0: generic loop).
+template <int DPL>
+__device__ void exact_batch(const SearchParams &P, int n, const uint32_t *slot_list, float *cd, const uint32_t *ci,
+                            const float (&qr)[DPL > 0 ? DPL : 1], const float *qv) {
+    const int lane = lane_id();
+    const int h = lane >> 5, nl = lane & 31;
+    const bool ip = P.use_ip != 0;
+    if constexpr (DPL > 0) {
+        constexpr int PB = 8;
+        for (int e0 = 0; e0 < n; e0 += 2 * PB) {
+            float v[PB][DPL];
+            int slot[PB];
+#pragma unroll
+            for (int j = 0; j < PB; ++j) {
+                const int e = e0 + 2 * j + h;
+                const bool act = e < n;
+                slot[j] = act ? static_cast<int>(slot_list ? slot_list[e] : static_cast<uint32_t>(e)) : -1;
+                const uint32_t child = act ? ci[slot[j]] : 0u;
+                const float *row = P.data + static_cast<uint64_t>(child) * P.row_offset;
+#pragma unroll
+                for (int k = 0; k < DPL; ++k) {
+                    const int i = nl + 32 * k;
+                    v[j][k] = (act && i < P.dim) ? row[i] : 0.0f;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < PB; ++j) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int k = 0; k < DPL; ++k) {
+                    const int i = nl + 32 * k;
+                    if (i < P.dim) {
+                        if (ip) {
+                            acc = fmaf(qr[k], v[j][k], acc);
+                        } else {
+                            const float d = qr[k] - v[j][k];
+                            acc = fmaf(d, d, acc);
+                        }
+                    }
+                }
+                acc += __shfl_xor(acc, 16);
+                acc += __shfl_xor(acc, 8);
+                acc += __shfl_xor(acc, 4);
+                acc += __shfl_xor(acc, 2);
+                acc += __shfl_xor(acc, 1);
+                if (slot[j] >= 0 && nl == 0) cd[slot[j]] = ip ? -acc : acc;
+            }
+            if (2 * PB >= n - e0) break;
+        }
+    } else {
+        for (int e0 = 0; e0 < n; e0 += 2) {
+            const int e = e0 + h;
+            const bool act = e < n;
+            const int slot = act ? static_cast<int>(slot_list ? slot_list[e] : static_cast<uint32_t>(e)) : 0;
+            const uint32_t child = act ? ci[slot] : 0u;
+            const float d = half_distance(P.data + static_cast<uint64_t>(child) * P.row_offset, qv, P.dim, nl, ip, act);
+            if (act && nl == 0) cd[slot] = d;
+        }
+    }
+}
+
+// The keep_k smallest valid (value, lane) pairs of each 32-lane half, as
+// warp_keep_topk_smallest_f32 (utils.cuh:251-267) selects them, found by
+// keep_k rounds of half-wave argmin instead of a 32-step rank count.
+__device__ __forceinline__ bool select_smallest(float value, bool valid, int keep_k, int max_k) {
+    const int lane = lane_id();
+    const int h = lane >> 5, nl = lane & 31;
+    bool remaining = valid;
+    bool kept = false;
+    for (int r = 0; r < max_k; ++r) {
+        float m = remaining ? value : INFINITY;
+        m = fminf(m, __shfl_xor(m, 16));
+        m = fminf(m, __shfl_xor(m, 8));
+        m = fminf(m, __shfl_xor(m, 4));
+        m = fminf(m, __shfl_xor(m, 2));
+        m = fminf(m, __shfl_xor(m, 1));
+        const uint32_t cand = half_bits(ballot(remaining && value == m), h);
+        const bool take = r < keep_k && cand != 0u && nl == __builtin_ctz(cand | (cand == 0u ? 1u : 0u));
+        kept |= take;
+        remaining &= !take;
+    }
+    return kept;
+}
+
+// Visited test for up to four keys per lane, probes advanced together.
+template <int NK>
+__device__ __forceinline__ void hash_contains_n(const uint32_t *t, int bitlen, const uint32_t (&key)[NK],
+                                                bool (&test)[NK]) {
+    const uint32_t mask = (1u << bitlen) - 1u;
+    uint32_t idx[NK];
+    bool pend[NK];
+#pragma unroll
+    for (int s = 0; s < NK; ++s) {
+        idx[s] = (key[s] ^ (key[s] >> bitlen)) & mask;
+        pend[s] = test[s];
+    }
+    for (uint32_t step = 0; step <= mask; ++step) {
+        bool anyp = false;
+#pragma unroll
+        for (int s = 0; s < NK; ++s) {
+            if (pend[s]) {
+                const uint32_t old = t[idx[s]];
+                if (old == key[s]) {
+                    pend[s] = false;          // contained: not a fresh child
+                    test[s] = false;
+                } else if (old == kMaxIndex) {
+                    pend[s] = false;          // absent
+                } else {
+                    idx[s] = (idx[s] + 1u) & mask;
+                }
+            }
+            anyp |= pend[s];
+        }
+        if (!__any(anyp)) break;
+    }
+}
+
+template <int WT, int DPL>
 __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int qid = blockIdx.x;
@@ -607,6 +746,7 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
     const int B = P.padded_dim, W = B >> 5;
     const int deg = P.degree;
     const int bitlen = P.bitlen;
+    const bool vec_ok = P.vec_ok != 0;
 
     uint32_t *H = reinterpret_cast<uint32_t *>(smem + P.lds.hash_off);
     float *bd0 = reinterpret_cast<float *>(smem + P.lds.beam_off);
@@ -617,8 +757,7 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
     uint32_t *ci = reinterpret_cast<uint32_t *>(cd + 32);
     float *qv = reinterpret_cast<float *>(smem + P.lds.query_off);
     uint32_t *planes = reinterpret_cast<uint32_t *>(smem + P.lds.plane_off);
-    uint32_t *rchild = reinterpret_cast<uint32_t *>(smem + P.lds.scratch_off);
-    uint32_t *alist = rchild + 256;
+    uint32_t *alist = reinterpret_cast<uint32_t *>(smem + P.lds.scratch_off);
     uint32_t *plist = alist + 32;
     uint32_t *pnode = plist + 8;
     float *pdist = reinterpret_cast<float *>(pnode + 8);
@@ -628,6 +767,26 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
     int sum_q;
     prepare_query(P.queries + static_cast<uint64_t>(qid) * P.dim, P.signs, P.dim, B, reinterpret_cast<float *>(H),
                   qv, planes, qlow, qhigh, qwidth, sum_q, nullptr);
+    constexpr int WTR = WT > 0 ? WT : 1;
+    uint32_t pl[kPlanes + 1][WTR];
+    bool any_wrap = false;
+    if constexpr (WT > 0) {
+#pragma unroll
+        for (int p = 0; p <= kPlanes; ++p)
+#pragma unroll
+            for (int w = 0; w < WT; ++w) pl[p][w] = planes[p * WT + w];
+        uint32_t wor = 0;
+#pragma unroll
+        for (int w = 0; w < WT; ++w) wor |= pl[kPlanes][w];
+        any_wrap = wor != 0u;
+    }
+    constexpr int DPLR = DPL > 0 ? DPL : 1;
+    float qr[DPLR];
+#pragma unroll
+    for (int k = 0; k < DPLR; ++k) {
+        const int i = nl + 32 * k;
+        qr[k] = (DPL > 0 && i < P.dim) ? qv[i] : 0.0f;
+    }
 
     // ---- state (adaptive_search.cuh:67-107)
     hash_reset(H, bitlen);
@@ -640,7 +799,6 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
         ci[lane] = kMaxIndex;
     }
     __syncthreads();
-    // entry point (adaptive_search.cuh:109-119)
     const float entry_d = uni(half_distance(P.data + static_cast<uint64_t>(P.entry) * P.row_offset, qv, P.dim, nl,
                                             P.use_ip != 0, true));
     if (lane == 0) {
@@ -745,18 +903,19 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
                 const float *factors = prow + P.factor_offset;
                 const uint32_t *codes = reinterpret_cast<const uint32_t *>(prow + P.code_offset);
                 const bool valid = child != kMaxIndex;
-                float tx = 0.0f, fdq = 0.0f, fvq = 0.0f;
-                int32_t part = 0;
-                if (valid) {
-                    tx = factors[nl];
-                    fdq = factors[deg + nl];
-                    fvq = factors[2 * deg + nl];
-                    const int hw = W >> 1;
-                    part = raw_partial(codes + static_cast<uint64_t>(nl) * W, h * hw, (h + 1) * hw, planes, W);
-                }
-                const int32_t raw = part + __shfl_xor(part, 32);
                 float est = FLT_MAX;
                 if (valid) {
+                    const float tx = factors[nl];
+                    const float fdq = factors[deg + nl];
+                    const float fvq = factors[2 * deg + nl];
+                    int32_t raw;
+                    if constexpr (WT > 0) {
+                        uint32_t c[WT];
+                        load_code<WT>(codes + static_cast<uint64_t>(nl) * WT, vec_ok, c);
+                        raw = raw_regs<WT>(c, pl, any_wrap);
+                    } else {
+                        raw = raw_partial(codes + static_cast<uint64_t>(nl) * W, 0, W, planes, W);
+                    }
                     est = tx == FLT_MAX ? 0.0f : estimate_formula(raw, sum_q, qwidth, qlow, tx, fdq, fvq, pd0);
                     if (!isfinite(est)) {
                         child = kMaxIndex;
@@ -794,14 +953,16 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
                     dist = FLT_MAX;
                 }
             }
+            const uint32_t ins_mask = half_bits(ballot(ins), 0);
             if (h == 0) {
                 cd[nl] = dist;
                 ci[nl] = child;
+                if (ins) alist[__popc(ins_mask & ((1u << nl) - 1u))] = static_cast<uint32_t>(nl);
             }
             __syncthreads();
-            const uint32_t ins_mask = half_bits(ballot(ins), 0);
-            c_exact += static_cast<uint32_t>(__popc(ins_mask));
-            exact_for_slots(P, ins_mask, cd, ci, qv);
+            const int nins = __popc(ins_mask);
+            c_exact += static_cast<uint32_t>(nins);
+            exact_batch<DPL>(P, nins, alist, cd, ci, qr, qv);
         } else {
             // ---------------- speculative expansion (adaptive_search.cuh:344-444)
             if (c_st2 == kMaxIndex) c_st2 = static_cast<uint32_t>(iter);
@@ -809,87 +970,121 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
             const int tasks = static_cast<int>(nexp) * tiles;
             uint32_t compact = 0;
             for (int rbase = 0; rbase < tasks; rbase += kSearchWidth) {
-                uint32_t kept_masks[kSearchWidth];
-                for (int sr = 0; sr < kSearchWidth / 2; ++sr) {
-                    const int wslot = 2 * sr + h;
-                    const int task = rbase + wslot;
+                constexpr int SR = kSearchWidth / 2;  // sub-rounds: two reference warps per wave
+                uint32_t cid[SR];
+                bool val[SR];
+                int an[SR], tsk[SR], pix[SR];
+                const float *prw[SR];
+                // (a) neighbour ids of the round's 8 tasks, loads issued together
+#pragma unroll
+                for (int sr = 0; sr < SR; ++sr) {
+                    const int task = rbase + 2 * sr + h;
                     const bool tact = task < tasks;
                     const int pidx = tact ? task / tiles : 0;
                     const int tile = tact ? task - pidx * tiles : 0;
                     const int nidx = tile * 32 + nl;
-                    const uint32_t parent = pnode[pidx];
-                    const float *prow = data + static_cast<uint64_t>(parent) * P.row_offset;
-                    uint32_t child = kMaxIndex;
-                    bool valid = false;
-                    if (tact && nidx < deg) {
-                        child = reinterpret_cast<const uint32_t *>(prow + P.neighbor_offset)[nidx];
-                        valid = child != kMaxIndex && child < P.npoints && !hash_contains(H, bitlen, child);
-                    }
-                    const uint64_t idsm = ballot(tact && nidx < deg);
-                    c_ids += static_cast<uint32_t>(__popcll(idsm));
-                    int an = tact ? deg - tile * 32 : 0;
-                    if (an > 32) an = 32;
-                    const int keep = tact ? keep_count_for_expander(static_cast<uint32_t>(an), theta, ctl.rho, false, 0) : 0;
-                    const uint64_t vm = ballot(valid);
-                    const int rvc = __popc(half_bits(vm, h));
-                    const bool keep_all = keep >= rvc;
-                    float est = FLT_MAX;
-                    const uint64_t estm = ballot(!keep_all && valid);
-                    c_est += static_cast<uint32_t>(__popcll(estm));
-                    if (!keep_all && valid) {
-                        const float *factors = prow + P.factor_offset;
-                        const float tx = factors[nidx];
-                        if (tx != FLT_MAX) {
-                            const float fdq = factors[deg + nidx];
-                            const float fvq = factors[2 * deg + nidx];
-                            const uint32_t *code =
-                                reinterpret_cast<const uint32_t *>(prow + P.code_offset) + static_cast<uint64_t>(nidx) * W;
-                            const int32_t raw = raw_partial(code, 0, W, planes, W);
-                            est = estimate_formula(raw, sum_q, qwidth, qlow, tx, fdq, fvq, pdist[pidx]);
-                        }
-                        valid = isfinite(est);
-                    }
-                    bool keep_lane = valid;
-                    if (!keep_all) {
-                        const uint32_t near =
-                            __popc(half_bits(ballot(valid && kth_valid && est <= kth), h));
-                        const int eff = keep_count_for_expander(static_cast<uint32_t>(an), theta, ctl.rho, kth_valid, near);
-                        // warp_keep_topk_smallest_f32 (utils.cuh:251-267) within the half
-                        const float mine = valid ? est : FLT_MAX;
-                        const uint32_t vmh = half_bits(ballot(valid), h);
-                        int rank = 0;
-                        for (int s = 0; s < 32; ++s) {
-                            const float o0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), s));
-                            const float o1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), s + 32));
-                            const float other = h ? o1 : o0;
-                            const bool ov = (vmh >> s) & 1u;
-                            rank += (ov && (other < mine || (other == mine && s < nl))) ? 1 : 0;
-                        }
-                        keep_lane = valid && eff > 0 && rank < eff;
-                    }
-                    const uint64_t km = ballot(keep_lane);
-                    kept_masks[2 * sr] = uni(half_bits(km, 0));
-                    kept_masks[2 * sr + 1] = uni(half_bits(km, 1));
-                    rchild[wslot * 32 + nl] = child;
+                    tsk[sr] = tact ? tile * 32 : -1;
+                    pix[sr] = pidx;
+                    prw[sr] = data + static_cast<uint64_t>(pnode[pidx]) * P.row_offset;
+                    cid[sr] = (tact && nidx < deg) ? reinterpret_cast<const uint32_t *>(prw[sr] + P.neighbor_offset)[nidx]
+                                                   : kMaxIndex;
+                    int a = tact ? deg - tile * 32 : 0;
+                    an[sr] = a > 32 ? 32 : a;
+                    c_ids += static_cast<uint32_t>(__popcll(ballot(tact && nidx < deg)));
                 }
-                __syncthreads();
-                // list kept children in (task, lane) order
-                uint32_t total = 0;
-                for (int t = 0; t < kSearchWidth; ++t) {
-                    const uint32_t m = kept_masks[t];
-                    if (lane < 32 && ((m >> lane) & 1u)) {
-                        const uint32_t e = total + static_cast<uint32_t>(__popc(m & ((1u << lane) - 1u)));
-                        if (e < 32) alist[e] = rchild[t * 32 + lane];
+                // (b) visited test against the table as it stood at the round's start
+#pragma unroll
+                for (int sr = 0; sr < SR; ++sr) val[sr] = cid[sr] != kMaxIndex && cid[sr] < P.npoints;
+                hash_contains_n<SR>(H, bitlen, cid, val);
+                // (c) which tasks need estimates; their codes and factors, loads issued together
+                bool need[SR];
+                int keep[SR];
+                float tx[SR], fdq[SR], fvq[SR];
+                uint32_t code[SR][WTR];
+#pragma unroll
+                for (int sr = 0; sr < SR; ++sr) {
+                    const int rvc = __popc(half_bits(ballot(val[sr]), h));
+                    keep[sr] = tsk[sr] >= 0 ? keep_count_for_expander(static_cast<uint32_t>(an[sr]), theta, ctl.rho, false, 0) : 0;
+                    need[sr] = !(keep[sr] >= rvc);
+                    tx[sr] = FLT_MAX;
+                    fdq[sr] = 0.0f;
+                    fvq[sr] = 0.0f;
+                    if (need[sr] && val[sr]) {
+                        const int nidx = tsk[sr] + nl;
+                        const float *factors = prw[sr] + P.factor_offset;
+                        tx[sr] = factors[nidx];
+                        fdq[sr] = factors[deg + nidx];
+                        fvq[sr] = factors[2 * deg + nidx];
+                        if constexpr (WT > 0)
+                            load_code<WT>(reinterpret_cast<const uint32_t *>(prw[sr] + P.code_offset) +
+                                              static_cast<uint64_t>(nidx) * WT,
+                                          vec_ok, code[sr]);
                     }
-                    total += static_cast<uint32_t>(__popc(m));
+                    c_est += static_cast<uint32_t>(__popcll(ballot(need[sr] && val[sr])));
+                }
+                // (d) estimates, kth-near counts, keep decisions
+                uint32_t kept_mask[kSearchWidth];
+                bool keepl[SR];
+#pragma unroll
+                for (int sr = 0; sr < SR; ++sr) {
+                    float est = FLT_MAX;
+                    if (need[sr] && val[sr]) {
+                        if (tx[sr] != FLT_MAX) {
+                            int32_t raw;
+                            if constexpr (WT > 0) {
+                                raw = raw_regs<WT>(code[sr], pl, any_wrap);
+                            } else {
+                                const int nidx = tsk[sr] + nl;
+                                raw = raw_partial(reinterpret_cast<const uint32_t *>(prw[sr] + P.code_offset) +
+                                                      static_cast<uint64_t>(nidx) * W,
+                                                  0, W, planes, W);
+                            }
+                            est = estimate_formula(raw, sum_q, qwidth, qlow, tx[sr], fdq[sr], fvq[sr], pdist[pix[sr]]);
+                        }
+                        val[sr] = isfinite(est);
+                    }
+                    bool kl = val[sr];
+                    const bool any_need = __any(need[sr]);
+                    if (any_need) {
+                        const uint32_t near = __popc(half_bits(ballot(val[sr] && kth_valid && est <= kth), h));
+                        int eff = keep[sr];
+                        if (need[sr]) eff = keep_count_for_expander(static_cast<uint32_t>(an[sr]), theta, ctl.rho, kth_valid, near);
+                        const int maxk = uni(max(eff, __shfl_xor(eff, 32)));
+                        const bool sel = select_smallest(est, val[sr], eff, maxk);
+                        if (need[sr]) kl = val[sr] && eff > 0 && sel;
+                    }
+                    keepl[sr] = kl;
+                    const uint64_t km = ballot(kl);
+                    kept_mask[2 * sr] = uni(half_bits(km, 0));
+                    kept_mask[2 * sr + 1] = uni(half_bits(km, 1));
+                }
+                // (e) kept children listed in (task, lane) order
+                uint32_t base_t[kSearchWidth];
+                uint32_t total = 0;
+#pragma unroll
+                for (int t = 0; t < kSearchWidth; ++t) {
+                    base_t[t] = total;
+                    total += static_cast<uint32_t>(__popc(kept_mask[t]));
+                }
+#pragma unroll
+                for (int sr = 0; sr < SR; ++sr) {
+                    if (keepl[sr]) {
+                        const int t = 2 * sr + h;
+                        const uint32_t e = base_t[t] + static_cast<uint32_t>(__popc(kept_mask[t] & ((1u << nl) - 1u)));
+                        if (e < 32) alist[e] = cid[sr];
+                    }
                 }
                 __syncthreads();
                 if (total > 32) total = 32;  // <= 4 kept per task at theta = 8
+                // (f) insert in list order; a repeat of an earlier entry is dropped
                 const bool mine = lane < static_cast<int>(total);
                 const uint32_t key = mine ? alist[lane] : kMaxIndex;
-                const uint32_t members = half_bits(ballot(mine), 0);
-                const bool acc = mine && !dup_of_earlier(key, members, nl, 0);
-                if (acc) hash_insert(H, bitlen, key);
+                const uint32_t got = mine ? hash_insert(H, bitlen, key) : 0u;
+                bool acc = got != 0u;
+                if (__any(mine && !got)) {
+                    const uint32_t members = half_bits(ballot(mine), 0);
+                    acc = mine && !dup_of_earlier(key, members, nl, 0);
+                }
                 const uint32_t accm = half_bits(ballot(acc), 0);
                 if (acc) {
                     const uint32_t slot = compact + static_cast<uint32_t>(__popc(accm & ((1u << lane) - 1u)));
@@ -902,9 +1097,8 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
                 __syncthreads();
             }
             if (compact > static_cast<uint32_t>(P.collect_cap)) compact = static_cast<uint32_t>(P.collect_cap);
-            const uint32_t emask = compact >= 32 ? 0xFFFFFFFFu : ((1u << compact) - 1u);
             c_exact += compact;
-            exact_for_slots(P, emask, cd, ci, qv);
+            exact_batch<DPL>(P, static_cast<int>(compact), nullptr, cd, ci, qr, qv);
         }
         __syncthreads();
     }
@@ -1127,6 +1321,7 @@ int make_params(fg_index *ix, uint32_t nq, uint32_t K, uint32_t beam, SearchPara
     P.phase2_rho = ix->degree <= 4u ? 0.0f : 1.0f - 4.0f / static_cast<float>(ix->degree);  // utils 20-23
     P.use_ip = ix->metric == FG_METRIC_IP ? 1 : 0;
     P.dup_free = ix->dup_free;
+    P.vec_ok = (ix->row_offset % 4 == 0 && ix->code_offset % 4 == 0) ? 1 : 0;
     P.entry = ix->entry;
     P.nq = static_cast<int>(nq);
     P.lds = lds_layout(ix->dim, ix->padded_dim, static_cast<uint32_t>(P.pbeam), static_cast<uint32_t>(P.bitlen));
@@ -1135,7 +1330,16 @@ int make_params(fg_index *ix, uint32_t nq, uint32_t K, uint32_t beam, SearchPara
 
 int launch(fg_index *ix, const SearchParams &P, hipStream_t stream) {
     if (P.nq == 0) return FG_OK;
-    hipLaunchKernelGGL(fg_search_kernel, dim3(P.nq), dim3(64), P.lds.total, stream, P);
+    const int W = P.padded_dim / 32;
+    if (W == 2 && P.dim <= 64) {
+        hipLaunchKernelGGL((fg_search_kernel<2, 2>), dim3(P.nq), dim3(64), P.lds.total, stream, P);
+    } else if (W == 4 && P.dim <= 96) {
+        hipLaunchKernelGGL((fg_search_kernel<4, 3>), dim3(P.nq), dim3(64), P.lds.total, stream, P);
+    } else if (W == 4) {
+        hipLaunchKernelGGL((fg_search_kernel<4, 4>), dim3(P.nq), dim3(64), P.lds.total, stream, P);
+    } else {
+        hipLaunchKernelGGL((fg_search_kernel<0, 0>), dim3(P.nq), dim3(64), P.lds.total, stream, P);
+    }
     FG_HIP(hipGetLastError(), "search kernel launch");
     (void)ix;
     return FG_OK;

@@ -1,0 +1,92 @@
+"""Codebook builder: graph shape, the per-edge encoding against its
+definition, and the quality of the resulting RaBitQ estimates."""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from conftest import small_index
+from oracle import oracle as O
+
+
+def test_graph_shape():
+    cb, _, base = small_index()
+    nb = cb.neighbors().astype(np.int64)
+    n, deg = nb.shape
+    assert deg == cb.layout.degree
+    assert (nb < n).all()
+    assert not (nb == np.arange(n)[:, None]).any()
+    for row in nb[:500]:
+        assert len(set(row.tolist())) == deg
+    d = ((base[nb[:200]] - base[:200, None, :]) ** 2).sum(-1)
+    assert (np.diff(d, axis=1) >= 0).all()                       # sorted by distance
+
+
+def test_encoding_matches_definition():
+    from flashgann_amd.builder import hadamard_rotation
+    from flashgann_amd.codebook import unpack_codes
+    cb, _, base = small_index()
+    lay = cb.layout
+    P = hadamard_rotation(cb.signs, "cpu").numpy()
+    nb = cb.neighbors().astype(np.int64)
+    codes = cb.codes()
+    fac = cb.factors()
+    rng = np.random.default_rng(0)
+    for u in rng.integers(0, cb.npoints, 25):
+        for j in rng.integers(0, lay.degree, 4):
+            v = nb[u, j]
+            r = np.zeros(lay.padded_dim)
+            r[: lay.dim] = base[v].astype(np.float64) - base[u]
+            y = P @ r
+            bits = (y > 0).astype(np.uint8)
+            assert np.array_equal(unpack_codes(codes[u, j]), bits)
+            s = 2.0 * bits - 1.0
+            pc = P @ np.pad(base[u].astype(np.float64), (0, lay.padded_dim - lay.dim))
+            f = -2.0 * (r @ r) / np.abs(y).sum()
+            assert fac[u, 1, j] == np.float32(f)
+            assert fac[u, 2, j] == np.float32(f * s.sum())
+            assert fac[u, 0, j] == np.float32(r @ r - f * (s @ pc))
+
+
+def test_estimates_track_exact_distances():
+    """RaBitQ estimates of d(q, v) via a parent u: small relative error and
+    close to unbiased (the property the prune relies on)."""
+    cb, q, base = small_index()
+    lay = cb.layout
+    L = O.lib()
+    nb = cb.neighbors().astype(np.int64)
+    codes = cb.codes()
+    fac = cb.factors()
+    rng = np.random.default_rng(1)
+    rel = []
+    for qi in range(8):
+        qf = O.query_prepare(q[qi], cb.signs, lay.dim, lay.padded_dim)
+        for u in rng.integers(0, cb.npoints, 30):
+            pd = float(((q[qi].astype(np.float64) - base[u]) ** 2).sum())
+            for j in range(lay.degree):
+                v = nb[u, j]
+                code = np.ascontiguousarray(codes[u, j])
+                est = L.fgo_estimate_seq(C.byref(qf), O.ptr(code, C.c_uint8), float(fac[u, 0, j]),
+                                         float(fac[u, 1, j]), float(fac[u, 2, j]), pd, lay.padded_dim)
+                ex = float(((q[qi].astype(np.float64) - base[v]) ** 2).sum())
+                rel.append((est - ex) / ex)
+    rel = np.array(rel)
+    assert abs(np.median(rel)) < 0.05
+    assert np.percentile(np.abs(rel), 90) < 0.25
+
+
+def test_truncated_codebook_rejected(tmp_path):
+    import pytest
+    from flashgann_amd import _lib
+    from flashgann_amd.codebook import read_codebook, write_codebook
+    cb, _, _ = small_index()
+    p = str(tmp_path / "cb.index")
+    write_codebook(p, cb.rows[:100], cb.signs, cb.entry)
+    with open(p, "r+b") as f:
+        f.truncate(4 + 100 * cb.layout.row_offset * 4)
+    with pytest.raises(ValueError):
+        read_codebook(p, 100, cb.layout.dim, cb.layout.degree)
+    h = C.c_void_p()
+    rc = _lib.lib().fg_index_load(p.encode(), 100, cb.layout.dim, cb.layout.degree, 0, C.byref(h))
+    assert rc == _lib.FG_EIO

@@ -1,0 +1,78 @@
+"""Whole-search checks of the oracle: recall against brute force, internal
+invariants, thread-count independence and the result-writer edge cases."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import small_index
+from oracle import oracle as O
+
+
+def test_recall_against_brute_force():
+    from flashgann_amd import builder
+    from flashgann_amd.metrics import compute_recall
+    cb, q, base = small_index(n=4000, nq=64, comps=16)
+    gt = builder.ground_truth(base, q, 100)
+    ix = O.OracleIndex.from_codebook(cb)
+    out, cnt = ix.search(q, 100, 128)
+    assert compute_recall(out, gt, 100) >= 0.95
+    out10, _ = ix.search(q, 10, 64)
+    assert compute_recall(out10, gt[:, :10], 10) >= 0.95
+
+
+def test_invariants_and_counters():
+    cb, q, _ = small_index()
+    ix = O.OracleIndex.from_codebook(cb)
+    for K, beam in [(10, 32), (100, 128), (100, 256)]:
+        out, cnt = ix.search(q, K, beam)
+        assert (out < cb.npoints).all()
+        assert (cnt["exact"] >= 1).all()
+        assert (cnt["expansions"] <= cnt["iterations"] * 8).all()
+        assert (cnt["estimates"] <= cnt["ids_read"]).all()
+        assert (cnt["iterations"] <= min(1024, (beam * 11 + 9) // 10)).all()
+        # stage II starts after at least 4 stalled iterations of stage I
+        st2 = cnt["stage2_iter"]
+        assert ((st2 == 0xFFFFFFFF) | (st2 >= 4)).all()
+
+
+def test_thread_count_independent():
+    cb, q, _ = small_index()
+    ix = O.OracleIndex.from_codebook(cb)
+    a, ca = ix.search(q, 100, 128, threads=1)
+    b, cb_ = ix.search(q, 100, 128, threads=7)
+    assert np.array_equal(a, b) and np.array_equal(ca, cb_)
+    one, c1, _ = ix.search_one(q[3], 100, 128)
+    assert np.array_equal(one, a[3])
+
+
+def test_k_larger_than_beam_repeats_last():
+    cb, q, _ = small_index()
+    ix = O.OracleIndex.from_codebook(cb)
+    out, _ = ix.search(q[:4], 20, 8)
+    assert (out[:, 8:] == out[:, 7:8]).all()
+
+
+def test_beam_one_and_invalid_args():
+    cb, q, _ = small_index()
+    ix = O.OracleIndex.from_codebook(cb)
+    out, cnt = ix.search(q[:4], 5, 1)
+    assert (out == out[:, :1]).all()
+    with pytest.raises(ValueError):
+        ix.search(q[:1], 10, 2048)
+    with pytest.raises(ValueError):
+        ix.search(q[:1], 0, 64)
+
+
+def test_trace_records_theta_switch():
+    cb, q, _ = small_index()
+    ix = O.OracleIndex.from_codebook(cb)
+    out, cnt, tr = ix.search_one(q[0], 100, 128, trace_cap=1024)
+    assert len(tr) == cnt.iterations
+    thetas = [t.theta for t in tr]
+    assert thetas[0] == 1
+    if cnt.stage2_iter != 0xFFFFFFFF:
+        k = cnt.stage2_iter
+        assert all(t == 8 for t in thetas[k:]) and all(t == 1 for t in thetas[:k])
+    rhos = [t.rho for t in tr if t.theta == 1]
+    assert rhos[0] >= 0.25 and all(b >= a for a, b in zip(rhos, rhos[1:]))   # stage-I rho never decreases
