@@ -6,14 +6,18 @@ reference's layout (include/qg.hpp:66-73).  It runs on whatever torch device
 it is handed: the GPU for million-point indexes, the CPU for test fixtures.
 
 Graph.  Exactly `degree` out-edges per node:
-  * local edges (degree - degree/4 slots): exact k-nearest candidates
-    (k = 2*degree) pruned with the relative-neighbourhood rule (drop v if a
-    kept w has d(w,v) < d(u,v)), backfilled from the candidates in distance
-    order;
-  * long links (degree/4 slots): seeded uniform-random targets.  Mixture data
-    with well-separated components has no between-component edges in a k-NN
-    graph; random links make every component reachable and let the beam
-    search sample other components cheaply through RaBitQ estimates.
+  * local edges: exact k-nearest candidates (k = 2*degree) pruned with the
+    relative-neighbourhood rule (drop v if a kept w has d(w,v) < d(u,v)),
+    at most degree - degree/4 of them;
+  * long links: seeded uniform-random targets in every remaining slot (at
+    least degree/4).  Mixture data with well-separated components has no
+    between-component edges in a k-NN graph; the random links make every
+    component reachable and let the beam search probe other components
+    cheaply through RaBitQ estimates.  Recall is bimodal on such data (a query
+    finds its component or misses it), and the miss rate falls with the number
+    of random probes per expansion, so slots the RNG rule leaves empty go to
+    random links rather than to backfilled near duplicates
+    (fill_random=False backfills them from the k-NN candidates instead).
 Neighbour lists are sorted by (distance, id); short lists (tiny N) are padded
 with 0xFFFFFFFF, which the search treats as "no neighbour".
 
@@ -157,7 +161,7 @@ def hadamard_rotation(signs: np.ndarray, device) -> torch.Tensor:
 
 def build_graph(x: torch.Tensor, degree: int, random_links: int | None = None,
                 seed: int = 0x5EED, alpha: float = 1.0, candidates: int | None = None,
-                verbose: bool = False) -> torch.Tensor:
+                fill_random: bool = True, verbose: bool = False) -> torch.Tensor:
     """Returns (n, degree) int64 neighbour ids (-1 = padding)."""
     n = x.shape[0]
     dev = x.device
@@ -178,10 +182,11 @@ def build_graph(x: torch.Tensor, degree: int, random_links: int | None = None,
     if nr:
         g = torch.Generator().manual_seed(seed)
         # uniform targets != self: draw in [0, n-1) and skip over the owner
-        r = torch.randint(0, n - 1, (n, 2 * nr), generator=g).to(dev)
+        nfill = degree if fill_random else nr
+        r = torch.randint(0, n - 1, (n, 2 * nfill), generator=g).to(dev)
         own = torch.arange(n, device=dev)[:, None]
         r = r + (r >= own).to(r.dtype)
-        parts.append(_first_unique(r, nr))
+        parts.append(_first_unique(r, nfill))
     parts.append(cand)
     merged = _first_unique(torch.cat(parts, 1), degree)
     # sort each list by (distance, id)
@@ -257,7 +262,7 @@ def entry_point(x: torch.Tensor) -> int:
 
 def build_codebook(base: np.ndarray, degree: int, signs: np.ndarray, use_ip: bool = False,
                    device: str | torch.device = "cpu", random_links: int | None = None,
-                   alpha: float = 1.0, candidates: int | None = None,
+                   alpha: float = 1.0, candidates: int | None = None, fill_random: bool = True,
                    store_entry: bool = True, verbose: bool = False) -> Codebook:
     """Builds a complete codebook in the reference layout."""
     n, dim = base.shape
@@ -266,7 +271,7 @@ def build_codebook(base: np.ndarray, degree: int, signs: np.ndarray, use_ip: boo
         raise ValueError("signs must have padded_dim entries")
     x = torch.as_tensor(np.ascontiguousarray(base, dtype=np.float32), device=device)
     nbrs = build_graph(x, degree, random_links=random_links, alpha=alpha, candidates=candidates,
-                       verbose=verbose)
+                       fill_random=fill_random, verbose=verbose)
     codes, factors = encode(x, nbrs, signs, use_ip=use_ip,
                             chunk_edges=(1 << 22) if x.device.type == "cuda" else (1 << 20))
     rows = np.zeros((n, lay.row_offset), dtype=np.float32)

@@ -95,13 +95,15 @@ __host__ __device__ inline int keep_count_for_expander(uint32_t active, int thet
 
 // Visited-table size.  Between two resets the table receives at most
 // beam + 16 * 32 * tiles distinct keys (restore + one reset interval of
-// inserts, <= 32 per 8-task round), so any table that stays below 75% load
-// behaves as an exact set, as the reference's 2^11-entry table does
-// (utils.cuh:137-151).  Membership answers are therefore identical.
+// inserts, <= 32 per 8-task round).  Any open-addressing table with more
+// slots than that never fills, so it answers every membership query exactly
+// like the reference's 2^11-entry table (utils.cuh:137-151), which never fills
+// either.  The table is the smallest power of two keeping that worst case at
+// <= 90% load.
 __host__ __device__ inline uint32_t visited_bitlen(uint32_t beam, uint32_t degree) {
     const uint32_t tiles = (degree + 31) / 32;
     const uint32_t need = beam + 16u * 32u * tiles + 1u;
-    const uint32_t target = (need * 4u + 2u) / 3u;
+    const uint32_t target = (need * 10u + 8u) / 9u;
     uint32_t bitlen = 8;
     while ((1u << bitlen) < target) ++bitlen;
     return bitlen;
@@ -112,7 +114,7 @@ struct LdsLayout {
 };
 
 // Per-query LDS: visited table (aliased by the rotated query during
-// preparation), two beam buffers (ping-pong for the merge-path variant), the
+// preparation), the beam, the
 // 32-entry candidate buffer, the raw query, 8 x B/32 plane words and a small
 // scratch area (32-entry child list + parent lists).
 __host__ __device__ inline LdsLayout lds_layout(uint32_t dim, uint32_t padded_dim, uint32_t pbeam,
@@ -124,7 +126,7 @@ __host__ __device__ inline LdsLayout lds_layout(uint32_t dim, uint32_t padded_di
     if (hash_bytes < padded_dim * 4u) hash_bytes = padded_dim * 4u;
     off += hash_bytes;
     L.beam_off = off;
-    off += (pbeam > 128 ? 2u : 1u) * pbeam * 8u;
+    off += pbeam * 8u;
     L.cand_off = off;
     off += 32u * 8u;
     L.query_off = off;
@@ -167,16 +169,48 @@ __device__ __forceinline__ uint32_t half_bits(uint64_t m, int h) {
     return static_cast<uint32_t>(m >> (32 * h));
 }
 
+// Lane i reads lane i ^ m.  Masks below 32 stay inside a 32-lane half and use
+// DPP (1, 2: quad_perm; 4: half-row mirror then quad reverse, (i^7)^3 = i^4;
+// 8: row mirror then half-row mirror, (i^15)^7 = i^8) or ds_swizzle's bit mode
+// (16); 32 crosses halves through ds_bpermute.  Call with every lane active.
+__device__ __forceinline__ int xshfl(int v, int m) {
+    switch (m) {
+    case 1:
+        return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+    case 2:
+        return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+    case 4: {
+        const int t = __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
+        return __builtin_amdgcn_update_dpp(0, t, 0x1B, 0xF, 0xF, false);
+    }
+    case 8: {
+        const int t = __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);
+        return __builtin_amdgcn_update_dpp(0, t, 0x141, 0xF, 0xF, false);
+    }
+    case 16:
+        return __builtin_amdgcn_ds_swizzle(v, 0x401F);
+    default:
+        return __shfl_xor(v, m);
+    }
+}
+__device__ __forceinline__ float xshfl(float v, int m) { return __int_as_float(xshfl(__float_as_int(v), m)); }
+__device__ __forceinline__ uint32_t xshfl(uint32_t v, int m) {
+    return static_cast<uint32_t>(xshfl(static_cast<int>(v), m));
+}
+
 __device__ __forceinline__ float wave_min(float v) {
-    for (int m = 32; m >= 1; m >>= 1) v = fminf(v, __shfl_xor(v, m));
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fminf(v, xshfl(v, m));
     return v;
 }
 __device__ __forceinline__ float wave_max(float v) {
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, xshfl(v, m));
     return v;
 }
 __device__ __forceinline__ int wave_sum(int v) {
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += xshfl(v, m);
     return v;
 }
 
@@ -246,8 +280,8 @@ __device__ void prepare_query(const float *__restrict__ query, const float *__re
             if (nl == 0) planes[p * W + w] = half_bits(m, h);
         }
         // a chunk's full-nibble LUT entry is (q0+q1+q2+q3) mod 256 (utils.cuh:913-917)
-        uint32_t s = q + static_cast<uint32_t>(__shfl_xor(static_cast<int>(q), 1));
-        s += static_cast<uint32_t>(__shfl_xor(static_cast<int>(s), 2));
+        uint32_t s = q + xshfl(q, 1);
+        s += xshfl(s, 2);
         const uint64_t wm = ballot(s >= 256u);
         if (nl == 0) planes[kPlanes * W + w] = half_bits(wm, h);
     }
@@ -304,11 +338,11 @@ __device__ __forceinline__ float half_distance(const float *__restrict__ row, co
             }
         }
     }
-    val += __shfl_xor(val, 16);
-    val += __shfl_xor(val, 8);
-    val += __shfl_xor(val, 4);
-    val += __shfl_xor(val, 2);
-    val += __shfl_xor(val, 1);
+    val += xshfl(val, 16);
+    val += xshfl(val, 8);
+    val += xshfl(val, 4);
+    val += xshfl(val, 2);
+    val += xshfl(val, 1);
     return use_ip ? -val : val;
 }
 
@@ -322,13 +356,14 @@ __device__ __forceinline__ float half_distance(const float *__restrict__ row, co
 // with ascending = (pos_lo & kk) == 0.
 template <int E>
 __device__ __forceinline__ void bitonic_stage(float (&k)[E], uint32_t (&v)[E], int base, int kk, int jstart) {
+#pragma unroll
     for (int j = jstart; j >= 1; j >>= 1) {
         if (j >= E) {
             const int m = j / E;
 #pragma unroll
             for (int e = 0; e < E; ++e) {
-                const float pk = __shfl_xor(k[e], m);
-                const uint32_t pv = static_cast<uint32_t>(__shfl_xor(static_cast<int>(v[e]), m));
+                const float pk = xshfl(k[e], m);
+                const uint32_t pv = xshfl(v[e], m);
                 const int pos = base + e;
                 const bool p = ((pos & kk) != 0) == ((pos & j) != 0);
                 if (k[e] != pk && ((k[e] < pk) != p)) {
@@ -356,6 +391,7 @@ __device__ __forceinline__ void bitonic_stage(float (&k)[E], uint32_t (&v)[E], i
 __device__ __forceinline__ void sort32(float &key, uint32_t &val, int nl) {
     float k[1] = {key};
     uint32_t v[1] = {val};
+#pragma unroll
     for (int kk = 2; kk <= 32; kk <<= 1) bitonic_stage<1>(k, v, nl, kk, kk >> 1);
     key = k[0];
     val = v[0];
@@ -386,16 +422,13 @@ __device__ __forceinline__ int merge_path_partition(const float *a, int na, cons
 // is the identity.  pbeam > 128: topk_candidate_sort_and_merge
 // (utils.cuh:618-680) with the reference block's segmentation, writing into
 // the other beam buffer; returns the index of the buffer holding the beam.
-__device__ int merge_beam(const SearchParams &P, float *bd0, uint32_t *bi0, float *bd1, uint32_t *bi1, int cur,
-                          float *cd, uint32_t *ci) {
+__device__ void merge_beam(const SearchParams &P, float *bd, uint32_t *bi, float *cd, uint32_t *ci) {
     const int lane = lane_id();
     const int nl = lane & 31, h = lane >> 5;
     const int cbs = P.cbs, pbeam = P.pbeam;
     float ck = nl < cbs ? cd[nl] : FLT_MAX;
     uint32_t cv = nl < cbs ? ci[nl] : kMaxIndex;
     sort32(ck, cv, nl);
-    float *bd = cur ? bd1 : bd0;
-    uint32_t *bi = cur ? bi1 : bi0;
     if (pbeam <= 128) {
         if (pbeam == 128) {
             float k[2];
@@ -431,7 +464,8 @@ __device__ int merge_beam(const SearchParams &P, float *bd0, uint32_t *bi0, floa
                 k[0] = kk2;
                 v[0] = vv2;
             }
-            bitonic_stage<1>(k, v, pos, pbeam, pbeam >> 1);
+            if (pbeam == 64) bitonic_stage<1>(k, v, pos, 64, 32);
+            else bitonic_stage<1>(k, v, pos, 32, 16);
             __syncthreads();
             if (pbeam == 64 || h == 0) {
                 bd[pos] = k[0];
@@ -439,7 +473,7 @@ __device__ int merge_beam(const SearchParams &P, float *bd0, uint32_t *bi0, floa
             }
         }
         __syncthreads();
-        return cur;
+        return;
     }
     // merge-path variant: sorted candidates to LDS, then segments
     if (h == 0 && nl < cbs) {
@@ -447,34 +481,125 @@ __device__ int merge_beam(const SearchParams &P, float *bd0, uint32_t *bi0, floa
         ci[nl] = cv;
     }
     __syncthreads();
-    float *od = cur ? bd0 : bd1;
-    uint32_t *oi = cur ? bi0 : bi1;
     int active = (pbeam + 3) / 4;
     active = ((active + 31) / 32) * 32;
     if (active > kRefBlock) active = kRefBlock;
-    for (int t = lane; t < active; t += 64) {
-        const uint32_t ub = static_cast<uint32_t>(pbeam);
-        const int ob = static_cast<int>(min(ub, (static_cast<uint32_t>(t) * ub) / static_cast<uint32_t>(active)));
-        const int oe = static_cast<int>(min(ub, (static_cast<uint32_t>(t + 1) * ub) / static_cast<uint32_t>(active)));
-        const int tb = merge_path_partition(bd, pbeam, cd, cbs, ob);
-        const int te = merge_path_partition(bd, pbeam, cd, cbs, oe);
-        int ti = tb, cix = ob - tb;
-        const int cend = oe - te;
-        for (int o = ob; o < oe; ++o) {
-            const bool take_top = (cix >= cend) || (ti < te && bd[ti] <= cd[cix]);
-            if (take_top) {
-                od[o] = bd[ti];
-                oi[o] = bi[ti];
-                ++ti;
+    // Lane l owns segments [l*spl, (l+1)*spl); their spl+1 partition points
+    // are found by binary searches advanced together.  Segment t writes
+    // outputs [ob_t, ob_{t+1}) with ob_t = min(pbeam, t*pbeam/active); each
+    // segment holds at most 4 outputs because active >= pbeam/4.
+    constexpr int kMaxSpl = kRefBlock / 64;
+    const int spl = (active + 63) / 64;
+    const int t0 = lane * spl;
+    const uint32_t ub = static_cast<uint32_t>(pbeam);
+    int dg[kMaxSpl + 1], lo[kMaxSpl + 1], hi[kMaxSpl + 1], res[kMaxSpl + 1];
+    bool pend[kMaxSpl + 1];
+#pragma unroll
+    for (int k = 0; k <= kMaxSpl; ++k) {
+        const int t = t0 + k;
+        pend[k] = k <= spl && t <= active;
+        dg[k] = pend[k] ? static_cast<int>(min(ub, (static_cast<uint32_t>(t) * ub) / static_cast<uint32_t>(active))) : 0;
+        lo[k] = dg[k] - cbs > 0 ? dg[k] - cbs : 0;
+        hi[k] = dg[k] < pbeam ? dg[k] : pbeam;
+        res[k] = 0;
+    }
+    // utils.cuh:588-616, several diagonals at once
+    for (int round = 0; round < 16; ++round) {
+        bool anyp = false;
+#pragma unroll
+        for (int k = 0; k <= kMaxSpl; ++k) {
+            if (!pend[k]) continue;
+            if (lo[k] > hi[k]) {
+                res[k] = lo[k];
+                pend[k] = false;
+                continue;
+            }
+            const int ai = (lo[k] + hi[k]) >> 1;
+            const int bj = dg[k] - ai;
+            const float al = ai > 0 ? bd[ai - 1] : -FLT_MAX;
+            const float ar = ai < pbeam ? bd[ai] : FLT_MAX;
+            const float bl = bj > 0 ? cd[bj - 1] : -FLT_MAX;
+            const float br = bj < cbs ? cd[bj] : FLT_MAX;
+            if (al > br) {
+                hi[k] = ai - 1;
+            } else if (bl > ar) {
+                lo[k] = ai + 1;
             } else {
-                od[o] = cd[cix];
-                oi[o] = ci[cix];
-                ++cix;
+                res[k] = ai;
+                pend[k] = false;
+            }
+            anyp |= pend[k];
+        }
+        if (!__any(anyp)) break;
+    }
+    // utils.cuh:652-671 per segment: beam first on ties, at most 4 outputs,
+    // held in registers until every lane has read its inputs, then written
+    // back in place (no second beam buffer)
+    float okey[kMaxSpl][4];
+    uint32_t oval[kMaxSpl][4];
+    int obase[kMaxSpl], ocount[kMaxSpl];
+#pragma unroll
+    for (int k = 0; k < kMaxSpl; ++k) {
+        obase[k] = 0;
+        ocount[k] = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            okey[k][i] = FLT_MAX;
+            oval[k][i] = kMaxIndex;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kMaxSpl; ++k) {
+        const int t = t0 + k;
+        if (k >= spl || t >= active) continue;
+        const int ob = dg[k], oe = dg[k + 1];
+        const int tb = res[k], te = res[k + 1];
+        const int cb = ob - tb;
+        const int ce = oe - te;
+        float ak[4], ck2[4];
+        uint32_t av[4], cv2[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const bool ina = tb + i < te;
+            ak[i] = ina ? bd[tb + i] : FLT_MAX;
+            av[i] = ina ? bi[tb + i] : kMaxIndex;
+            const bool inb = cb + i < ce;
+            ck2[i] = inb ? cd[cb + i] : FLT_MAX;
+            cv2[i] = inb ? ci[cb + i] : kMaxIndex;
+        }
+        int na = te - tb, nb = ce - cb;
+        obase[k] = ob;
+        ocount[k] = oe - ob;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int o = ob + i;
+            if (o < oe) {
+                const bool take_top = (nb <= 0) || (na > 0 && ak[0] <= ck2[0]);
+                okey[k][i] = take_top ? ak[0] : ck2[0];
+                oval[k][i] = take_top ? av[0] : cv2[0];
+                // advance the consumed list by one (register shift, no indexing)
+#pragma unroll
+                for (int j = 0; j < 3; ++j) {
+                    ak[j] = take_top ? ak[j + 1] : ak[j];
+                    av[j] = take_top ? av[j + 1] : av[j];
+                    ck2[j] = take_top ? ck2[j] : ck2[j + 1];
+                    cv2[j] = take_top ? cv2[j] : cv2[j + 1];
+                }
+                na -= take_top ? 1 : 0;
+                nb -= take_top ? 0 : 1;
             }
         }
     }
     __syncthreads();
-    return cur ^ 1;
+#pragma unroll
+    for (int k = 0; k < kMaxSpl; ++k)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (i < ocount[k]) {
+                bd[obase[k] + i] = okey[k][i];
+                bi[obase[k] + i] = oval[k][i];
+            }
+    __syncthreads();
 }
 
 // ------------------------------------------------------------ visited table
@@ -590,6 +715,55 @@ __device__ __forceinline__ void load_code(const uint32_t *__restrict__ code, boo
     for (int w = 0; w < WT; ++w) c[w] = code[w];
 }
 
+// raw for NB code blocks at once, walking the planes one at a time from LDS
+// (one plane's WT words live at a time): raw_b = sum_p 2^p popcount(code_b &
+// plane_p) - 256 * wraps_b.
+template <int NB, int WT>
+__device__ __forceinline__ void raw_batch(const uint32_t (&c)[NB][WT], const uint32_t *planes, bool any_wrap,
+                                          int32_t (&raw)[NB]) {
+    uint32_t acc[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[b] = 0;
+#pragma unroll
+    for (int p = 0; p < kPlanes; ++p) {
+        uint32_t pw[WT];
+#pragma unroll
+        for (int w = 0; w < WT; ++w) pw[w] = planes[p * WT + w];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            uint32_t t = 0;
+#pragma unroll
+            for (int w = 0; w < WT; ++w) t += __popc(c[b][w] & pw[w]);
+            acc[b] += t << p;
+        }
+    }
+    if (any_wrap) {
+        uint32_t pw[WT];
+#pragma unroll
+        for (int w = 0; w < WT; ++w) pw[w] = planes[kPlanes * WT + w];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            uint32_t wr = 0;
+#pragma unroll
+            for (int w = 0; w < WT; ++w) {
+                const uint32_t x = c[b][w] & pw[w];
+                wr += __popc(x & (x >> 1) & (x >> 2) & (x >> 3) & 0x11111111u);
+            }
+            acc[b] -= 256u * wr;
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) raw[b] = static_cast<int32_t>(acc[b]);
+}
+
+template <int WT>
+__device__ __forceinline__ void load_planes(const uint32_t *planes, uint32_t (&pl)[kPlanes + 1][WT]) {
+#pragma unroll
+    for (int p = 0; p <= kPlanes; ++p)
+#pragma unroll
+        for (int w = 0; w < WT; ++w) pl[p][w] = planes[p * WT + w];
+}
+
 // raw = sum_cb LUT[cb][nibble] from register-held planes (see raw_partial).
 template <int WT>
 __device__ __forceinline__ int32_t raw_regs(const uint32_t (&c)[WT], const uint32_t (&pl)[kPlanes + 1][WT],
@@ -644,28 +818,56 @@ __device__ void exact_batch(const SearchParams &P, int n, const uint32_t *slot_l
                     v[j][k] = (act && i < P.dim) ? row[i] : 0.0f;
                 }
             }
+            float acc[PB];
 #pragma unroll
             for (int j = 0; j < PB; ++j) {
-                float acc = 0.0f;
+                acc[j] = 0.0f;
 #pragma unroll
                 for (int k = 0; k < DPL; ++k) {
                     const int i = nl + 32 * k;
                     if (i < P.dim) {
                         if (ip) {
-                            acc = fmaf(qr[k], v[j][k], acc);
+                            acc[j] = fmaf(qr[k], v[j][k], acc[j]);
                         } else {
                             const float d = qr[k] - v[j][k];
-                            acc = fmaf(d, d, acc);
+                            acc[j] = fmaf(d, d, acc[j]);
                         }
                     }
                 }
-                acc += __shfl_xor(acc, 16);
-                acc += __shfl_xor(acc, 8);
-                acc += __shfl_xor(acc, 4);
-                acc += __shfl_xor(acc, 2);
-                acc += __shfl_xor(acc, 1);
-                if (slot[j] >= 0 && nl == 0) cd[slot[j]] = ip ? -acc : acc;
             }
+            // Reduce-scatter over the half: at distance 16 lanes keep children
+            // j (lower) / j+4 (upper), at 8 keep j / j+2, at 4 keep j / j+1, then
+            // butterflies at 2 and 1.  Every step adds lane l and lane l^m of
+            // the same child, so each child's sum is the shfl_down tree of
+            // utils.cuh:277-281 up to operand order.
+            float r16[4], r8[2];
+            const bool b16 = (nl & 16) != 0, b8 = (nl & 8) != 0, b4 = (nl & 4) != 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float send = b16 ? acc[j] : acc[j + 4];
+                const float own = b16 ? acc[j + 4] : acc[j];
+                r16[j] = own + xshfl(send, 16);
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const float send = b8 ? r16[j] : r16[j + 2];
+                const float own = b8 ? r16[j + 2] : r16[j];
+                r8[j] = own + xshfl(send, 8);
+            }
+            float r4;
+            {
+                const float send = b4 ? r8[0] : r8[1];
+                const float own = b4 ? r8[1] : r8[0];
+                r4 = own + xshfl(send, 4);
+            }
+            r4 += xshfl(r4, 2);
+            r4 += xshfl(r4, 1);
+            const int c = (b16 ? 4 : 0) + (b8 ? 2 : 0) + (b4 ? 1 : 0);
+            int my_slot = -1;
+#pragma unroll
+            for (int j = 0; j < PB; ++j)
+                if (j == c) my_slot = slot[j];
+            if (my_slot >= 0 && (nl & 3) == 0) cd[my_slot] = ip ? -r4 : r4;
             if (2 * PB >= n - e0) break;
         }
     } else {
@@ -690,11 +892,11 @@ __device__ __forceinline__ bool select_smallest(float value, bool valid, int kee
     bool kept = false;
     for (int r = 0; r < max_k; ++r) {
         float m = remaining ? value : INFINITY;
-        m = fminf(m, __shfl_xor(m, 16));
-        m = fminf(m, __shfl_xor(m, 8));
-        m = fminf(m, __shfl_xor(m, 4));
-        m = fminf(m, __shfl_xor(m, 2));
-        m = fminf(m, __shfl_xor(m, 1));
+        m = fminf(m, xshfl(m, 16));
+        m = fminf(m, xshfl(m, 8));
+        m = fminf(m, xshfl(m, 4));
+        m = fminf(m, xshfl(m, 2));
+        m = fminf(m, xshfl(m, 1));
         const uint32_t cand = half_bits(ballot(remaining && value == m), h);
         const bool take = r < keep_k && cand != 0u && nl == __builtin_ctz(cand | (cand == 0u ? 1u : 0u));
         kept |= take;
@@ -751,8 +953,6 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
     uint32_t *H = reinterpret_cast<uint32_t *>(smem + P.lds.hash_off);
     float *bd0 = reinterpret_cast<float *>(smem + P.lds.beam_off);
     uint32_t *bi0 = reinterpret_cast<uint32_t *>(bd0 + P.pbeam);
-    float *bd1 = reinterpret_cast<float *>(bi0 + P.pbeam);
-    uint32_t *bi1 = reinterpret_cast<uint32_t *>(bd1 + P.pbeam);
     float *cd = reinterpret_cast<float *>(smem + P.lds.cand_off);
     uint32_t *ci = reinterpret_cast<uint32_t *>(cd + 32);
     float *qv = reinterpret_cast<float *>(smem + P.lds.query_off);
@@ -768,17 +968,12 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
     prepare_query(P.queries + static_cast<uint64_t>(qid) * P.dim, P.signs, P.dim, B, reinterpret_cast<float *>(H),
                   qv, planes, qlow, qhigh, qwidth, sum_q, nullptr);
     constexpr int WTR = WT > 0 ? WT : 1;
-    uint32_t pl[kPlanes + 1][WTR];
     bool any_wrap = false;
     if constexpr (WT > 0) {
-#pragma unroll
-        for (int p = 0; p <= kPlanes; ++p)
-#pragma unroll
-            for (int w = 0; w < WT; ++w) pl[p][w] = planes[p * WT + w];
         uint32_t wor = 0;
 #pragma unroll
-        for (int w = 0; w < WT; ++w) wor |= pl[kPlanes][w];
-        any_wrap = wor != 0u;
+        for (int w = 0; w < WT; ++w) wor |= planes[kPlanes * WT + w];
+        any_wrap = uni(wor) != 0u;
     }
     constexpr int DPLR = DPL > 0 ? DPL : 1;
     float qr[DPLR];
@@ -810,14 +1005,13 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
 
     Controller ctl{1, kPhase1Rho, 0, kMaxIndex, 0, false, entry_d, FLT_MAX, FLT_MAX};
     uint32_t c_iters = 0, c_exp = 0, c_ids = 0, c_est = 0, c_exact = 1, c_st2 = kMaxIndex;
-    int cur = 0;
     const int beam_sz = P.beam, pbeam = P.pbeam;
     const int cbs = P.cbs;
     const float *data = P.data;
 
     for (int iter = 0; iter < kMaxIterations; ++iter) {
-        float *bd = cur ? bd1 : bd0;
-        uint32_t *bi = cur ? bi1 : bi0;
+        float *bd = bd0;
+        uint32_t *bi = bi0;
         if (((iter + 1) % kHashReset) == 0) {  // adaptive_search.cuh:128-134
             hash_reset(H, bitlen);
             __syncthreads();
@@ -826,9 +1020,7 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
         }
         if (iter >= P.max_iter) break;
 
-        cur = merge_beam(P, bd0, bi0, bd1, bi1, cur, cd, ci);
-        bd = cur ? bd1 : bd0;
-        bi = cur ? bi1 : bi0;
+        merge_beam(P, bd, bi, cd, ci);
         for (int i = beam_sz + lane; i < pbeam; i += 64) {
             bd[i] = FLT_MAX;
             bi[i] = kMaxIndex;
@@ -910,9 +1102,11 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
                     const float fvq = factors[2 * deg + nl];
                     int32_t raw;
                     if constexpr (WT > 0) {
-                        uint32_t c[WT];
-                        load_code<WT>(codes + static_cast<uint64_t>(nl) * WT, vec_ok, c);
-                        raw = raw_regs<WT>(c, pl, any_wrap);
+                        uint32_t c[1][WT];
+                        load_code<WT>(codes + static_cast<uint64_t>(nl) * WT, vec_ok, c[0]);
+                        int32_t r1[1];
+                        raw_batch<1, WT>(c, planes, any_wrap, r1);
+                        raw = r1[0];
                     } else {
                         raw = raw_partial(codes + static_cast<uint64_t>(nl) * W, 0, W, planes, W);
                     }
@@ -1009,6 +1203,8 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
                     tx[sr] = FLT_MAX;
                     fdq[sr] = 0.0f;
                     fvq[sr] = 0.0f;
+#pragma unroll
+                    for (int w = 0; w < WTR; ++w) code[sr][w] = 0u;
                     if (need[sr] && val[sr]) {
                         const int nidx = tsk[sr] + nl;
                         const float *factors = prw[sr] + P.factor_offset;
@@ -1025,6 +1221,8 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
                 // (d) estimates, kth-near counts, keep decisions
                 uint32_t kept_mask[kSearchWidth];
                 bool keepl[SR];
+                int32_t rawb[SR];
+                if constexpr (WT > 0) raw_batch<SR, WT>(code, planes, any_wrap, rawb);
 #pragma unroll
                 for (int sr = 0; sr < SR; ++sr) {
                     float est = FLT_MAX;
@@ -1032,7 +1230,7 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
                         if (tx[sr] != FLT_MAX) {
                             int32_t raw;
                             if constexpr (WT > 0) {
-                                raw = raw_regs<WT>(code[sr], pl, any_wrap);
+                                raw = rawb[sr];
                             } else {
                                 const int nidx = tsk[sr] + nl;
                                 raw = raw_partial(reinterpret_cast<const uint32_t *>(prw[sr] + P.code_offset) +
@@ -1103,8 +1301,8 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
         __syncthreads();
     }
 
-    cur = merge_beam(P, bd0, bi0, bd1, bi1, cur, cd, ci);
-    const uint32_t *bi = cur ? bi1 : bi0;
+    merge_beam(P, bd0, bi0, cd, ci);
+    const uint32_t *bi = bi0;
     // result writer (adaptive_search.cuh:455-464)
     for (int i = lane; i < P.K; i += 64) {
         const uint32_t r = i < beam_sz ? (bi[i] & 0x7fffffffu) : (bi[beam_sz - 1] & 0x7fffffffu);

@@ -61,3 +61,51 @@ def test_scores_match_oracle(gpu_available, kind, dim):
         assert np.float32(es[t]) == np.float32(ref_s), t
         assert np.float32(ex[t]) == np.float32(ref_x), t
     ix.close()
+
+
+def _wrap_queries(signs, B, count, seed=12):
+    """Queries whose rotation puts four 64s in some 4-dim chunk (the uint8
+    LUT entry of that chunk wraps): z non-zero only at multiples of 4 makes
+    H z constant on every chunk, and x = s * z keeps the rotation exact."""
+    from oracle import oracle as O
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < count:
+        z = np.zeros(B, np.float32)
+        z[::4] = rng.integers(-40, 60, B // 4)
+        x = (signs * z).astype(np.float32)
+        qf = O.query_prepare(x, signs, B, B)
+        q = np.ctypeslib.as_array(qf.q)[:B]
+        if (q.reshape(-1, 4) == 64).all(1).any():
+            out.append(x)
+    return np.stack(out)
+
+
+def test_wrap_chunks_scores_and_search(gpu_available):
+    """The popcount planes' wrap correction reproduces the uint8 LUT."""
+    from flashgann_amd import Index
+    from oracle import oracle as O
+    cb, _, _ = small_index(n=1200, nq=4, dim=64, comps=8)
+    q = _wrap_queries(cb.signs, 64, 6)
+    ix = Index.from_codebook(cb)
+    rng = np.random.default_rng(3)
+    n = 200
+    qi = rng.integers(0, q.shape[0], n).astype(np.uint32)
+    pa = rng.integers(0, cb.npoints, n).astype(np.uint32)
+    sl = rng.integers(0, cb.layout.degree, n).astype(np.uint32)
+    el, es, _ = ix.score_edges(q, qi, pa, sl)
+    L = O.lib()
+    codes, fac = cb.codes(), cb.factors()
+    for t in range(n):
+        qf = O.query_prepare(q[qi[t]], cb.signs, 64, 64)
+        pd = L.fgo_warp_l2(64, O.ptr(np.ascontiguousarray(q[qi[t]]), C.c_float),
+                           O.ptr(np.ascontiguousarray(cb.rows[pa[t], :64]), C.c_float))
+        code = np.ascontiguousarray(codes[pa[t], sl[t]])
+        args = (float(fac[pa[t], 0, sl[t]]), float(fac[pa[t], 1, sl[t]]), float(fac[pa[t], 2, sl[t]]), pd, 64)
+        assert np.float32(el[t]) == np.float32(L.fgo_estimate_lanes(C.byref(qf), O.ptr(code, C.c_uint8), *args))
+        assert np.float32(es[t]) == np.float32(L.fgo_estimate_seq(C.byref(qf), O.ptr(code, C.c_uint8), *args))
+    ids, _, cnt = ix.search(q, 10, 64, counters=True)
+    rids, rcnt = O.OracleIndex.from_codebook(cb).search(q, 10, 64)
+    assert np.array_equal(ids, rids)
+    assert np.array_equal(cnt, rcnt.view(np.uint32).reshape(-1, 6))
+    ix.close()
