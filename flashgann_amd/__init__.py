@@ -115,6 +115,13 @@ class Index:
                                      C.c_void_p(results_ptr), C.c_void_p(counters_ptr or None),
                                      C.c_void_p(stream or None)))
 
+    def search_profile(self, queries_ptr: int, nq: int, K: int, beam: int, results_ptr: int,
+                       phase_ptr: int, stream: int = 0) -> None:
+        """Profiling build of the search: 10 uint64 phase-cycle sums per query."""
+        check(lib().fg_search_profile(self._h, C.c_void_p(queries_ptr), nq, K, beam,
+                                      C.c_void_p(results_ptr), C.c_void_p(phase_ptr),
+                                      C.c_void_p(stream or None)))
+
     def query_prepare(self, queries: np.ndarray):
         q = np.ascontiguousarray(queries, dtype=np.float32)
         nq, b = q.shape[0], int(self.info.padded_dim)

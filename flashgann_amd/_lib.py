@@ -22,7 +22,7 @@ FG_COUNTERS_PER_QUERY = 6
 
 EXPORTED = (
     "fg_index_create", "fg_index_load", "fg_index_destroy", "fg_index_get_info", "fg_search",
-    "fg_search_device", "fg_lds_bytes", "fg_query_prepare", "fg_score_edges", "fg_last_error",
+    "fg_search_device", "fg_search_profile", "fg_lds_bytes", "fg_query_prepare", "fg_score_edges", "fg_last_error",
     "fg_version",
 )
 
@@ -69,6 +69,7 @@ def lib():
         L.fg_search.argtypes = [vp, f32p, C.c_uint32, C.c_uint32, C.c_uint32, u32p, u32p,
                                 C.POINTER(Stats)]
         L.fg_search_device.argtypes = [vp, vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp, vp]
+        L.fg_search_profile.argtypes = [vp, vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp, vp]
         L.fg_lds_bytes.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32]
         L.fg_lds_bytes.restype = C.c_uint32
         L.fg_query_prepare.argtypes = [vp, f32p, C.c_uint32, f32p, u8p, f32p, i32p]

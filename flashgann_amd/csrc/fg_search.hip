@@ -110,7 +110,7 @@ __host__ __device__ inline uint32_t visited_bitlen(uint32_t beam, uint32_t degre
 }
 
 struct LdsLayout {
-    uint32_t hash_off, beam_off, cand_off, query_off, plane_off, scratch_off, total;
+    uint32_t hash_off, beam_off, cand_off, query_off, plane_off, scratch_off, prof_off, total;
 };
 
 // Per-query LDS: visited table (aliased by the rotated query during
@@ -119,14 +119,10 @@ struct LdsLayout {
 // scratch area (32-entry child list + parent lists).
 __host__ __device__ inline LdsLayout lds_layout(uint32_t dim, uint32_t padded_dim, uint32_t pbeam,
                                                 uint32_t bitlen) {
+    // fixed-size regions first (compile-time offsets for a fixed geometry),
+    // then the beam-dependent visited table and beam
     LdsLayout L;
     uint32_t off = 0;
-    L.hash_off = off;
-    uint32_t hash_bytes = (1u << bitlen) * 4u;
-    if (hash_bytes < padded_dim * 4u) hash_bytes = padded_dim * 4u;
-    off += hash_bytes;
-    L.beam_off = off;
-    off += pbeam * 8u;
     L.cand_off = off;
     off += 32u * 8u;
     L.query_off = off;
@@ -135,6 +131,16 @@ __host__ __device__ inline LdsLayout lds_layout(uint32_t dim, uint32_t padded_di
     off += 8u * (padded_dim / 32u) * 4u;
     L.scratch_off = off;
     off += (32u + 3u * 8u) * 4u;
+    off = (off + 7u) & ~7u;
+    L.prof_off = off;
+    off += 16u * 8u;
+    off = (off + 15u) & ~15u;
+    L.hash_off = off;
+    uint32_t hash_bytes = (1u << bitlen) * 4u;
+    if (hash_bytes < padded_dim * 4u) hash_bytes = padded_dim * 4u;
+    off += hash_bytes;
+    L.beam_off = off;
+    off += pbeam * 8u;
     L.total = (off + 15u) & ~15u;
     return L;
 }
@@ -145,6 +151,7 @@ struct SearchParams {
     const float *queries;
     uint32_t *results;
     uint32_t *counters;
+    unsigned long long *phase;  // per-query phase cycles (profiling build only)
     uint64_t npoints;
     uint64_t row_offset, code_offset, factor_offset, neighbor_offset;
     int dim, padded_dim, degree;
@@ -159,6 +166,31 @@ struct SearchParams {
     LdsLayout lds;
 };
 
+
+// Row geometry (include/qg.hpp:66-73), compile-time for the specialised
+// shapes (DIM_T, DEG_T > 0) so every field offset is an immediate, runtime
+// otherwise.
+__host__ __device__ constexpr int pow2_at_least(int d) { return d <= 1 ? 1 : 2 * pow2_at_least((d + 1) / 2); }
+
+template <int DIM_T, int DEG_T>
+struct Geo {
+    static constexpr bool kFixed = DIM_T > 0 && DEG_T > 0;
+    static constexpr int kB = kFixed ? pow2_at_least(DIM_T) : 0;
+    static constexpr int kFactor = DIM_T + kB / 64 * 2 * DEG_T;
+    static constexpr int kNbr = kFactor + 3 * DEG_T;
+    static constexpr int kRow = kNbr + DEG_T;
+    int dim, deg, B;
+    uint64_t row, code, factor, nbr;
+    __device__ __forceinline__ explicit Geo(const SearchParams &P)
+        : dim(kFixed ? DIM_T : P.dim),
+          deg(kFixed ? DEG_T : P.degree),
+          B(kFixed ? kB : P.padded_dim),
+          row(kFixed ? static_cast<uint64_t>(kRow) : P.row_offset),
+          code(kFixed ? static_cast<uint64_t>(DIM_T) : P.code_offset),
+          factor(kFixed ? static_cast<uint64_t>(kFactor) : P.factor_offset),
+          nbr(kFixed ? static_cast<uint64_t>(kNbr) : P.neighbor_offset) {}
+};
+
 // ------------------------------------------------------------ device helpers
 
 __device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & 63; }
@@ -169,26 +201,44 @@ __device__ __forceinline__ uint32_t half_bits(uint64_t m, int h) {
     return static_cast<uint32_t>(m >> (32 * h));
 }
 
-// Lane i reads lane i ^ m.  Masks below 32 stay inside a 32-lane half and use
-// DPP (1, 2: quad_perm; 4: half-row mirror then quad reverse, (i^7)^3 = i^4;
-// 8: row mirror then half-row mirror, (i^15)^7 = i^8) or ds_swizzle's bit mode
-// (16); 32 crosses halves through ds_bpermute.  Call with every lane active.
+// Lanes whose index has bit v set (v a power of two <= 32).
+__host__ __device__ constexpr uint64_t lane_bit_mask(int v) {
+    return v == 1    ? 0xAAAAAAAAAAAAAAAAull
+           : v == 2  ? 0xCCCCCCCCCCCCCCCCull
+           : v == 4  ? 0xF0F0F0F0F0F0F0F0ull
+           : v == 8  ? 0xFF00FF00FF00FF00ull
+           : v == 16 ? 0xFFFF0000FFFF0000ull
+           : v == 32 ? 0xFFFFFFFF00000000ull
+                     : 0ull;
+}
+
+// A uniform lane mask as this lane's bool (no instructions: the mask is the
+// condition register).
+__device__ __forceinline__ bool lane_in(uint64_t mask) { return __builtin_amdgcn_inverse_ballot_w64(mask); }
+
+// Lane i reads lane i ^ m, all lanes active.  m < 16 stays inside a 16-lane
+// row: DPP quad_perm (1, 2), half-row mirror then quad reverse
+// ((i^7)^3 = i^4), row mirror then half-row mirror ((i^15)^7 = i^8).  16 and
+// 32 use gfx950's permlane16/32 swaps (row pairs / wave halves exchanged
+// between two copies of the value) and keep the half this lane needs.
 __device__ __forceinline__ int xshfl(int v, int m) {
     switch (m) {
     case 1:
-        return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+        return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
     case 2:
-        return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
-    case 4: {
-        const int t = __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
-        return __builtin_amdgcn_update_dpp(0, t, 0x1B, 0xF, 0xF, false);
+        return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);
+    case 4:
+        return __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false), 0x1B, 0xF, 0xF, false);
+    case 8:
+        return __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, false), 0x141, 0xF, 0xF, false);
+    case 16: {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return lane_in(lane_bit_mask(16)) ? static_cast<int>(r[0]) : static_cast<int>(r[1]);
     }
-    case 8: {
-        const int t = __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);
-        return __builtin_amdgcn_update_dpp(0, t, 0x141, 0xF, 0xF, false);
+    case 32: {
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return lane_in(lane_bit_mask(32)) ? static_cast<int>(r[0]) : static_cast<int>(r[1]);
     }
-    case 16:
-        return __builtin_amdgcn_ds_swizzle(v, 0x401F);
     default:
         return __shfl_xor(v, m);
     }
@@ -348,14 +398,25 @@ __device__ __forceinline__ float half_distance(const float *__restrict__ row, co
 
 // ------------------------------------------------------------ sorting networks
 
-// One bitonic stage of block size kk over E positions per lane (position of
-// item e is base + e), compare distance j = jstart .. 1.  Cross-lane steps use
-// the reference's per-lane rule (utils.cuh:309-316, 340-341): lane takes its
-// partner's pair iff the keys differ and (k < pk) != p with
-// p = (pos & kk != 0) == (pos & j != 0).  In-lane steps are utils.cuh:319-328
-// with ascending = (pos_lo & kk) == 0.
-template <int E>
-__device__ __forceinline__ void bitonic_stage(float (&k)[E], uint32_t (&v)[E], int base, int kk, int jstart) {
+// Positions of a register layout: item e of lane l sits at position
+// E*l + e, or at l & 31 when HALF (both 32-lane halves hold the same 32
+// positions).  pos_bit(v, e) is the lane mask of items e whose position has
+// bit v set.
+template <int E, bool HALF>
+__device__ __forceinline__ uint64_t pos_bit(int v, int e) {
+    if (HALF) return v >= 32 ? 0ull : lane_bit_mask(v);
+    if (v < E) return (e & v) ? ~0ull : 0ull;
+    return lane_bit_mask(v / E);
+}
+
+// One bitonic stage of block size kk, compare distance j = jstart .. 1, on
+// the layout (E, HALF).  Cross-lane steps use the reference's per-lane rule
+// (utils.cuh:309-316, 340-341): a lane takes its partner's pair iff the keys
+// differ and (k < pk) != p with p = (pos & kk != 0) == (pos & j != 0).
+// In-lane steps are utils.cuh:319-328 with ascending = (pos_lo & kk) == 0.
+// Directions are uniform lane masks (compile-time after unrolling).
+template <int E, bool HALF>
+__device__ __forceinline__ void bitonic_stage(float (&k)[E], uint32_t (&v)[E], int kk, int jstart) {
 #pragma unroll
     for (int j = jstart; j >= 1; j >>= 1) {
         if (j >= E) {
@@ -364,8 +425,7 @@ __device__ __forceinline__ void bitonic_stage(float (&k)[E], uint32_t (&v)[E], i
             for (int e = 0; e < E; ++e) {
                 const float pk = xshfl(k[e], m);
                 const uint32_t pv = xshfl(v[e], m);
-                const int pos = base + e;
-                const bool p = ((pos & kk) != 0) == ((pos & j) != 0);
+                const bool p = lane_in(~(pos_bit<E, HALF>(kk, e) ^ pos_bit<E, HALF>(j, e)));
                 if (k[e] != pk && ((k[e] < pk) != p)) {
                     k[e] = pk;
                     v[e] = pv;
@@ -376,7 +436,7 @@ __device__ __forceinline__ void bitonic_stage(float (&k)[E], uint32_t (&v)[E], i
             for (int e = 0; e < E; ++e) {
                 if (e & j) continue;
                 const int hi = e | j;
-                const bool asc = ((base + e) & kk) == 0;
+                const bool asc = lane_in(~pos_bit<E, HALF>(kk, e));
                 if (k[e] != k[hi] && ((k[e] < k[hi]) != asc)) {
                     const float tk = k[e]; k[e] = k[hi]; k[hi] = tk;
                     const uint32_t tv = v[e]; v[e] = v[hi]; v[hi] = tv;
@@ -388,11 +448,11 @@ __device__ __forceinline__ void bitonic_stage(float (&k)[E], uint32_t (&v)[E], i
 
 // warp_sort<1> on 32 positions (utils.cuh:409-414): position = lane & 31, both
 // halves sort the same data.
-__device__ __forceinline__ void sort32(float &key, uint32_t &val, int nl) {
+__device__ __forceinline__ void sort32(float &key, uint32_t &val) {
     float k[1] = {key};
     uint32_t v[1] = {val};
 #pragma unroll
-    for (int kk = 2; kk <= 32; kk <<= 1) bitonic_stage<1>(k, v, nl, kk, kk >> 1);
+    for (int kk = 2; kk <= 32; kk <<= 1) bitonic_stage<1, true>(k, v, kk, kk >> 1);
     key = k[0];
     val = v[0];
 }
@@ -428,7 +488,7 @@ __device__ void merge_beam(const SearchParams &P, float *bd, uint32_t *bi, float
     const int cbs = P.cbs, pbeam = P.pbeam;
     float ck = nl < cbs ? cd[nl] : FLT_MAX;
     uint32_t cv = nl < cbs ? ci[nl] : kMaxIndex;
-    sort32(ck, cv, nl);
+    sort32(ck, cv);
     if (pbeam <= 128) {
         if (pbeam == 128) {
             float k[2];
@@ -446,7 +506,7 @@ __device__ void merge_beam(const SearchParams &P, float *bd, uint32_t *bi, float
                     v[e] = vv2;
                 }
             }
-            bitonic_stage<2>(k, v, base, 128, 64);
+            bitonic_stage<2, false>(k, v, 128, 64);
             __syncthreads();
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
@@ -464,8 +524,8 @@ __device__ void merge_beam(const SearchParams &P, float *bd, uint32_t *bi, float
                 k[0] = kk2;
                 v[0] = vv2;
             }
-            if (pbeam == 64) bitonic_stage<1>(k, v, pos, 64, 32);
-            else bitonic_stage<1>(k, v, pos, 32, 16);
+            if (pbeam == 64) bitonic_stage<1, false>(k, v, 64, 32);
+            else bitonic_stage<1, true>(k, v, 32, 16);
             __syncthreads();
             if (pbeam == 64 || h == 0) {
                 bd[pos] = k[0];
@@ -794,9 +854,9 @@ __device__ __forceinline__ int32_t raw_regs(const uint32_t (&c)[WT], const uint3
 // (or 0..n when slot_list is null): two children per pass, PB passes with
 // their row loads issued together (DPL > 0: dims per lane known at compile
 // time; DPL == 0: generic loop).
-template <int DPL>
-__device__ void exact_batch(const SearchParams &P, int n, const uint32_t *slot_list, float *cd, const uint32_t *ci,
-                            const float (&qr)[DPL > 0 ? DPL : 1], const float *qv) {
+template <int DPL, class G>
+__device__ void exact_batch(const SearchParams &P, const G &g, int n, const uint32_t *slot_list, float *cd,
+                            const uint32_t *ci, const float (&qr)[DPL > 0 ? DPL : 1], const float *qv) {
     const int lane = lane_id();
     const int h = lane >> 5, nl = lane & 31;
     const bool ip = P.use_ip != 0;
@@ -811,11 +871,11 @@ __device__ void exact_batch(const SearchParams &P, int n, const uint32_t *slot_l
                 const bool act = e < n;
                 slot[j] = act ? static_cast<int>(slot_list ? slot_list[e] : static_cast<uint32_t>(e)) : -1;
                 const uint32_t child = act ? ci[slot[j]] : 0u;
-                const float *row = P.data + static_cast<uint64_t>(child) * P.row_offset;
+                const float *row = P.data + static_cast<uint64_t>(child) * g.row;
 #pragma unroll
                 for (int k = 0; k < DPL; ++k) {
                     const int i = nl + 32 * k;
-                    v[j][k] = (act && i < P.dim) ? row[i] : 0.0f;
+                    v[j][k] = (act && i < g.dim) ? row[i] : 0.0f;
                 }
             }
             float acc[PB];
@@ -825,7 +885,7 @@ __device__ void exact_batch(const SearchParams &P, int n, const uint32_t *slot_l
 #pragma unroll
                 for (int k = 0; k < DPL; ++k) {
                     const int i = nl + 32 * k;
-                    if (i < P.dim) {
+                    if (i < g.dim) {
                         if (ip) {
                             acc[j] = fmaf(qr[k], v[j][k], acc[j]);
                         } else {
@@ -876,7 +936,7 @@ __device__ void exact_batch(const SearchParams &P, int n, const uint32_t *slot_l
             const bool act = e < n;
             const int slot = act ? static_cast<int>(slot_list ? slot_list[e] : static_cast<uint32_t>(e)) : 0;
             const uint32_t child = act ? ci[slot] : 0u;
-            const float d = half_distance(P.data + static_cast<uint64_t>(child) * P.row_offset, qv, P.dim, nl, ip, act);
+            const float d = half_distance(P.data + static_cast<uint64_t>(child) * g.row, qv, g.dim, nl, ip, act);
             if (act && nl == 0) cd[slot] = d;
         }
     }
@@ -888,16 +948,20 @@ __device__ void exact_batch(const SearchParams &P, int n, const uint32_t *slot_l
 __device__ __forceinline__ bool select_smallest(float value, bool valid, int keep_k, int max_k) {
     const int lane = lane_id();
     const int h = lane >> 5, nl = lane & 31;
+    // order-preserving unsigned image of the float; -0 joins +0 so equal
+    // values tie exactly as in the float comparison
+    const uint32_t bits = __float_as_uint(value == 0.0f ? 0.0f : value);
+    const uint32_t key = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
     bool remaining = valid;
     bool kept = false;
     for (int r = 0; r < max_k; ++r) {
-        float m = remaining ? value : INFINITY;
-        m = fminf(m, xshfl(m, 16));
-        m = fminf(m, xshfl(m, 8));
-        m = fminf(m, xshfl(m, 4));
-        m = fminf(m, xshfl(m, 2));
-        m = fminf(m, xshfl(m, 1));
-        const uint32_t cand = half_bits(ballot(remaining && value == m), h);
+        uint32_t m = remaining ? key : 0xFFFFFFFFu;
+        m = min(m, xshfl(m, 16));
+        m = min(m, xshfl(m, 8));
+        m = min(m, xshfl(m, 4));
+        m = min(m, xshfl(m, 2));
+        m = min(m, xshfl(m, 1));
+        const uint32_t cand = half_bits(ballot(remaining && key == m), h);
         const bool take = r < keep_k && cand != 0u && nl == __builtin_ctz(cand | (cand == 0u ? 1u : 0u));
         kept |= take;
         remaining &= !take;
@@ -938,34 +1002,67 @@ __device__ __forceinline__ void hash_contains_n(const uint32_t *t, int bitlen, c
     }
 }
 
-template <int WT, int DPL>
+// Phase timer for the profiling instantiation: cycles since the previous
+// mark are added to LDS counter `i` (s_memtime, per wave).
+#define FG_PHASE(i)                                                  \
+    do {                                                             \
+        if constexpr (PROF) {                                        \
+            const unsigned long long t_ = __builtin_amdgcn_s_memtime(); \
+            if (lane == 0) prof[i] += t_ - t_last;                   \
+            t_last = t_;                                             \
+        }                                                            \
+    } while (0)
+
+#define FG_COUNT(stmt)            \
+    do {                          \
+        if constexpr (COUNT) stmt; \
+    } while (0)
+
+template <int WT, int DPL, int DIM_T, int DEG_T, bool COUNT, bool PROF>
 __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int qid = blockIdx.x;
     if (qid >= P.nq) return;
     const int lane = lane_id();
     const int h = lane >> 5, nl = lane & 31;
-    const int B = P.padded_dim, W = B >> 5;
-    const int deg = P.degree;
+    const Geo<DIM_T, DEG_T> g(P);
+    const int B = g.B, W = B >> 5;
+    const int deg = g.deg;
     const int bitlen = P.bitlen;
     const bool vec_ok = P.vec_ok != 0;
 
+    // fixed-size regions at compile-time offsets for the specialised shapes
+    constexpr bool kFixedGeo = Geo<DIM_T, DEG_T>::kFixed;
+    constexpr uint32_t kQueryOff = 256u;
+    constexpr uint32_t kPlaneOff = kQueryOff + ((DIM_T + 3u) & ~3u) * 4u;
+    constexpr uint32_t kScratchOff = kPlaneOff + 8u * (Geo<DIM_T, DEG_T>::kB / 32u) * 4u;
+    constexpr uint32_t kProfOff = (kScratchOff + (32u + 3u * 8u) * 4u + 7u) & ~7u;
+    const uint32_t query_off = kFixedGeo ? kQueryOff : P.lds.query_off;
+    const uint32_t plane_off = kFixedGeo ? kPlaneOff : P.lds.plane_off;
+    const uint32_t scratch_off = kFixedGeo ? kScratchOff : P.lds.scratch_off;
+    const uint32_t prof_off = kFixedGeo ? kProfOff : P.lds.prof_off;
     uint32_t *H = reinterpret_cast<uint32_t *>(smem + P.lds.hash_off);
     float *bd0 = reinterpret_cast<float *>(smem + P.lds.beam_off);
     uint32_t *bi0 = reinterpret_cast<uint32_t *>(bd0 + P.pbeam);
-    float *cd = reinterpret_cast<float *>(smem + P.lds.cand_off);
+    float *cd = reinterpret_cast<float *>(smem);
     uint32_t *ci = reinterpret_cast<uint32_t *>(cd + 32);
-    float *qv = reinterpret_cast<float *>(smem + P.lds.query_off);
-    uint32_t *planes = reinterpret_cast<uint32_t *>(smem + P.lds.plane_off);
-    uint32_t *alist = reinterpret_cast<uint32_t *>(smem + P.lds.scratch_off);
+    float *qv = reinterpret_cast<float *>(smem + query_off);
+    uint32_t *planes = reinterpret_cast<uint32_t *>(smem + plane_off);
+    uint32_t *alist = reinterpret_cast<uint32_t *>(smem + scratch_off);
     uint32_t *plist = alist + 32;
     uint32_t *pnode = plist + 8;
     float *pdist = reinterpret_cast<float *>(pnode + 8);
+    unsigned long long *prof = reinterpret_cast<unsigned long long *>(smem + prof_off);
+    unsigned long long t_last = 0;
+    if constexpr (PROF) {
+        if (lane < 16) prof[lane] = 0;
+        t_last = __builtin_amdgcn_s_memtime();
+    }
 
     // ---- query preparation (the visited table's LDS holds the rotation)
     float qlow, qhigh, qwidth;
     int sum_q;
-    prepare_query(P.queries + static_cast<uint64_t>(qid) * P.dim, P.signs, P.dim, B, reinterpret_cast<float *>(H),
+    prepare_query(P.queries + static_cast<uint64_t>(qid) * g.dim, P.signs, g.dim, B, reinterpret_cast<float *>(H),
                   qv, planes, qlow, qhigh, qwidth, sum_q, nullptr);
     constexpr int WTR = WT > 0 ? WT : 1;
     bool any_wrap = false;
@@ -980,7 +1077,7 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
 #pragma unroll
     for (int k = 0; k < DPLR; ++k) {
         const int i = nl + 32 * k;
-        qr[k] = (DPL > 0 && i < P.dim) ? qv[i] : 0.0f;
+        qr[k] = (DPL > 0 && i < g.dim) ? qv[i] : 0.0f;
     }
 
     // ---- state (adaptive_search.cuh:67-107)
@@ -994,7 +1091,7 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
         ci[lane] = kMaxIndex;
     }
     __syncthreads();
-    const float entry_d = uni(half_distance(P.data + static_cast<uint64_t>(P.entry) * P.row_offset, qv, P.dim, nl,
+    const float entry_d = uni(half_distance(P.data + static_cast<uint64_t>(P.entry) * g.row, qv, g.dim, nl,
                                             P.use_ip != 0, true));
     if (lane == 0) {
         cd[0] = entry_d;
@@ -1009,6 +1106,7 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
     const int cbs = P.cbs;
     const float *data = P.data;
 
+    FG_PHASE(0);
     for (int iter = 0; iter < kMaxIterations; ++iter) {
         float *bd = bd0;
         uint32_t *bi = bi0;
@@ -1018,9 +1116,11 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
             for (int i = lane; i < beam_sz; i += 64) hash_insert(H, bitlen, bi[i] & ~kMsb);
             __syncthreads();
         }
+        FG_PHASE(1);
         if (iter >= P.max_iter) break;
 
         merge_beam(P, bd, bi, cd, ci);
+        FG_PHASE(2);
         for (int i = beam_sz + lane; i < pbeam; i += 64) {
             bd[i] = FLT_MAX;
             bi[i] = kMaxIndex;
@@ -1058,8 +1158,8 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
         }
         __syncthreads();
         if (nexp == 0) break;
-        c_iters++;
-        c_exp += nexp;
+        FG_COUNT(c_iters++);
+        FG_COUNT(c_exp += nexp);
         if (lane < static_cast<int>(nexp)) {
             const uint32_t pos = plist[lane];
             pnode[lane] = bi[pos] & 0x7fffffffu;
@@ -1070,18 +1170,31 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
         ctl.last_e = finite_below_max(ctl.cur_e) ? ctl.cur_e : ctl.entry_d;
         ctl.cur_e = uni(pdist[nexp - 1]);
         const bool kth_valid = finite_below_max(kth);
+        FG_PHASE(3);
 
         if (theta <= 1) {
             // ---------------- single expander (adaptive_search.cuh:221-343)
             const int cwc = deg < cbs ? deg : cbs;
             const uint32_t parent = uni(pnode[0]);
             const float pd0 = uni(pdist[0]);
-            const float *prow = data + static_cast<uint64_t>(parent) * P.row_offset;
-            const uint32_t *nbrs = reinterpret_cast<const uint32_t *>(prow + P.neighbor_offset);
-            c_ids += static_cast<uint32_t>(cwc);
+            const float *prow = data + static_cast<uint64_t>(parent) * g.row;
+            const uint32_t *nbrs = reinterpret_cast<const uint32_t *>(prow + g.nbr);
+            FG_COUNT(c_ids += static_cast<uint32_t>(cwc));
             uint32_t child = kMaxIndex;
+            float tx = 0.0f, fdq = 0.0f, fvq = 0.0f;
+            uint32_t c1[1][WTR];
+#pragma unroll
+            for (int w = 0; w < WTR; ++w) c1[0][w] = 0u;
             if (nl < cwc) {
+                // id, factors and code issued together (one HBM round trip)
+                const float *factors = prow + g.factor;
                 child = nbrs[nl];
+                tx = factors[nl];
+                fdq = factors[deg + nl];
+                fvq = factors[2 * deg + nl];
+                if constexpr (WT > 0)
+                    load_code<WT>(reinterpret_cast<const uint32_t *>(prow + g.code) + static_cast<uint64_t>(nl) * WT,
+                                  vec_ok, c1[0]);
                 if (child >= P.npoints || hash_contains(H, bitlen, child)) child = kMaxIndex;
             }
             const uint32_t vmask = half_bits(ballot(child != kMaxIndex), 0);
@@ -1091,21 +1204,15 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
             float dist = child == kMaxIndex ? FLT_MAX : 0.0f;
             uint32_t admit_mask;
             if (!keep_all) {
-                c_est += static_cast<uint32_t>(valid_count);
-                const float *factors = prow + P.factor_offset;
-                const uint32_t *codes = reinterpret_cast<const uint32_t *>(prow + P.code_offset);
+                FG_COUNT(c_est += static_cast<uint32_t>(valid_count));
+                const uint32_t *codes = reinterpret_cast<const uint32_t *>(prow + g.code);
                 const bool valid = child != kMaxIndex;
                 float est = FLT_MAX;
+                int32_t r1[1] = {0};
+                if constexpr (WT > 0) raw_batch<1, WT>(c1, planes, any_wrap, r1);
                 if (valid) {
-                    const float tx = factors[nl];
-                    const float fdq = factors[deg + nl];
-                    const float fvq = factors[2 * deg + nl];
                     int32_t raw;
                     if constexpr (WT > 0) {
-                        uint32_t c[1][WT];
-                        load_code<WT>(codes + static_cast<uint64_t>(nl) * WT, vec_ok, c[0]);
-                        int32_t r1[1];
-                        raw_batch<1, WT>(c, planes, any_wrap, r1);
                         raw = r1[0];
                     } else {
                         raw = raw_partial(codes + static_cast<uint64_t>(nl) * W, 0, W, planes, W);
@@ -1124,7 +1231,7 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
                 // dispatch_candidate_bitonic_sort over the cbs-entry buffer (padding beyond it)
                 float sk = nl < cbs ? dist : FLT_MAX;
                 uint32_t sv = nl < cbs ? child : kMaxIndex;
-                sort32(sk, sv, nl);
+                sort32(sk, sv);
                 dist = sk;
                 child = sv;
                 if (nl >= eff) {
@@ -1155,11 +1262,13 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
             }
             __syncthreads();
             const int nins = __popc(ins_mask);
-            c_exact += static_cast<uint32_t>(nins);
-            exact_batch<DPL>(P, nins, alist, cd, ci, qr, qv);
+            FG_COUNT(c_exact += static_cast<uint32_t>(nins));
+            FG_PHASE(4);
+            exact_batch<DPL>(P, g, nins, alist, cd, ci, qr, qv);
+            FG_PHASE(5);
         } else {
             // ---------------- speculative expansion (adaptive_search.cuh:344-444)
-            if (c_st2 == kMaxIndex) c_st2 = static_cast<uint32_t>(iter);
+            FG_COUNT(if (c_st2 == kMaxIndex) c_st2 = static_cast<uint32_t>(iter));
             const int tiles = (deg + 31) / 32;
             const int tasks = static_cast<int>(nexp) * tiles;
             uint32_t compact = 0;
@@ -1169,6 +1278,8 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
                 bool val[SR];
                 int an[SR], tsk[SR], pix[SR];
                 const float *prw[SR];
+                float tx[SR], fdq[SR], fvq[SR];
+                uint32_t code[SR][WTR];
                 // (a) neighbour ids of the round's 8 tasks, loads issued together
 #pragma unroll
                 for (int sr = 0; sr < SR; ++sr) {
@@ -1179,12 +1290,29 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
                     const int nidx = tile * 32 + nl;
                     tsk[sr] = tact ? tile * 32 : -1;
                     pix[sr] = pidx;
-                    prw[sr] = data + static_cast<uint64_t>(pnode[pidx]) * P.row_offset;
-                    cid[sr] = (tact && nidx < deg) ? reinterpret_cast<const uint32_t *>(prw[sr] + P.neighbor_offset)[nidx]
+                    prw[sr] = data + static_cast<uint64_t>(pnode[pidx]) * g.row;
+                    cid[sr] = (tact && nidx < deg) ? reinterpret_cast<const uint32_t *>(prw[sr] + g.nbr)[nidx]
                                                    : kMaxIndex;
+                    // the neighbour's factors and code are issued with its id: their addresses
+                    // do not depend on it, and most lanes need them (one HBM round trip)
+                    tx[sr] = FLT_MAX;
+                    fdq[sr] = 0.0f;
+                    fvq[sr] = 0.0f;
+#pragma unroll
+                    for (int w = 0; w < WTR; ++w) code[sr][w] = 0u;
+                    if (tact && nidx < deg) {
+                        const float *factors = prw[sr] + g.factor;
+                        tx[sr] = factors[nidx];
+                        fdq[sr] = factors[deg + nidx];
+                        fvq[sr] = factors[2 * deg + nidx];
+                        if constexpr (WT > 0)
+                            load_code<WT>(reinterpret_cast<const uint32_t *>(prw[sr] + g.code) +
+                                              static_cast<uint64_t>(nidx) * WT,
+                                          vec_ok, code[sr]);
+                    }
                     int a = tact ? deg - tile * 32 : 0;
                     an[sr] = a > 32 ? 32 : a;
-                    c_ids += static_cast<uint32_t>(__popcll(ballot(tact && nidx < deg)));
+                    FG_COUNT(c_ids += static_cast<uint32_t>(__popcll(ballot(tact && nidx < deg))));
                 }
                 // (b) visited test against the table as it stood at the round's start
 #pragma unroll
@@ -1193,31 +1321,14 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
                 // (c) which tasks need estimates; their codes and factors, loads issued together
                 bool need[SR];
                 int keep[SR];
-                float tx[SR], fdq[SR], fvq[SR];
-                uint32_t code[SR][WTR];
 #pragma unroll
                 for (int sr = 0; sr < SR; ++sr) {
                     const int rvc = __popc(half_bits(ballot(val[sr]), h));
                     keep[sr] = tsk[sr] >= 0 ? keep_count_for_expander(static_cast<uint32_t>(an[sr]), theta, ctl.rho, false, 0) : 0;
                     need[sr] = !(keep[sr] >= rvc);
-                    tx[sr] = FLT_MAX;
-                    fdq[sr] = 0.0f;
-                    fvq[sr] = 0.0f;
-#pragma unroll
-                    for (int w = 0; w < WTR; ++w) code[sr][w] = 0u;
-                    if (need[sr] && val[sr]) {
-                        const int nidx = tsk[sr] + nl;
-                        const float *factors = prw[sr] + P.factor_offset;
-                        tx[sr] = factors[nidx];
-                        fdq[sr] = factors[deg + nidx];
-                        fvq[sr] = factors[2 * deg + nidx];
-                        if constexpr (WT > 0)
-                            load_code<WT>(reinterpret_cast<const uint32_t *>(prw[sr] + P.code_offset) +
-                                              static_cast<uint64_t>(nidx) * WT,
-                                          vec_ok, code[sr]);
-                    }
-                    c_est += static_cast<uint32_t>(__popcll(ballot(need[sr] && val[sr])));
+                    FG_COUNT(c_est += static_cast<uint32_t>(__popcll(ballot(need[sr] && val[sr]))));
                 }
+                FG_PHASE(6);
                 // (d) estimates, kth-near counts, keep decisions
                 uint32_t kept_mask[kSearchWidth];
                 bool keepl[SR];
@@ -1233,7 +1344,7 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
                                 raw = rawb[sr];
                             } else {
                                 const int nidx = tsk[sr] + nl;
-                                raw = raw_partial(reinterpret_cast<const uint32_t *>(prw[sr] + P.code_offset) +
+                                raw = raw_partial(reinterpret_cast<const uint32_t *>(prw[sr] + g.code) +
                                                       static_cast<uint64_t>(nidx) * W,
                                                   0, W, planes, W);
                             }
@@ -1295,12 +1406,15 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
                 __syncthreads();
             }
             if (compact > static_cast<uint32_t>(P.collect_cap)) compact = static_cast<uint32_t>(P.collect_cap);
-            c_exact += compact;
-            exact_batch<DPL>(P, static_cast<int>(compact), nullptr, cd, ci, qr, qv);
+            FG_COUNT(c_exact += compact);
+            FG_PHASE(7);
+            exact_batch<DPL>(P, g, static_cast<int>(compact), nullptr, cd, ci, qr, qv);
+            FG_PHASE(8);
         }
         __syncthreads();
     }
 
+    FG_PHASE(3);
     merge_beam(P, bd0, bi0, cd, ci);
     const uint32_t *bi = bi0;
     // result writer (adaptive_search.cuh:455-464)
@@ -1308,7 +1422,11 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
         const uint32_t r = i < beam_sz ? (bi[i] & 0x7fffffffu) : (bi[beam_sz - 1] & 0x7fffffffu);
         P.results[static_cast<uint64_t>(qid) * P.K + i] = r;
     }
-    if (P.counters && lane == 0) {
+    FG_PHASE(9);
+    if constexpr (PROF) {
+        if (lane < 10) P.phase[static_cast<uint64_t>(qid) * 10 + lane] = prof[lane];
+    }
+    if (COUNT && P.counters && lane == 0) {
         uint32_t *c = P.counters + static_cast<uint64_t>(qid) * FG_COUNTERS_PER_QUERY;
         c[0] = c_iters;
         c[1] = c_exp;
@@ -1526,22 +1644,44 @@ int make_params(fg_index *ix, uint32_t nq, uint32_t K, uint32_t beam, SearchPara
     return FG_OK;
 }
 
-int launch(fg_index *ix, const SearchParams &P, hipStream_t stream) {
+template <int WT, int DPL, int DIM_T, int DEG_T>
+void launch_geo(const SearchParams &P, hipStream_t stream, bool count, bool prof) {
+    const dim3 grid(P.nq), block(64);
+    if (prof)
+        hipLaunchKernelGGL((fg_search_kernel<WT, DPL, DIM_T, DEG_T, false, true>), grid, block, P.lds.total, stream, P);
+    else if (count)
+        hipLaunchKernelGGL((fg_search_kernel<WT, DPL, DIM_T, DEG_T, true, false>), grid, block, P.lds.total, stream, P);
+    else
+        hipLaunchKernelGGL((fg_search_kernel<WT, DPL, DIM_T, DEG_T, false, false>), grid, block, P.lds.total, stream, P);
+}
+
+// Shape classes: the benchmark shapes (d 128 / deg 32; d 96 / deg 32 and 16)
+// get fully compile-time geometry; other shapes use runtime offsets.
+template <bool PROF>
+int launch_t(const SearchParams &P, hipStream_t stream) {
     if (P.nq == 0) return FG_OK;
+    const bool count = P.counters != nullptr;
     const int W = P.padded_dim / 32;
-    if (W == 2 && P.dim <= 64) {
-        hipLaunchKernelGGL((fg_search_kernel<2, 2>), dim3(P.nq), dim3(64), P.lds.total, stream, P);
+    if (P.dim == 128 && P.degree == 32) {
+        launch_geo<4, 4, 128, 32>(P, stream, count, PROF);
+    } else if (P.dim == 96 && P.degree == 32) {
+        launch_geo<4, 3, 96, 32>(P, stream, count, PROF);
+    } else if (P.dim == 96 && P.degree == 16) {
+        launch_geo<4, 3, 96, 16>(P, stream, count, PROF);
+    } else if (W == 2 && P.dim <= 64) {
+        launch_geo<2, 2, 0, 0>(P, stream, count, PROF);
     } else if (W == 4 && P.dim <= 96) {
-        hipLaunchKernelGGL((fg_search_kernel<4, 3>), dim3(P.nq), dim3(64), P.lds.total, stream, P);
+        launch_geo<4, 3, 0, 0>(P, stream, count, PROF);
     } else if (W == 4) {
-        hipLaunchKernelGGL((fg_search_kernel<4, 4>), dim3(P.nq), dim3(64), P.lds.total, stream, P);
+        launch_geo<4, 4, 0, 0>(P, stream, count, PROF);
     } else {
-        hipLaunchKernelGGL((fg_search_kernel<0, 0>), dim3(P.nq), dim3(64), P.lds.total, stream, P);
+        launch_geo<0, 0, 0, 0>(P, stream, count, PROF);
     }
     FG_HIP(hipGetLastError(), "search kernel launch");
-    (void)ix;
     return FG_OK;
 }
+
+int launch(fg_index *, const SearchParams &P, hipStream_t stream) { return launch_t<false>(P, stream); }
 
 bool rows_dup_free(const float *rows, uint64_t n, uint32_t degree, uint64_t nbr_off, uint64_t row_off) {
     std::vector<uint32_t> tmp(degree);
@@ -1675,7 +1815,21 @@ int fg_search_device(fg_index *ix, const float *d_queries, uint32_t nq, uint32_t
     P.queries = d_queries;
     P.results = d_results;
     P.counters = d_counters;
+    P.phase = nullptr;
     return launch(ix, P, reinterpret_cast<hipStream_t>(stream));
+}
+
+int fg_search_profile(fg_index *ix, const float *d_queries, uint32_t nq, uint32_t K, uint32_t beam,
+                      uint32_t *d_results, unsigned long long *d_phase, void *stream) {
+    if (!ix) return fail(FG_EINVAL, "index is NULL");
+    if (nq && (!d_queries || !d_results || !d_phase)) return fail(FG_EINVAL, "NULL device buffer");
+    SearchParams P;
+    if (int rc = make_params(ix, nq, K, beam, P)) return rc;
+    P.queries = d_queries;
+    P.results = d_results;
+    P.counters = nullptr;
+    P.phase = d_phase;
+    return launch_t<true>(P, reinterpret_cast<hipStream_t>(stream));
 }
 
 int fg_search(fg_index *ix, const float *queries, uint32_t nq, uint32_t K, uint32_t beam, uint32_t *result_ids,
@@ -1703,6 +1857,7 @@ int fg_search(fg_index *ix, const float *queries, uint32_t nq, uint32_t K, uint3
     P.queries = ix->d_q;
     P.results = ix->d_res;
     P.counters = counters ? ix->d_cnt : nullptr;
+    P.phase = nullptr;
     const auto t0 = std::chrono::high_resolution_clock::now();
     FG_HIP(hipEventRecord(ix->ev0, nullptr), "event record");
     if (int rc = launch(ix, P, nullptr)) return rc;

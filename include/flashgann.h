@@ -99,6 +99,16 @@ int fg_search(fg_index *index, const float *queries, uint32_t nq, uint32_t K, ui
 int fg_search_device(fg_index *index, const float *d_queries, uint32_t nq, uint32_t K,
                      uint32_t beam, uint32_t *d_results, uint32_t *d_counters, void *stream);
 
+/* Diagnostics: the same search as fg_search_device, built with phase timers.
+ * d_phase receives 10 uint64 per query: s_memtime cycles spent in query
+ * preparation + set-up, visited-table restore, beam merge, controller + pick,
+ * single-expander scoring, single-expander exact distances, speculative id
+ * loads + visited tests, speculative estimates + selection + inserts,
+ * speculative exact distances, and the final merge + result write.  No
+ * counterpart in the reference (its only diagnostics are printfs). */
+int fg_search_profile(fg_index *index, const float *d_queries, uint32_t nq, uint32_t K, uint32_t beam,
+                      uint32_t *d_results, unsigned long long *d_phase, void *stream);
+
 /* Dynamic LDS bytes one query's workgroup needs (the analogue of
  * calculate_shared_mem_size, src/adaptive_search_utils.cuh:152-176). */
 uint32_t fg_lds_bytes(uint32_t dim, uint32_t beam, uint32_t degree);

@@ -72,3 +72,17 @@ def test_search_entry_auto(gpu_available):
     ix.close()
     ids, cnt, rids, rcnt = _run(cb, q, 10, 64, entry=0xFFFFFFFF)
     _assert_equal(ids, cnt, rids, rcnt, "entry auto")
+
+
+@pytest.mark.parametrize("dim,degree,kind", [(128, 32, "int"), (96, 16, "unit"), (100, 32, "int"), (64, 32, "int")])
+def test_timed_instantiation_matches_counting_one(gpu_available, dim, degree, kind):
+    """The kernel built without work counters (the one bench.py times) returns
+    the same ids as the counting build the parity tests compare."""
+    from flashgann_amd import Index
+    cb, q, _ = small_index(n=2500, dim=dim, degree=degree, kind=kind, comps=16)
+    ix = Index.from_codebook(cb)
+    for K, beam in [(10, 64), (100, 256)]:
+        a, _, _ = ix.search(q, K, beam, counters=True)
+        b, _, _ = ix.search(q, K, beam, counters=False)
+        assert np.array_equal(a, b), (dim, degree, K, beam)
+    ix.close()
