@@ -18,7 +18,7 @@ import numpy as np
 
 from . import _lib
 from ._lib import (FG_COUNTERS_PER_QUERY, FG_ENTRY_AUTO, FG_METRIC_IP, FG_METRIC_L2,
-                   FlashGannError, IndexInfo, Stats, check, lib)
+                   FG_PROFILE_SLOTS, FlashGannError, IndexInfo, Stats, check, lib)
 from .codebook import Codebook, Layout, read_codebook
 
 METRIC_L2 = FG_METRIC_L2
@@ -117,7 +117,9 @@ class Index:
 
     def search_profile(self, queries_ptr: int, nq: int, K: int, beam: int, results_ptr: int,
                        phase_ptr: int, stream: int = 0) -> None:
-        """Profiling build of the search: 10 uint64 phase-cycle sums per query."""
+        """Profiling build of the search: per query, 10 uint64 phase-cycle sums
+        followed by the start and end time on the 100 MHz device clock
+        (FG_PROFILE_SLOTS values)."""
         check(lib().fg_search_profile(self._h, C.c_void_p(queries_ptr), nq, K, beam,
                                       C.c_void_p(results_ptr), C.c_void_p(phase_ptr),
                                       C.c_void_p(stream or None)))

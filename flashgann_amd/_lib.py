@@ -19,6 +19,7 @@ FG_METRIC_L2 = 0
 FG_METRIC_IP = 1
 FG_ENTRY_AUTO = 0xFFFFFFFF
 FG_COUNTERS_PER_QUERY = 6
+FG_PROFILE_SLOTS = 12
 
 EXPORTED = (
     "fg_index_create", "fg_index_load", "fg_index_destroy", "fg_index_get_info", "fg_search",

@@ -110,38 +110,52 @@ __host__ __device__ inline uint32_t visited_bitlen(uint32_t beam, uint32_t degre
 }
 
 struct LdsLayout {
-    uint32_t hash_off, beam_off, cand_off, query_off, plane_off, scratch_off, prof_off, total;
+    uint32_t hash_off, beam_off, cand_off, msort_off, query_off, plane_off, scratch_off, prof_off, total,
+        total_prof;
 };
 
+// Sorted-candidate staging for the beam merge: (distance, id) pairs at
+// indices -1 .. kMsortHi, the 32 sorted candidates at 0..31 between a
+// -FLT_MAX sentinel (index -1) and FLT_MAX sentinels (32 and up).
+constexpr int kMsortHi = 35;
+constexpr uint32_t kMsortPairs = 40;
+// Beam: (distance, id) pairs at indices -1 .. pbeam + kBeamPad - 1: a
+// -FLT_MAX sentinel, the pbeam entries, a FLT_MAX sentinel at pbeam, then pad
+// entries (segment reads may run up to 3 past pbeam; the merge's unused
+// slots are written to pbeam + 2).
+constexpr uint32_t kBeamPad = 4;
+
 // Per-query LDS: visited table (aliased by the rotated query during
-// preparation), the beam, the
-// 32-entry candidate buffer, the raw query, 8 x B/32 plane words and a small
-// scratch area (32-entry child list + parent lists).
-__host__ __device__ inline LdsLayout lds_layout(uint32_t dim, uint32_t padded_dim, uint32_t pbeam,
-                                                uint32_t bitlen) {
+// preparation), the beam, the 32-entry candidate buffer, the sorted-candidate
+// staging area, the raw query, 8 x B/32 plane words and a small scratch area
+// (32-entry child list + parent lists).
+__host__ __device__ constexpr LdsLayout lds_layout(uint32_t dim, uint32_t padded_dim, uint32_t pbeam,
+                                                   uint32_t bitlen) {
     // fixed-size regions first (compile-time offsets for a fixed geometry),
     // then the beam-dependent visited table and beam
-    LdsLayout L;
+    LdsLayout L{};
     uint32_t off = 0;
     L.cand_off = off;
     off += 32u * 8u;
+    L.msort_off = off;
+    off += kMsortPairs * 8u;
     L.query_off = off;
     off += ((dim + 3u) & ~3u) * 4u;
     L.plane_off = off;
     off += 8u * (padded_dim / 32u) * 4u;
     L.scratch_off = off;
     off += (32u + 3u * 8u) * 4u;
-    off = (off + 7u) & ~7u;
-    L.prof_off = off;
-    off += 16u * 8u;
     off = (off + 15u) & ~15u;
     L.hash_off = off;
     uint32_t hash_bytes = (1u << bitlen) * 4u;
     if (hash_bytes < padded_dim * 4u) hash_bytes = padded_dim * 4u;
     off += hash_bytes;
     L.beam_off = off;
-    off += pbeam * 8u;
+    off += (pbeam + 1u + kBeamPad) * 8u;
     L.total = (off + 15u) & ~15u;
+    // phase timers of the profiling build only, past the end of the rest
+    L.prof_off = L.total;
+    L.total_prof = L.total + 16u * 8u;
     return L;
 }
 
@@ -151,12 +165,14 @@ struct SearchParams {
     const float *queries;
     uint32_t *results;
     uint32_t *counters;
-    unsigned long long *phase;  // per-query phase cycles (profiling build only)
+    unsigned long long *phase;  // per-query phase cycles + start/end time (profiling build only)
     uint64_t npoints;
     uint64_t row_offset, code_offset, factor_offset, neighbor_offset;
     int dim, padded_dim, degree;
     int K, beam, pbeam, cbs, collect_cap;
     int bitlen, max_iter;
+    int seg_active;      // merge-path segments (pbeam > 128)
+    uint32_t seg_magic;  // floor(2^32 / seg_active) + 1: t * pbeam / seg_active by one mulhi
     float phase2_rho;
     int use_ip;
     int dup_free;
@@ -194,6 +210,15 @@ struct Geo {
 // ------------------------------------------------------------ device helpers
 
 __device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & 63; }
+
+// The lane id through an empty asm: values derived from it are computed where
+// they are used instead of being hoisted out of the search loop, where they
+// would hold registers through every phase of every iteration.
+__device__ __forceinline__ int lane_id_opaque() {
+    int l = lane_id();
+    asm volatile("" : "+v"(l));
+    return l;
+}
 
 __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
 
@@ -409,41 +434,53 @@ __device__ __forceinline__ uint64_t pos_bit(int v, int e) {
     return lane_bit_mask(v / E);
 }
 
-// One bitonic stage of block size kk, compare distance j = jstart .. 1, on
-// the layout (E, HALF).  Cross-lane steps use the reference's per-lane rule
-// (utils.cuh:309-316, 340-341): a lane takes its partner's pair iff the keys
-// differ and (k < pk) != p with p = (pos & kk != 0) == (pos & j != 0).
-// In-lane steps are utils.cuh:319-328 with ascending = (pos_lo & kk) == 0.
-// Directions are uniform lane masks (compile-time after unrolling).
-template <int E, bool HALF>
-__device__ __forceinline__ void bitonic_stage(float (&k)[E], uint32_t (&v)[E], int kk, int jstart) {
+// One compare-exchange step of a bitonic network, block size KK and compare
+// distance J, on the layout (E, HALF).  Cross-lane steps use the reference's
+// per-lane rule (utils.cuh:309-316, 340-341): a lane takes its partner's pair
+// iff the keys differ and (k < pk) != p with p = (pos & KK != 0) ==
+// (pos & J != 0).  In-lane steps are utils.cuh:319-328 with ascending =
+// (pos_lo & KK) == 0.  KK and J are template arguments so that every step is
+// straight-line code with immediate lane masks and shuffle patterns.
+template <int E, bool HALF, int KK, int J>
+__device__ __forceinline__ void bitonic_step(float (&k)[E], uint32_t (&v)[E]) {
+    if constexpr (J >= E) {
+        constexpr int M = J / E;
 #pragma unroll
-    for (int j = jstart; j >= 1; j >>= 1) {
-        if (j >= E) {
-            const int m = j / E;
-#pragma unroll
-            for (int e = 0; e < E; ++e) {
-                const float pk = xshfl(k[e], m);
-                const uint32_t pv = xshfl(v[e], m);
-                const bool p = lane_in(~(pos_bit<E, HALF>(kk, e) ^ pos_bit<E, HALF>(j, e)));
-                if (k[e] != pk && ((k[e] < pk) != p)) {
-                    k[e] = pk;
-                    v[e] = pv;
-                }
+        for (int e = 0; e < E; ++e) {
+            const float pk = xshfl(k[e], M);
+            const uint32_t pv = xshfl(v[e], M);
+            const bool p = lane_in(~(pos_bit<E, HALF>(KK, e) ^ pos_bit<E, HALF>(J, e)));
+            if (k[e] != pk && ((k[e] < pk) != p)) {
+                k[e] = pk;
+                v[e] = pv;
             }
-        } else {
+        }
+    } else {
 #pragma unroll
-            for (int e = 0; e < E; ++e) {
-                if (e & j) continue;
-                const int hi = e | j;
-                const bool asc = lane_in(~pos_bit<E, HALF>(kk, e));
-                if (k[e] != k[hi] && ((k[e] < k[hi]) != asc)) {
-                    const float tk = k[e]; k[e] = k[hi]; k[hi] = tk;
-                    const uint32_t tv = v[e]; v[e] = v[hi]; v[hi] = tv;
-                }
+        for (int e = 0; e < E; ++e) {
+            if (e & J) continue;
+            const int hi = e | J;
+            const bool asc = lane_in(~pos_bit<E, HALF>(KK, e));
+            if (k[e] != k[hi] && ((k[e] < k[hi]) != asc)) {
+                const float tk = k[e]; k[e] = k[hi]; k[hi] = tk;
+                const uint32_t tv = v[e]; v[e] = v[hi]; v[hi] = tv;
             }
         }
     }
+}
+
+// The steps J, J/2, .. 1 of block size KK.
+template <int E, bool HALF, int KK, int J>
+__device__ __forceinline__ void bitonic_stage(float (&k)[E], uint32_t (&v)[E]) {
+    bitonic_step<E, HALF, KK, J>(k, v);
+    if constexpr (J > 1) bitonic_stage<E, HALF, KK, J / 2>(k, v);
+}
+
+// Block sizes KK, 2 KK, .. 32 on the HALF layout.
+template <int KK>
+__device__ __forceinline__ void sort32_from(float (&k)[1], uint32_t (&v)[1]) {
+    bitonic_stage<1, true, KK, KK / 2>(k, v);
+    if constexpr (KK < 32) sort32_from<KK * 2>(k, v);
 }
 
 // warp_sort<1> on 32 positions (utils.cuh:409-414): position = lane & 31, both
@@ -451,214 +488,168 @@ __device__ __forceinline__ void bitonic_stage(float (&k)[E], uint32_t (&v)[E], i
 __device__ __forceinline__ void sort32(float &key, uint32_t &val) {
     float k[1] = {key};
     uint32_t v[1] = {val};
-#pragma unroll
-    for (int kk = 2; kk <= 32; kk <<= 1) bitonic_stage<1, true>(k, v, kk, kk >> 1);
+    sort32_from<2>(k, v);
     key = k[0];
     val = v[0];
 }
 
-// utils.cuh:588-616
-__device__ __forceinline__ int merge_path_partition(const float *a, int na, const float *b, int nb, int diag) {
-    int low = diag - nb > 0 ? diag - nb : 0;
-    int high = diag < na ? diag : na;
-    while (low <= high) {
-        const int ai = (low + high) >> 1;
-        const int bi = diag - ai;
-        const float al = ai > 0 ? a[ai - 1] : -FLT_MAX;
-        const float ar = ai < na ? a[ai] : FLT_MAX;
-        const float bl = bi > 0 ? b[bi - 1] : -FLT_MAX;
-        const float br = bi < nb ? b[bi] : FLT_MAX;
-        if (al > br) high = ai - 1;
-        else if (bl > ar) low = ai + 1;
-        else return ai;
+__device__ __forceinline__ float pair_key(uint2 e) { return __uint_as_float(e.x); }
+
+// Small merge, pbeam <= 128: topk_small_by_bitonic_sort<1, pbeam/32>
+// (utils.cuh:490-586).  Beam position p takes sorted candidate pbeam-1-p when
+// that one is smaller (the reversed candidates turn beam + candidates into a
+// bitonic sequence), then the merge stages of block size pbeam.  The sorted
+// candidates come from the staging array: index min(pbeam-1-p, 32) is a
+// FLT_MAX entry whenever pbeam-1-p >= cbs, which never replaces anything.
+// The reference's `first` strided load + sort is skipped: it runs only at
+// iteration 0, when every beam entry is the identical (FLT_MAX, MAX_INDEX)
+// pair, where it is the identity.
+template <int E, bool HALF>
+__device__ __forceinline__ void small_merge(int pbeam, uint2 *bp, const uint2 *ms, int base, bool writer) {
+    float k[E];
+    uint32_t v[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const uint2 b = bp[base + e];
+        const int kc = pbeam - 1 - (base + e);
+        const uint2 c = ms[kc < 32 ? kc : 32];
+        const bool take = pair_key(c) < pair_key(b);
+        k[e] = take ? pair_key(c) : pair_key(b);
+        v[e] = take ? c.y : b.y;
     }
-    return low;
+    bitonic_stage<E, HALF, (HALF ? 32 : 64 * E), (HALF ? 16 : 32 * E)>(k, v);
+    if (writer) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) bp[base + e] = make_uint2(__float_as_uint(k[e]), v[e]);
+    }
 }
 
-// Beam merge (utils.cuh:1369-1399 dispatch for a <= 32-entry buffer).
-// pbeam <= 128: topk_small_by_bitonic_sort<1, pbeam/32> (utils.cuh:490-586).
-// The `first` strided load + sort is skipped: it runs only at iteration 0,
-// when every beam entry is the identical (FLT_MAX, MAX_INDEX) pair, where it
-// is the identity.  pbeam > 128: topk_candidate_sort_and_merge
-// (utils.cuh:618-680) with the reference block's segmentation, writing into
-// the other beam buffer; returns the index of the buffer holding the beam.
-__device__ void merge_beam(const SearchParams &P, float *bd, uint32_t *bi, float *cd, uint32_t *ci) {
-    const int lane = lane_id();
+// Merge-path, pbeam > 128: topk_candidate_sort_and_merge (utils.cuh:618-680)
+// with the reference block's segmentation: `active` segments, segment t
+// writes outputs [d(t), d(t+1)) with d(t) = t * pbeam / active (at most 4,
+// since active >= pbeam / 4), its split point found by the reference's
+// binary search (utils.cuh:588-616); inside a segment beam entries go first
+// on ties (utils.cuh:652-671).  Lane l owns segments l*SPL .. l*SPL+SPL-1.
+// It searches its right boundaries; the left one is its neighbour's.  The
+// search reads the sentinel-padded arrays, so no bound needs a branch:
+// bp[-1], ms[-1] = -FLT_MAX and bp[pbeam], ms[32] = FLT_MAX stand for the
+// reference's out-of-range values.
+template <int SPL>
+__device__ __forceinline__ void merge_path(const SearchParams &P, uint2 *bp, const uint2 *ms) {
+    const int lane = lane_id_opaque();
+    const int cbs = P.cbs, pbeam = P.pbeam, active = P.seg_active;
+    const int t0 = lane * SPL;
+    const float *bk = reinterpret_cast<const float *>(bp);  // key of entry i at bk[2 i]
+    const float *mk = reinterpret_cast<const float *>(ms);
+    int dg[SPL + 1], res[SPL + 1];
+#pragma unroll
+    for (int k = 0; k <= SPL; ++k) {
+        const int t = min(t0 + k, active);
+        dg[k] = static_cast<int>(__umulhi(static_cast<uint32_t>(t * pbeam), P.seg_magic));
+    }
+    int lo[SPL], hi[SPL];
+    bool done[SPL];
+#pragma unroll
+    for (int k = 0; k < SPL; ++k) {
+        lo[k] = max(dg[k + 1] - cbs, 0);
+        hi[k] = min(dg[k + 1], pbeam);
+        done[k] = t0 + k + 1 > active;
+        res[k + 1] = 0;
+    }
+    for (;;) {
+        bool live = false;
+#pragma unroll
+        for (int k = 0; k < SPL; ++k) {
+            if (!done[k] && lo[k] > hi[k]) {  // loop exit: return low
+                res[k + 1] = lo[k];
+                done[k] = true;
+            }
+            const int ai = done[k] ? 0 : (lo[k] + hi[k]) >> 1;
+            const int bj = done[k] ? 0 : dg[k + 1] - ai;
+            const float al = bk[2 * ai - 2], ar = bk[2 * ai];
+            const float bl = mk[2 * bj - 2], br = mk[2 * bj];
+            if (!done[k]) {
+                if (al > br) {
+                    hi[k] = ai - 1;
+                } else if (bl > ar) {
+                    lo[k] = ai + 1;
+                } else {
+                    res[k + 1] = ai;
+                    done[k] = true;
+                }
+            }
+            live |= !done[k];
+        }
+        if (!__any(live)) break;
+    }
+    res[0] = __shfl_up(res[SPL], 1);
+    if (lane == 0) res[0] = 0;
+    // Each segment's na beam entries and nb candidates (na + nb <= 4) are
+    // read into 4 slots: slot s is beam entry tb + s for s < na, candidate
+    // cb + s - na after.  Output position of a slot = d(t) + the number of
+    // slots ordered before it: within one list by index, across lists beam
+    // first unless the candidate is strictly smaller.
+    uint2 slot[SPL][4];
+    int pos[SPL][4];
+    int nsl[SPL];
+#pragma unroll
+    for (int k = 0; k < SPL; ++k) {
+        const bool act = t0 + k < active;
+        const int tb = act ? res[k] : 0;
+        const int cb = act ? dg[k] - res[k] : 0;
+        const int na = act ? res[k + 1] - res[k] : 0;
+        nsl[k] = act ? dg[k + 1] - dg[k] : 0;
+        bool ina[4];
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2) {
+            ina[s2] = s2 < na;
+            slot[k][s2] = ina[s2] ? bp[tb + s2] : ms[cb + s2 - na];
+            pos[k][s2] = dg[k];
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2)
+#pragma unroll
+            for (int u = s2 + 1; u < 4; ++u) {
+                // slots at or past nsl are unused: they never count
+                const bool cross = ina[s2] && !ina[u];
+                const bool first = !cross || !(pair_key(slot[k][u]) < pair_key(slot[k][s2]));
+                pos[k][u] += first ? 1 : 0;
+                pos[k][s2] += (!first && u < nsl[k]) ? 1 : 0;
+            }
+    }
+    // every lane has read its inputs before any output overwrites them
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < SPL; ++k)
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2) bp[s2 < nsl[k] ? pos[k][s2] : pbeam + 2] = slot[k][s2];
+}
+
+// Beam merge (utils.cuh:1369-1399 dispatch for a <= 32-entry buffer): the
+// candidates are sorted (warp_sort<1>), staged in `ms`, and merged into the
+// beam in place.
+__device__ __forceinline__ void merge_beam(const SearchParams &P, uint2 *bp, uint2 *ms, const float *cd,
+                                           const uint32_t *ci) {
+    const int lane = lane_id_opaque();
     const int nl = lane & 31, h = lane >> 5;
     const int cbs = P.cbs, pbeam = P.pbeam;
     float ck = nl < cbs ? cd[nl] : FLT_MAX;
     uint32_t cv = nl < cbs ? ci[nl] : kMaxIndex;
     sort32(ck, cv);
-    if (pbeam <= 128) {
-        if (pbeam == 128) {
-            float k[2];
-            uint32_t v[2];
-            const int base = 2 * lane;
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                k[e] = bd[base + e];
-                v[e] = bi[base + e];
-                const int kc = pbeam - 1 - (base + e);
-                const float kk2 = __shfl(ck, kc & 31);
-                const uint32_t vv2 = static_cast<uint32_t>(__shfl(static_cast<int>(cv), kc & 31));
-                if (kc < cbs && k[e] > kk2) {
-                    k[e] = kk2;
-                    v[e] = vv2;
-                }
-            }
-            bitonic_stage<2, false>(k, v, 128, 64);
-            __syncthreads();
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                bd[base + e] = k[e];
-                bi[base + e] = v[e];
-            }
-        } else {
-            const int pos = pbeam == 64 ? lane : nl;
-            float k[1] = {bd[pos]};
-            uint32_t v[1] = {bi[pos]};
-            const int kc = pbeam - 1 - pos;
-            const float kk2 = __shfl(ck, kc & 31);
-            const uint32_t vv2 = static_cast<uint32_t>(__shfl(static_cast<int>(cv), kc & 31));
-            if (kc < cbs && k[0] > kk2) {
-                k[0] = kk2;
-                v[0] = vv2;
-            }
-            if (pbeam == 64) bitonic_stage<1, false>(k, v, 64, 32);
-            else bitonic_stage<1, true>(k, v, 32, 16);
-            __syncthreads();
-            if (pbeam == 64 || h == 0) {
-                bd[pos] = k[0];
-                bi[pos] = v[0];
-            }
-        }
-        __syncthreads();
-        return;
-    }
-    // merge-path variant: sorted candidates to LDS, then segments
-    if (h == 0 && nl < cbs) {
-        cd[nl] = ck;
-        ci[nl] = cv;
-    }
+    if (h == 0) ms[nl] = make_uint2(__float_as_uint(ck), cv);
     __syncthreads();
-    int active = (pbeam + 3) / 4;
-    active = ((active + 31) / 32) * 32;
-    if (active > kRefBlock) active = kRefBlock;
-    // Lane l owns segments [l*spl, (l+1)*spl); their spl+1 partition points
-    // are found by binary searches advanced together.  Segment t writes
-    // outputs [ob_t, ob_{t+1}) with ob_t = min(pbeam, t*pbeam/active); each
-    // segment holds at most 4 outputs because active >= pbeam/4.
-    constexpr int kMaxSpl = kRefBlock / 64;
-    const int spl = (active + 63) / 64;
-    const int t0 = lane * spl;
-    const uint32_t ub = static_cast<uint32_t>(pbeam);
-    int dg[kMaxSpl + 1], lo[kMaxSpl + 1], hi[kMaxSpl + 1], res[kMaxSpl + 1];
-    bool pend[kMaxSpl + 1];
-#pragma unroll
-    for (int k = 0; k <= kMaxSpl; ++k) {
-        const int t = t0 + k;
-        pend[k] = k <= spl && t <= active;
-        dg[k] = pend[k] ? static_cast<int>(min(ub, (static_cast<uint32_t>(t) * ub) / static_cast<uint32_t>(active))) : 0;
-        lo[k] = dg[k] - cbs > 0 ? dg[k] - cbs : 0;
-        hi[k] = dg[k] < pbeam ? dg[k] : pbeam;
-        res[k] = 0;
+    if (pbeam == 128) {
+        small_merge<2, false>(pbeam, bp, ms, 2 * lane, true);
+    } else if (pbeam == 64) {
+        small_merge<1, false>(pbeam, bp, ms, lane, true);
+    } else if (pbeam == 32) {
+        small_merge<1, true>(pbeam, bp, ms, nl, h == 0);
+    } else {
+        const int spl = (P.seg_active + 63) / 64;
+        if (spl == 1) merge_path<1>(P, bp, ms);
+        else if (spl == 2) merge_path<2>(P, bp, ms);
+        else merge_path<4>(P, bp, ms);
     }
-    // utils.cuh:588-616, several diagonals at once
-    for (int round = 0; round < 16; ++round) {
-        bool anyp = false;
-#pragma unroll
-        for (int k = 0; k <= kMaxSpl; ++k) {
-            if (!pend[k]) continue;
-            if (lo[k] > hi[k]) {
-                res[k] = lo[k];
-                pend[k] = false;
-                continue;
-            }
-            const int ai = (lo[k] + hi[k]) >> 1;
-            const int bj = dg[k] - ai;
-            const float al = ai > 0 ? bd[ai - 1] : -FLT_MAX;
-            const float ar = ai < pbeam ? bd[ai] : FLT_MAX;
-            const float bl = bj > 0 ? cd[bj - 1] : -FLT_MAX;
-            const float br = bj < cbs ? cd[bj] : FLT_MAX;
-            if (al > br) {
-                hi[k] = ai - 1;
-            } else if (bl > ar) {
-                lo[k] = ai + 1;
-            } else {
-                res[k] = ai;
-                pend[k] = false;
-            }
-            anyp |= pend[k];
-        }
-        if (!__any(anyp)) break;
-    }
-    // utils.cuh:652-671 per segment: beam first on ties, at most 4 outputs,
-    // held in registers until every lane has read its inputs, then written
-    // back in place (no second beam buffer)
-    float okey[kMaxSpl][4];
-    uint32_t oval[kMaxSpl][4];
-    int obase[kMaxSpl], ocount[kMaxSpl];
-#pragma unroll
-    for (int k = 0; k < kMaxSpl; ++k) {
-        obase[k] = 0;
-        ocount[k] = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            okey[k][i] = FLT_MAX;
-            oval[k][i] = kMaxIndex;
-        }
-    }
-#pragma unroll
-    for (int k = 0; k < kMaxSpl; ++k) {
-        const int t = t0 + k;
-        if (k >= spl || t >= active) continue;
-        const int ob = dg[k], oe = dg[k + 1];
-        const int tb = res[k], te = res[k + 1];
-        const int cb = ob - tb;
-        const int ce = oe - te;
-        float ak[4], ck2[4];
-        uint32_t av[4], cv2[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const bool ina = tb + i < te;
-            ak[i] = ina ? bd[tb + i] : FLT_MAX;
-            av[i] = ina ? bi[tb + i] : kMaxIndex;
-            const bool inb = cb + i < ce;
-            ck2[i] = inb ? cd[cb + i] : FLT_MAX;
-            cv2[i] = inb ? ci[cb + i] : kMaxIndex;
-        }
-        int na = te - tb, nb = ce - cb;
-        obase[k] = ob;
-        ocount[k] = oe - ob;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int o = ob + i;
-            if (o < oe) {
-                const bool take_top = (nb <= 0) || (na > 0 && ak[0] <= ck2[0]);
-                okey[k][i] = take_top ? ak[0] : ck2[0];
-                oval[k][i] = take_top ? av[0] : cv2[0];
-                // advance the consumed list by one (register shift, no indexing)
-#pragma unroll
-                for (int j = 0; j < 3; ++j) {
-                    ak[j] = take_top ? ak[j + 1] : ak[j];
-                    av[j] = take_top ? av[j + 1] : av[j];
-                    ck2[j] = take_top ? ck2[j] : ck2[j + 1];
-                    cv2[j] = take_top ? cv2[j] : cv2[j + 1];
-                }
-                na -= take_top ? 1 : 0;
-                nb -= take_top ? 0 : 1;
-            }
-        }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < kMaxSpl; ++k)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            if (i < ocount[k]) {
-                bd[obase[k] + i] = okey[k][i];
-                bi[obase[k] + i] = oval[k][i];
-            }
     __syncthreads();
 }
 
@@ -1032,18 +1023,18 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
     const bool vec_ok = P.vec_ok != 0;
 
     // fixed-size regions at compile-time offsets for the specialised shapes
+    // (the same layout function the host sizes the launch with)
     constexpr bool kFixedGeo = Geo<DIM_T, DEG_T>::kFixed;
-    constexpr uint32_t kQueryOff = 256u;
-    constexpr uint32_t kPlaneOff = kQueryOff + ((DIM_T + 3u) & ~3u) * 4u;
-    constexpr uint32_t kScratchOff = kPlaneOff + 8u * (Geo<DIM_T, DEG_T>::kB / 32u) * 4u;
-    constexpr uint32_t kProfOff = (kScratchOff + (32u + 3u * 8u) * 4u + 7u) & ~7u;
-    const uint32_t query_off = kFixedGeo ? kQueryOff : P.lds.query_off;
-    const uint32_t plane_off = kFixedGeo ? kPlaneOff : P.lds.plane_off;
-    const uint32_t scratch_off = kFixedGeo ? kScratchOff : P.lds.scratch_off;
-    const uint32_t prof_off = kFixedGeo ? kProfOff : P.lds.prof_off;
+    constexpr LdsLayout kL = lds_layout(DIM_T, Geo<DIM_T, DEG_T>::kB, 0, 0);
+    const uint32_t query_off = kFixedGeo ? kL.query_off : P.lds.query_off;
+    const uint32_t plane_off = kFixedGeo ? kL.plane_off : P.lds.plane_off;
+    const uint32_t scratch_off = kFixedGeo ? kL.scratch_off : P.lds.scratch_off;
+    const uint32_t prof_off = P.lds.prof_off;
+    static_assert(kL.cand_off == 0 && kL.msort_off == 256u, "fixed LDS regions");
     uint32_t *H = reinterpret_cast<uint32_t *>(smem + P.lds.hash_off);
-    float *bd0 = reinterpret_cast<float *>(smem + P.lds.beam_off);
-    uint32_t *bi0 = reinterpret_cast<uint32_t *>(bd0 + P.pbeam);
+    // beam pairs: bp[-1] and bp[pbeam] are sentinels
+    uint2 *bp = reinterpret_cast<uint2 *>(smem + P.lds.beam_off) + 1;
+    uint2 *ms = reinterpret_cast<uint2 *>(smem + kL.msort_off) + 1;
     float *cd = reinterpret_cast<float *>(smem);
     uint32_t *ci = reinterpret_cast<uint32_t *>(cd + 32);
     float *qv = reinterpret_cast<float *>(smem + query_off);
@@ -1053,9 +1044,10 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
     uint32_t *pnode = plist + 8;
     float *pdist = reinterpret_cast<float *>(pnode + 8);
     unsigned long long *prof = reinterpret_cast<unsigned long long *>(smem + prof_off);
-    unsigned long long t_last = 0;
+    unsigned long long t_last = 0, t_begin = 0;
     if constexpr (PROF) {
         if (lane < 16) prof[lane] = 0;
+        t_begin = __builtin_amdgcn_s_memrealtime();
         t_last = __builtin_amdgcn_s_memtime();
     }
 
@@ -1082,10 +1074,10 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
 
     // ---- state (adaptive_search.cuh:67-107)
     hash_reset(H, bitlen);
-    for (int i = lane; i < P.pbeam; i += 64) {
-        bd0[i] = FLT_MAX;
-        bi0[i] = kMaxIndex;
-    }
+    const uint2 kEmpty = make_uint2(__float_as_uint(FLT_MAX), kMaxIndex);
+    const uint2 kLowSentinel = make_uint2(__float_as_uint(-FLT_MAX), kMaxIndex);
+    for (int i = lane - 1; i < P.pbeam + static_cast<int>(kBeamPad); i += 64) bp[i] = i < 0 ? kLowSentinel : kEmpty;
+    if (lane <= kMsortHi + 1) ms[lane - 1] = lane == 0 ? kLowSentinel : kEmpty;
     if (lane < 32) {
         cd[lane] = FLT_MAX;
         ci[lane] = kMaxIndex;
@@ -1108,32 +1100,34 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
 
     FG_PHASE(0);
     for (int iter = 0; iter < kMaxIterations; ++iter) {
-        float *bd = bd0;
-        uint32_t *bi = bi0;
+        // lane-derived values are recomputed in each iteration, not held
+        const int lane = lane_id_opaque();
+        const int h = lane >> 5, nl = lane & 31;
         if (((iter + 1) % kHashReset) == 0) {  // adaptive_search.cuh:128-134
             hash_reset(H, bitlen);
             __syncthreads();
-            for (int i = lane; i < beam_sz; i += 64) hash_insert(H, bitlen, bi[i] & ~kMsb);
+            for (int i = lane; i < beam_sz; i += 64) hash_insert(H, bitlen, bp[i].y & ~kMsb);
             __syncthreads();
         }
         FG_PHASE(1);
-        if (iter >= P.max_iter) break;
-
-        merge_beam(P, bd, bi, cd, ci);
+        // The merge runs before the iteration-limit test, so a search stopped
+        // by the limit merges its last candidates here (the final merge,
+        // adaptive_search.cuh:447-451).  A search that stops because no beam entry is left to
+        // expand has merged them already: its final merge sees an empty
+        // candidate buffer and leaves the beam as it is.
+        merge_beam(P, bp, ms, cd, ci);
         FG_PHASE(2);
-        for (int i = beam_sz + lane; i < pbeam; i += 64) {
-            bd[i] = FLT_MAX;
-            bi[i] = kMaxIndex;
-        }
+        if (iter >= P.max_iter) break;
+        for (int i = beam_sz + lane; i < pbeam; i += 64) bp[i] = kEmpty;
         if (lane < 32) {
             cd[lane] = FLT_MAX;
             ci[lane] = kMaxIndex;
         }
         __syncthreads();
         float kth = FLT_MAX;  // adaptive_search_utils.cuh:25-30
-        if (bi[beam_sz - 1] != kMaxIndex) kth = bd[(P.K < beam_sz ? P.K : beam_sz) - 1];
+        if (bp[beam_sz - 1].y != kMaxIndex) kth = __uint_as_float(bp[(P.K < beam_sz ? P.K : beam_sz) - 1].x);
         kth = uni(kth);
-        controller_step(ctl, uni(bi[0]), P.phase2_rho);
+        controller_step(ctl, uni(bp[0].y), P.phase2_rho);
         const int theta = ctl.spec;
 
         // pick_expanders (utils.cuh:752-787): first theta unexpanded entries
@@ -1141,13 +1135,13 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
         for (int base = 0; base < beam_sz; base += 64) {
             const int j = base + lane;
             bool fresh = false;
-            if (j < beam_sz) fresh = (bi[j] & kMsb) == 0;
+            if (j < beam_sz) fresh = (bp[j].y & kMsb) == 0;
             const uint64_t m = ballot(fresh);
             if (fresh) {
                 const uint32_t r = static_cast<uint32_t>(__popcll(m & ((1ull << lane) - 1ull))) + nexp;
                 if (r < static_cast<uint32_t>(theta)) {
                     plist[r] = static_cast<uint32_t>(j);
-                    bi[j] |= kMsb;
+                    bp[j].y |= kMsb;
                 }
             }
             nexp += static_cast<uint32_t>(__popcll(m));
@@ -1162,8 +1156,9 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
         FG_COUNT(c_exp += nexp);
         if (lane < static_cast<int>(nexp)) {
             const uint32_t pos = plist[lane];
-            pnode[lane] = bi[pos] & 0x7fffffffu;
-            pdist[lane] = bd[pos];
+            const uint2 e = bp[pos];
+            pnode[lane] = e.y & 0x7fffffffu;
+            pdist[lane] = __uint_as_float(e.x);
         }
         __syncthreads();
         // adaptive_search_utils.cuh:41-49
@@ -1415,16 +1410,18 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
     }
 
     FG_PHASE(3);
-    merge_beam(P, bd0, bi0, cd, ci);
-    const uint32_t *bi = bi0;
     // result writer (adaptive_search.cuh:455-464)
     for (int i = lane; i < P.K; i += 64) {
-        const uint32_t r = i < beam_sz ? (bi[i] & 0x7fffffffu) : (bi[beam_sz - 1] & 0x7fffffffu);
+        const uint32_t r = i < beam_sz ? (bp[i].y & 0x7fffffffu) : (bp[beam_sz - 1].y & 0x7fffffffu);
         P.results[static_cast<uint64_t>(qid) * P.K + i] = r;
     }
     FG_PHASE(9);
     if constexpr (PROF) {
-        if (lane < 10) P.phase[static_cast<uint64_t>(qid) * 10 + lane] = prof[lane];
+        const unsigned long long t_end = __builtin_amdgcn_s_memrealtime();
+        unsigned long long *out = P.phase + static_cast<uint64_t>(qid) * FG_PROFILE_SLOTS;
+        if (lane < 10) out[lane] = prof[lane];
+        if (lane == 10) out[lane] = t_begin;
+        if (lane == 11) out[lane] = t_end;
     }
     if (COUNT && P.counters && lane == 0) {
         uint32_t *c = P.counters + static_cast<uint64_t>(qid) * FG_COUNTERS_PER_QUERY;
@@ -1634,6 +1631,18 @@ int make_params(fg_index *ix, uint32_t nq, uint32_t K, uint32_t beam, SearchPara
     P.collect_cap = P.cbs < kBufferBound ? P.cbs : kBufferBound;
     P.bitlen = static_cast<int>(visited_bitlen(beam, ix->degree));
     P.max_iter = static_cast<int>((beam * 11 + 9) / 10);  // gpu_search_adaptive.cu:96
+    // merge-path segmentation of the reference's 256-thread block
+    // (utils.cuh:633-641): ceil(pbeam / 4) rounded up to a multiple of 32
+    P.seg_active = 0;
+    P.seg_magic = 0;
+    if (P.pbeam > 128) {
+        int active = ((P.pbeam + 3) / 4 + 31) / 32 * 32;
+        if (active > kRefBlock) active = kRefBlock;
+        P.seg_active = active;
+        // exact for t * pbeam < 2^18: the reciprocal's error adds < 2^-14
+        // while t * pbeam / active sits >= 1 / active below the next integer
+        P.seg_magic = static_cast<uint32_t>((1ull << 32) / static_cast<uint64_t>(active) + 1ull);
+    }
     P.phase2_rho = ix->degree <= 4u ? 0.0f : 1.0f - 4.0f / static_cast<float>(ix->degree);  // utils 20-23
     P.use_ip = ix->metric == FG_METRIC_IP ? 1 : 0;
     P.dup_free = ix->dup_free;
@@ -1648,7 +1657,8 @@ template <int WT, int DPL, int DIM_T, int DEG_T>
 void launch_geo(const SearchParams &P, hipStream_t stream, bool count, bool prof) {
     const dim3 grid(P.nq), block(64);
     if (prof)
-        hipLaunchKernelGGL((fg_search_kernel<WT, DPL, DIM_T, DEG_T, false, true>), grid, block, P.lds.total, stream, P);
+        hipLaunchKernelGGL((fg_search_kernel<WT, DPL, DIM_T, DEG_T, false, true>), grid, block, P.lds.total_prof,
+                           stream, P);
     else if (count)
         hipLaunchKernelGGL((fg_search_kernel<WT, DPL, DIM_T, DEG_T, true, false>), grid, block, P.lds.total, stream, P);
     else

@@ -100,12 +100,14 @@ int fg_search_device(fg_index *index, const float *d_queries, uint32_t nq, uint3
                      uint32_t beam, uint32_t *d_results, uint32_t *d_counters, void *stream);
 
 /* Diagnostics: the same search as fg_search_device, built with phase timers.
- * d_phase receives 10 uint64 per query: s_memtime cycles spent in query
- * preparation + set-up, visited-table restore, beam merge, controller + pick,
- * single-expander scoring, single-expander exact distances, speculative id
- * loads + visited tests, speculative estimates + selection + inserts,
- * speculative exact distances, and the final merge + result write.  No
- * counterpart in the reference (its only diagnostics are printfs). */
+ * d_phase receives FG_PROFILE_SLOTS uint64 per query: shader-clock cycles
+ * spent in query preparation + set-up, visited-table restore, beam merge,
+ * controller + pick, single-expander scoring, single-expander exact
+ * distances, speculative id loads + visited tests, speculative estimates +
+ * selection + inserts, speculative exact distances, and the result write;
+ * then the query's start and end on the device's constant 100 MHz clock.
+ * No counterpart in the reference (its only diagnostics are printfs). */
+#define FG_PROFILE_SLOTS 12
 int fg_search_profile(fg_index *index, const float *d_queries, uint32_t nq, uint32_t K, uint32_t beam,
                       uint32_t *d_results, unsigned long long *d_phase, void *stream);
 

@@ -46,3 +46,12 @@ def test_lds_bytes_host_only():
     small = lds_bytes(128, 128, 32)
     big = lds_bytes(128, 1024, 32)
     assert 4096 < small < big < 64 * 1024
+
+
+def test_header_constants_match_binding():
+    from flashgann_amd import _lib
+    text = open(os.path.join(ROOT, "include", "flashgann.h")).read()
+    defs = {k: int(v.rstrip("u"), 0) for k, v in re.findall(r"^#define (FG_\w+)\s+(-?\w+)", text, re.M)}
+    for name in ("FG_OK", "FG_EINVAL", "FG_ENOMEM", "FG_EDEVICE", "FG_EIO", "FG_METRIC_L2", "FG_METRIC_IP",
+                 "FG_ENTRY_AUTO", "FG_COUNTERS_PER_QUERY", "FG_PROFILE_SLOTS"):
+        assert defs[name] == getattr(_lib, name), name
