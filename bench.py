@@ -179,6 +179,16 @@ def main() -> int:
     log(f"beam {chosen}: {ms_per_step:.3f} ms/step (kernel {kernel_ms:.3f} ms), {qps:.0f} QPS, "
         f"{achieved:.1f} GB/s algorithmic")
 
+    # the same search through the host-buffer entry point (queries copied in,
+    # ids copied out, PCIe included) -- reported beside, never as, `value`
+    host_q = np.ascontiguousarray(queries, dtype=np.float32)
+    index.search(host_q, args.K, chosen)
+    t_host = time.perf_counter()
+    for _ in range(3):
+        index.search(host_q, args.K, chosen)
+    host_qps = 3 * args.nq / (time.perf_counter() - t_host)
+    log(f"beam {chosen}: {host_qps:.0f} QPS through fg_search (host buffers, PCIe included)")
+
     traffic = None
     if os.path.exists(args.traffic):
         try:
@@ -203,10 +213,15 @@ def main() -> int:
         cids, _ = oix.search(queries[:sample], args.K, chosen, threads=threads)
         cpu_s = time.perf_counter() - t1
         same = float((cids == ids[:sample]).all(1).mean())
+        # one host thread over a proportionally smaller sample (about 2 s)
+        one = int(min(sample, max(8, 2.0 / max(per_q_cpu, 1e-6))))
+        t1 = time.perf_counter()
+        oix.search(queries[:one], args.K, chosen, threads=1)
+        one_qps = one / (time.perf_counter() - t1)
         cpu = {"value": round(sample / cpu_s, 1), "unit": "queries/s", "cores": threads, "kind": "port",
                "sample": f"first {sample} of the {args.nq} C2 queries at beam {chosen}, "
                          f"{threads} host threads, {cpu_s:.1f} s wall",
-               "ids_identical_to_gpu": same}
+               "ids_identical_to_gpu": same, "single_thread_value": round(one_qps, 1)}
         log(f"cpu oracle: {sample / cpu_s:.0f} QPS on {threads} threads; ids identical on {same * 100:.2f}% "
             f"of the sample")
 
@@ -225,6 +240,7 @@ def main() -> int:
         "data": "synthetic: seeded integer Gaussian mixture (1024 components), graph and codes built in-run",
         "config": {"workload": f"C2 {args.n}x{dim} deg {args.degree}, K={args.K}, nq={args.nq}, beam={chosen}",
                    "beam": chosen, "recall": round(float(recall), 5), "beam_sweep": sweep,
+                   "host_buffers_qps": round(host_qps, 1),
                    "lds_bytes": fg.lds_bytes(dim, chosen, args.degree)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
