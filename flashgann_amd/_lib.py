@@ -37,7 +37,7 @@ class IndexInfo(C.Structure):
 
 class Stats(C.Structure):
     _fields_ = [("elapsed_s", C.c_double), ("kernel_ms", C.c_float), ("lds_bytes", C.c_uint32),
-                ("hash_bitlen", C.c_uint32)]
+                ("visited_slots", C.c_uint32)]
 
 
 class FlashGannError(RuntimeError):

@@ -93,20 +93,18 @@ __host__ __device__ inline int keep_count_for_expander(uint32_t active, int thet
     return clamp_i(max_keep, 1, active_count);
 }
 
-// Visited-table size.  Between two resets the table receives at most
-// beam + 16 * 32 * tiles distinct keys (restore + one reset interval of
-// inserts, <= 32 per 8-task round).  Any open-addressing table with more
-// slots than that never fills, so it answers every membership query exactly
-// like the reference's 2^11-entry table (utils.cuh:137-151), which never fills
-// either.  The table is the smallest power of two keeping that worst case at
-// <= 90% load.
-__host__ __device__ inline uint32_t visited_bitlen(uint32_t beam, uint32_t degree) {
+// Visited-table size, in 4-slot buckets.  Between two resets the table
+// receives at most beam + 16 * 32 * tiles + 1 distinct keys (restore + one
+// reset interval of inserts, <= 32 per 8-task round, + the entry point).  A
+// table with more slots than that never fills, so it answers every
+// membership query exactly like the reference's 2^11-entry table
+// (utils.cuh:137-151), which never fills either.  The bucket count keeps that
+// worst case at <= 90% load.
+__host__ __device__ inline uint32_t visited_buckets(uint32_t beam, uint32_t degree) {
     const uint32_t tiles = (degree + 31) / 32;
     const uint32_t need = beam + 16u * 32u * tiles + 1u;
-    const uint32_t target = (need * 10u + 8u) / 9u;
-    uint32_t bitlen = 8;
-    while ((1u << bitlen) < target) ++bitlen;
-    return bitlen;
+    const uint32_t slots = (need * 10u + 8u) / 9u;
+    return (slots + 3u) / 4u;
 }
 
 struct LdsLayout {
@@ -130,7 +128,7 @@ constexpr uint32_t kBeamPad = 4;
 // staging area, the raw query, 8 x B/32 plane words and a small scratch area
 // (32-entry child list + parent lists).
 __host__ __device__ constexpr LdsLayout lds_layout(uint32_t dim, uint32_t padded_dim, uint32_t pbeam,
-                                                   uint32_t bitlen) {
+                                                   uint32_t buckets) {
     // fixed-size regions first (compile-time offsets for a fixed geometry),
     // then the beam-dependent visited table and beam
     LdsLayout L{};
@@ -147,7 +145,7 @@ __host__ __device__ constexpr LdsLayout lds_layout(uint32_t dim, uint32_t padded
     off += (32u + 3u * 8u) * 4u;
     off = (off + 15u) & ~15u;
     L.hash_off = off;
-    uint32_t hash_bytes = (1u << bitlen) * 4u;
+    uint32_t hash_bytes = buckets * 16u;
     if (hash_bytes < padded_dim * 4u) hash_bytes = padded_dim * 4u;
     off += hash_bytes;
     L.beam_off = off;
@@ -170,7 +168,7 @@ struct SearchParams {
     uint64_t row_offset, code_offset, factor_offset, neighbor_offset;
     int dim, padded_dim, degree;
     int K, beam, pbeam, cbs, collect_cap;
-    int bitlen, max_iter;
+    int buckets, max_iter;  // visited-table buckets (4 slots each), iteration limit
     int seg_active;      // merge-path segments (pbeam > 128)
     uint32_t seg_magic;  // floor(2^32 / seg_active) + 1: t * pbeam / seg_active by one mulhi
     float phase2_rho;
@@ -655,37 +653,67 @@ __device__ __forceinline__ void merge_beam(const SearchParams &P, uint2 *bp, uin
 
 // ------------------------------------------------------------ visited table
 
-// utils.cuh:697-735 hashing (slot = (k ^ (k >> bitlen)) & mask, linear probe,
-// empty = 0xFFFFFFFF) on an LDS table.
-__device__ __forceinline__ uint32_t hash_insert(uint32_t *t, int bitlen, uint32_t key) {
-    const uint32_t size = 1u << bitlen, mask = size - 1;
-    uint32_t idx = (key ^ (key >> bitlen)) & mask;
-    for (uint32_t i = 0; i < size; ++i) {
-        const uint32_t old = atomicCAS(&t[idx], kMaxIndex, key);
+// Visited set (the reference's utils.cuh:682-750 table, same membership
+// semantics): an exact set of node ids in LDS, open addressing over 4-slot
+// buckets, one 16-byte read per probe.  A key goes to the first bucket of its
+// probe sequence (home, home+1, .. wrapping) with an empty slot, so a lookup
+// stops at the first bucket that holds the key or an empty slot.  Empty slots
+// are 0xFFFFFFFF; keys (node ids, and 0x7FFFFFFF for the restore of an empty
+// beam slot, utils.cuh:747-748) have the top bit clear.
+__device__ __forceinline__ uint32_t hash_home(uint32_t key, uint32_t nb) {
+    const uint32_t h16 = (key ^ (key >> 13)) & 0xFFFFu;
+    return __umul24(h16, nb) >> 16;
+}
+
+__device__ __forceinline__ uint32_t hash_next(uint32_t b, uint32_t nb) { return b + 1u == nb ? 0u : b + 1u; }
+
+__device__ __forceinline__ bool bucket_has(uint4 s, uint32_t key) {
+    return s.x == key || s.y == key || s.z == key || s.w == key;
+}
+
+__device__ __forceinline__ bool bucket_open(uint4 s) { return static_cast<int32_t>(s.x | s.y | s.z | s.w) < 0; }
+
+// 1 if the key was added, 0 if it was present (utils.cuh:697-716).
+__device__ __forceinline__ uint32_t hash_insert(uint32_t *t, uint32_t nb, uint32_t key) {
+    const uint4 *t4 = reinterpret_cast<const uint4 *>(t);
+    uint32_t b = hash_home(key, nb);
+    // each pass either moves to the next bucket or retries after another
+    // lane filled a slot of this one: at most 5 passes per bucket
+    for (uint32_t i = 0; i < 5u * nb; ++i) {
+        const uint4 sl = t4[b];
+        if (bucket_has(sl, key)) return 0;
+        const int j = static_cast<int32_t>(sl.x) < 0   ? 0
+                      : static_cast<int32_t>(sl.y) < 0 ? 1
+                      : static_cast<int32_t>(sl.z) < 0 ? 2
+                      : static_cast<int32_t>(sl.w) < 0 ? 3
+                                                         : -1;
+        if (j < 0) {
+            b = hash_next(b, nb);
+            continue;
+        }
+        const uint32_t old = atomicCAS(&t[4u * b + static_cast<uint32_t>(j)], kMaxIndex, key);
         if (old == kMaxIndex) return 1;
         if (old == key) return 0;
-        idx = (idx + 1) & mask;
     }
     return 0;
 }
 
-__device__ __forceinline__ bool hash_contains(const uint32_t *t, int bitlen, uint32_t key) {
-    const uint32_t size = 1u << bitlen, mask = size - 1;
-    uint32_t idx = (key ^ (key >> bitlen)) & mask;
-    for (uint32_t i = 0; i < size; ++i) {
-        const uint32_t old = t[idx];
-        if (old == key) return true;
-        if (old == kMaxIndex) return false;
-        idx = (idx + 1) & mask;
+__device__ __forceinline__ bool hash_contains(const uint32_t *t, uint32_t nb, uint32_t key) {
+    const uint4 *t4 = reinterpret_cast<const uint4 *>(t);
+    uint32_t b = hash_home(key, nb);
+    for (uint32_t i = 0; i < nb; ++i) {
+        const uint4 sl = t4[b];
+        if (bucket_has(sl, key)) return true;
+        if (bucket_open(sl)) return false;
+        b = hash_next(b, nb);
     }
     return false;
 }
 
-__device__ __forceinline__ void hash_reset(uint32_t *t, int bitlen) {
-    const int n = 1 << bitlen;
+__device__ __forceinline__ void hash_reset(uint32_t *t, uint32_t nb) {
     uint4 *t4 = reinterpret_cast<uint4 *>(t);
     const uint4 e = make_uint4(kMaxIndex, kMaxIndex, kMaxIndex, kMaxIndex);
-    for (int i = lane_id(); i < (n >> 2); i += 64) t4[i] = e;
+    for (uint32_t i = static_cast<uint32_t>(lane_id()); i < nb; i += 64) t4[i] = e;
 }
 
 // true iff an earlier (lower-lane) member of `members` in this half carries
@@ -962,32 +990,35 @@ __device__ __forceinline__ bool select_smallest(float value, bool valid, int kee
 
 // Visited test for up to four keys per lane, probes advanced together.
 template <int NK>
-__device__ __forceinline__ void hash_contains_n(const uint32_t *t, int bitlen, const uint32_t (&key)[NK],
+__device__ __forceinline__ void hash_contains_n(const uint32_t *t, uint32_t nb, const uint32_t (&key)[NK],
                                                 bool (&test)[NK]) {
-    const uint32_t mask = (1u << bitlen) - 1u;
-    uint32_t idx[NK];
+    const uint4 *t4 = reinterpret_cast<const uint4 *>(t);
+    uint32_t b[NK];
     bool pend[NK];
 #pragma unroll
     for (int s = 0; s < NK; ++s) {
-        idx[s] = (key[s] ^ (key[s] >> bitlen)) & mask;
+        b[s] = hash_home(key[s], nb);
         pend[s] = test[s];
     }
-    for (uint32_t step = 0; step <= mask; ++step) {
+    for (uint32_t step = 0; step < nb; ++step) {
         bool anyp = false;
 #pragma unroll
         for (int s = 0; s < NK; ++s) {
             if (pend[s]) {
-                const uint32_t old = t[idx[s]];
-                if (old == key[s]) {
-                    pend[s] = false;          // contained: not a fresh child
+                const uint4 sl = t4[b[s]];
+                if (bucket_has(sl, key[s])) {
+                    pend[s] = false;  // contained: not a fresh child
                     test[s] = false;
-                } else if (old == kMaxIndex) {
-                    pend[s] = false;          // absent
+                } else if (bucket_open(sl)) {
+                    pend[s] = false;  // absent
                 } else {
-                    idx[s] = (idx[s] + 1u) & mask;
+                    b[s] = hash_next(b[s], nb);
                 }
             }
             anyp |= pend[s];
+            // at most two buckets (8 VGPRs) in flight: the search loop's
+            // codes and factors are live here too
+            if (s & 1) __builtin_amdgcn_sched_barrier(0);
         }
         if (!__any(anyp)) break;
     }
@@ -1009,8 +1040,11 @@ __device__ __forceinline__ void hash_contains_n(const uint32_t *t, int bitlen, c
         if constexpr (COUNT) stmt; \
     } while (0)
 
+// One wave per workgroup; the register budget targets 5 waves per SIMD
+// (<= 96 VGPRs), which LDS also allows for beams up to 256 (21 workgroups per
+// CU at 6,960 bytes).
 template <int WT, int DPL, int DIM_T, int DEG_T, bool COUNT, bool PROF>
-__global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg_search_kernel(SearchParams P) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int qid = blockIdx.x;
     if (qid >= P.nq) return;
@@ -1019,7 +1053,7 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
     const Geo<DIM_T, DEG_T> g(P);
     const int B = g.B, W = B >> 5;
     const int deg = g.deg;
-    const int bitlen = P.bitlen;
+    const uint32_t nbk = static_cast<uint32_t>(P.buckets);
     const bool vec_ok = P.vec_ok != 0;
 
     // fixed-size regions at compile-time offsets for the specialised shapes
@@ -1073,7 +1107,7 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
     }
 
     // ---- state (adaptive_search.cuh:67-107)
-    hash_reset(H, bitlen);
+    hash_reset(H, nbk);
     const uint2 kEmpty = make_uint2(__float_as_uint(FLT_MAX), kMaxIndex);
     const uint2 kLowSentinel = make_uint2(__float_as_uint(-FLT_MAX), kMaxIndex);
     for (int i = lane - 1; i < P.pbeam + static_cast<int>(kBeamPad); i += 64) bp[i] = i < 0 ? kLowSentinel : kEmpty;
@@ -1088,7 +1122,7 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
     if (lane == 0) {
         cd[0] = entry_d;
         ci[0] = P.entry;
-        hash_insert(H, bitlen, P.entry);
+        hash_insert(H, nbk, P.entry);
     }
     __syncthreads();
 
@@ -1104,9 +1138,9 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
         const int lane = lane_id_opaque();
         const int h = lane >> 5, nl = lane & 31;
         if (((iter + 1) % kHashReset) == 0) {  // adaptive_search.cuh:128-134
-            hash_reset(H, bitlen);
+            hash_reset(H, nbk);
             __syncthreads();
-            for (int i = lane; i < beam_sz; i += 64) hash_insert(H, bitlen, bp[i].y & ~kMsb);
+            for (int i = lane; i < beam_sz; i += 64) hash_insert(H, nbk, bp[i].y & ~kMsb);
             __syncthreads();
         }
         FG_PHASE(1);
@@ -1190,7 +1224,7 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
                 if constexpr (WT > 0)
                     load_code<WT>(reinterpret_cast<const uint32_t *>(prow + g.code) + static_cast<uint64_t>(nl) * WT,
                                   vec_ok, c1[0]);
-                if (child >= P.npoints || hash_contains(H, bitlen, child)) child = kMaxIndex;
+                if (child >= P.npoints || hash_contains(H, nbk, child)) child = kMaxIndex;
             }
             const uint32_t vmask = half_bits(ballot(child != kMaxIndex), 0);
             const int valid_count = __popc(vmask);
@@ -1242,7 +1276,7 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
             const uint32_t want_mask = half_bits(ballot(want), 0);
             bool ins = want;
             if (!P.dup_free) ins = want && !dup_of_earlier(child, want_mask, nl, 0);
-            if (h == 0 && ins) hash_insert(H, bitlen, child);
+            if (h == 0 && ins) hash_insert(H, nbk, child);
             if (!ins) {
                 if ((admit_mask >> nl) & 1u) {
                     child = kMaxIndex;
@@ -1312,7 +1346,7 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
                 // (b) visited test against the table as it stood at the round's start
 #pragma unroll
                 for (int sr = 0; sr < SR; ++sr) val[sr] = cid[sr] != kMaxIndex && cid[sr] < P.npoints;
-                hash_contains_n<SR>(H, bitlen, cid, val);
+                hash_contains_n<SR>(H, nbk, cid, val);
                 // (c) which tasks need estimates; their codes and factors, loads issued together
                 bool need[SR];
                 int keep[SR];
@@ -1372,9 +1406,13 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
                 }
 #pragma unroll
                 for (int sr = 0; sr < SR; ++sr) {
+                    // task 2 sr + h: selects between the two halves' uniform
+                    // values (a lane-dependent array index would put the
+                    // arrays in scratch memory)
+                    const uint32_t bt = h ? base_t[2 * sr + 1] : base_t[2 * sr];
+                    const uint32_t km = h ? kept_mask[2 * sr + 1] : kept_mask[2 * sr];
                     if (keepl[sr]) {
-                        const int t = 2 * sr + h;
-                        const uint32_t e = base_t[t] + static_cast<uint32_t>(__popc(kept_mask[t] & ((1u << nl) - 1u)));
+                        const uint32_t e = bt + static_cast<uint32_t>(__popc(km & ((1u << nl) - 1u)));
                         if (e < 32) alist[e] = cid[sr];
                     }
                 }
@@ -1383,7 +1421,7 @@ __global__ __launch_bounds__(64) void fg_search_kernel(SearchParams P) {
                 // (f) insert in list order; a repeat of an earlier entry is dropped
                 const bool mine = lane < static_cast<int>(total);
                 const uint32_t key = mine ? alist[lane] : kMaxIndex;
-                const uint32_t got = mine ? hash_insert(H, bitlen, key) : 0u;
+                const uint32_t got = mine ? hash_insert(H, nbk, key) : 0u;
                 bool acc = got != 0u;
                 if (__any(mine && !got)) {
                     const uint32_t members = half_bits(ballot(mine), 0);
@@ -1629,7 +1667,7 @@ int make_params(fg_index *ix, uint32_t nq, uint32_t K, uint32_t beam, SearchPara
     if (cap > static_cast<uint32_t>(kBufferBound)) cap = kBufferBound;
     P.cbs = static_cast<int>(round_up_pow2(cap));
     P.collect_cap = P.cbs < kBufferBound ? P.cbs : kBufferBound;
-    P.bitlen = static_cast<int>(visited_bitlen(beam, ix->degree));
+    P.buckets = static_cast<int>(visited_buckets(beam, ix->degree));
     P.max_iter = static_cast<int>((beam * 11 + 9) / 10);  // gpu_search_adaptive.cu:96
     // merge-path segmentation of the reference's 256-thread block
     // (utils.cuh:633-641): ceil(pbeam / 4) rounded up to a multiple of 32
@@ -1649,7 +1687,7 @@ int make_params(fg_index *ix, uint32_t nq, uint32_t K, uint32_t beam, SearchPara
     P.vec_ok = (ix->row_offset % 4 == 0 && ix->code_offset % 4 == 0) ? 1 : 0;
     P.entry = ix->entry;
     P.nq = static_cast<int>(nq);
-    P.lds = lds_layout(ix->dim, ix->padded_dim, static_cast<uint32_t>(P.pbeam), static_cast<uint32_t>(P.bitlen));
+    P.lds = lds_layout(ix->dim, ix->padded_dim, static_cast<uint32_t>(P.pbeam), static_cast<uint32_t>(P.buckets));
     return FG_OK;
 }
 
@@ -1715,7 +1753,7 @@ const char *fg_version(void) { return "flashgann-amd 0.1 (gfx950, wave64)"; }
 uint32_t fg_lds_bytes(uint32_t dim, uint32_t beam, uint32_t degree) {
     uint32_t b = 1;
     while (b < dim) b <<= 1;
-    return lds_layout(dim, b, effective_sort_beam(beam), visited_bitlen(beam, degree)).total;
+    return lds_layout(dim, b, effective_sort_beam(beam), visited_buckets(beam, degree)).total;
 }
 
 int fg_index_create(const float *rows, uint64_t npoints, uint32_t dim, uint32_t degree, const float *signs,
@@ -1852,7 +1890,7 @@ int fg_search(fg_index *ix, const float *queries, uint32_t nq, uint32_t K, uint3
         stats->elapsed_s = 0.0;
         stats->kernel_ms = 0.0f;
         stats->lds_bytes = P.lds.total;
-        stats->hash_bitlen = static_cast<uint32_t>(P.bitlen);
+        stats->visited_slots = 4u * static_cast<uint32_t>(P.buckets);
     }
     if (nq == 0) return FG_OK;
     const size_t qb = static_cast<size_t>(nq) * ix->dim * sizeof(float);

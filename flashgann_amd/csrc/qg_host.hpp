@@ -71,8 +71,8 @@ public:
             fprintf(stderr, "error %d: %s\n", rc, fg_last_error());
             exit(EXIT_FAILURE);
         }
-        printf("GPU adaptive search entry point: %u, visited table 2^%u, kernel %.3f ms (event)\n", active_entry_,
-               st.hash_bitlen, st.kernel_ms);
+        printf("GPU adaptive search entry point: %u, visited table %u slots, kernel %.3f ms (event)\n", active_entry_,
+               st.visited_slots, st.kernel_ms);
         elapsed = st.elapsed_s;
     }
 

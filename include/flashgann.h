@@ -59,7 +59,7 @@ typedef struct {
                                 (gpu_search_adaptive.cu:98-107) */
     float kernel_ms;         /* HIP-event time of the search kernel */
     uint32_t lds_bytes;      /* dynamic LDS per workgroup (one query) */
-    uint32_t hash_bitlen;    /* visited-table size used by the kernel */
+    uint32_t visited_slots;  /* visited-table slots used by the kernel */
 } fg_stats;
 
 /* Per-query work counters (6 x uint32 per query when requested):
