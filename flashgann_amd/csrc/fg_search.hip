@@ -81,6 +81,23 @@ __host__ __device__ inline int keep_count_per_parent(uint32_t max_degree, float 
     return static_cast<int>(k);
 }
 
+// keep_count_for_expander below, split: keep_limit is the part that does not
+// depend on the K-th cutoff, min(rho_keep, budget), always in [1, active];
+// with a valid cutoff the count is then min(max(near, 1), limit), otherwise
+// the limit itself.
+__host__ __device__ inline int keep_limit(uint32_t active, int theta, float rho) {
+    const int rho_keep = keep_count_per_parent(active, rho);
+    const int budget = clamp_i(static_cast<int>(static_cast<uint32_t>(kBufferBound) / static_cast<uint32_t>(theta)), 1,
+                               static_cast<int>(active));
+    return rho_keep < budget ? rho_keep : budget;
+}
+
+__host__ __device__ inline int keep_with_cutoff(int limit, bool kth_valid, uint32_t near) {
+    if (!kth_valid) return limit;
+    const int n = near < 1u ? 1 : static_cast<int>(near);
+    return n < limit ? n : limit;
+}
+
 // adaptive_search_utils.cuh:121-135
 __host__ __device__ inline int keep_count_for_expander(uint32_t active, int theta, float rho,
                                                        bool kth_valid, uint32_t near) {
@@ -116,17 +133,23 @@ struct LdsLayout {
 // indices -1 .. kMsortHi, the 32 sorted candidates at 0..31 between a
 // -FLT_MAX sentinel (index -1) and FLT_MAX sentinels (32 and up).
 constexpr int kMsortHi = 35;
-constexpr uint32_t kMsortPairs = 40;
+constexpr uint32_t kMsortPairs = 38;
 // Beam: (distance, id) pairs at indices -1 .. pbeam + kBeamPad - 1: a
 // -FLT_MAX sentinel, the pbeam entries, a FLT_MAX sentinel at pbeam, then pad
 // entries (segment reads may run up to 3 past pbeam; the merge's unused
 // slots are written to pbeam + 2).
 constexpr uint32_t kBeamPad = 4;
 
+// Whether the search keeps the raw query in LDS: only the generic kernel
+// (padded dim > 128) reads it there in the loop; the others hold it in
+// registers after preparation.
+__host__ __device__ constexpr bool query_in_lds(uint32_t padded_dim) { return padded_dim > 128u; }
+
 // Per-query LDS: visited table (aliased by the rotated query during
 // preparation), the beam, the 32-entry candidate buffer, the sorted-candidate
-// staging area, the raw query, 8 x B/32 plane words and a small scratch area
-// (32-entry child list + parent lists).
+// staging area, the raw query (aliased by the candidate buffer and staging
+// area when it is only read during set-up), 8 x B/32 plane words and a small
+// scratch area (32-entry child list + parent ids and distances).
 __host__ __device__ constexpr LdsLayout lds_layout(uint32_t dim, uint32_t padded_dim, uint32_t pbeam,
                                                    uint32_t buckets) {
     // fixed-size regions first (compile-time offsets for a fixed geometry),
@@ -137,12 +160,16 @@ __host__ __device__ constexpr LdsLayout lds_layout(uint32_t dim, uint32_t padded
     off += 32u * 8u;
     L.msort_off = off;
     off += kMsortPairs * 8u;
-    L.query_off = off;
-    off += ((dim + 3u) & ~3u) * 4u;
+    if (query_in_lds(padded_dim)) {
+        L.query_off = off;
+        off += ((dim + 3u) & ~3u) * 4u;
+    } else {
+        L.query_off = 0;  // set-up only: d <= 128 floats fit in the 560 bytes above
+    }
     L.plane_off = off;
     off += 8u * (padded_dim / 32u) * 4u;
     L.scratch_off = off;
-    off += (32u + 3u * 8u) * 4u;
+    off += (32u + 2u * 8u) * 4u;
     off = (off + 15u) & ~15u;
     L.hash_off = off;
     uint32_t hash_bytes = buckets * 16u;
@@ -754,9 +781,9 @@ __device__ __forceinline__ void controller_step(Controller &c, uint32_t beam0, f
     const float entry = c.entry_d;
     const float last = finite_below_max(c.last_e) ? c.last_e : entry;
     const float cur = finite_below_max(c.cur_e) ? c.cur_e : last;
-    float rate = 0.0f;
+    float rate = 0.0f;  // only read while the search stays in stage I
     const float denom = fabsf(entry);
-    if (isfinite(last) && isfinite(cur) && isfinite(entry) && denom > 1.0e-20f) {
+    if (!phase_changed && isfinite(last) && isfinite(cur) && isfinite(entry) && denom > 1.0e-20f) {
         const float pr = (last - cur) / denom;
         if (isfinite(pr) && pr > 0.0f) rate = pr < 1.0f ? pr : 1.0f;
     }
@@ -975,13 +1002,16 @@ __device__ __forceinline__ bool select_smallest(float value, bool valid, int kee
     bool kept = false;
     for (int r = 0; r < max_k; ++r) {
         uint32_t m = remaining ? key : 0xFFFFFFFFu;
+        // minimum over the 32-lane half: quad (xor 1, xor 2), then the
+        // half-row and row mirrors bring in the other quad and the other
+        // half-row, then the neighbouring row
+        m = min(m, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(m), 0xB1, 0xF, 0xF, false)));
+        m = min(m, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(m), 0x4E, 0xF, 0xF, false)));
+        m = min(m, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(m), 0x141, 0xF, 0xF, false)));
+        m = min(m, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(m), 0x140, 0xF, 0xF, false)));
         m = min(m, xshfl(m, 16));
-        m = min(m, xshfl(m, 8));
-        m = min(m, xshfl(m, 4));
-        m = min(m, xshfl(m, 2));
-        m = min(m, xshfl(m, 1));
         const uint32_t cand = half_bits(ballot(remaining && key == m), h);
-        const bool take = r < keep_k && cand != 0u && nl == __builtin_ctz(cand | (cand == 0u ? 1u : 0u));
+        const bool take = r < keep_k && cand != 0u && (lane & 31) == __builtin_ctz(cand | (cand == 0u ? 1u : 0u));
         kept |= take;
         remaining &= !take;
     }
@@ -1065,6 +1095,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
     const uint32_t scratch_off = kFixedGeo ? kL.scratch_off : P.lds.scratch_off;
     const uint32_t prof_off = P.lds.prof_off;
     static_assert(kL.cand_off == 0 && kL.msort_off == 256u, "fixed LDS regions");
+    static_assert(32u * 8u + kMsortPairs * 8u >= 128u * 4u, "an aliased query fits the candidate and staging area");
     uint32_t *H = reinterpret_cast<uint32_t *>(smem + P.lds.hash_off);
     // beam pairs: bp[-1] and bp[pbeam] are sentinels
     uint2 *bp = reinterpret_cast<uint2 *>(smem + P.lds.beam_off) + 1;
@@ -1074,8 +1105,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
     float *qv = reinterpret_cast<float *>(smem + query_off);
     uint32_t *planes = reinterpret_cast<uint32_t *>(smem + plane_off);
     uint32_t *alist = reinterpret_cast<uint32_t *>(smem + scratch_off);
-    uint32_t *plist = alist + 32;
-    uint32_t *pnode = plist + 8;
+    uint32_t *pnode = alist + 32;
     float *pdist = reinterpret_cast<float *>(pnode + 8);
     unsigned long long *prof = reinterpret_cast<unsigned long long *>(smem + prof_off);
     unsigned long long t_last = 0, t_begin = 0;
@@ -1106,6 +1136,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
         qr[k] = (DPL > 0 && i < g.dim) ? qv[i] : 0.0f;
     }
 
+    const float entry_d = uni(half_distance(P.data + static_cast<uint64_t>(P.entry) * g.row, qv, g.dim, nl,
+                                            P.use_ip != 0, true));
+    // the query's LDS copy may share the candidate and staging area: every
+    // lane is done reading it before that area is initialised
+    __syncthreads();
+
     // ---- state (adaptive_search.cuh:67-107)
     hash_reset(H, nbk);
     const uint2 kEmpty = make_uint2(__float_as_uint(FLT_MAX), kMaxIndex);
@@ -1117,8 +1153,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
         ci[lane] = kMaxIndex;
     }
     __syncthreads();
-    const float entry_d = uni(half_distance(P.data + static_cast<uint64_t>(P.entry) * g.row, qv, g.dim, nl,
-                                            P.use_ip != 0, true));
     if (lane == 0) {
         cd[0] = entry_d;
         ci[0] = P.entry;
@@ -1165,17 +1199,20 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
         const int theta = ctl.spec;
 
         // pick_expanders (utils.cuh:752-787): first theta unexpanded entries
+        // the picked entries' ids and distances go straight to the parent
+        // lists (an unexpanded entry's id has the top bit clear)
         uint32_t nexp = 0;
         for (int base = 0; base < beam_sz; base += 64) {
             const int j = base + lane;
-            bool fresh = false;
-            if (j < beam_sz) fresh = (bp[j].y & kMsb) == 0;
+            const uint2 e = j < beam_sz ? bp[j] : make_uint2(0u, kMsb);
+            const bool fresh = (e.y & kMsb) == 0;
             const uint64_t m = ballot(fresh);
             if (fresh) {
                 const uint32_t r = static_cast<uint32_t>(__popcll(m & ((1ull << lane) - 1ull))) + nexp;
                 if (r < static_cast<uint32_t>(theta)) {
-                    plist[r] = static_cast<uint32_t>(j);
-                    bp[j].y |= kMsb;
+                    pnode[r] = e.y;
+                    pdist[r] = __uint_as_float(e.x);
+                    bp[j].y = e.y | kMsb;
                 }
             }
             nexp += static_cast<uint32_t>(__popcll(m));
@@ -1188,13 +1225,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
         if (nexp == 0) break;
         FG_COUNT(c_iters++);
         FG_COUNT(c_exp += nexp);
-        if (lane < static_cast<int>(nexp)) {
-            const uint32_t pos = plist[lane];
-            const uint2 e = bp[pos];
-            pnode[lane] = e.y & 0x7fffffffu;
-            pdist[lane] = __uint_as_float(e.x);
-        }
-        __syncthreads();
         // adaptive_search_utils.cuh:41-49
         ctl.last_e = finite_below_max(ctl.cur_e) ? ctl.cur_e : ctl.entry_d;
         ctl.cur_e = uni(pdist[nexp - 1]);
@@ -1300,6 +1330,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
             FG_COUNT(if (c_st2 == kMaxIndex) c_st2 = static_cast<uint32_t>(iter));
             const int tiles = (deg + 31) / 32;
             const int tasks = static_cast<int>(nexp) * tiles;
+            // keep limits of a full 32-neighbour tile and of the last,
+            // partial one (utils uniform over the iteration)
+            const int an_full = deg < 32 ? deg : 32;
+            const int an_last = deg - (tiles - 1) * 32;
+            const int lim_full = uni(keep_limit(static_cast<uint32_t>(an_full), theta, ctl.rho));
+            const int lim_last = an_last == an_full ? lim_full : uni(keep_limit(static_cast<uint32_t>(an_last), theta, ctl.rho));
             uint32_t compact = 0;
             for (int rbase = 0; rbase < tasks; rbase += kSearchWidth) {
                 constexpr int SR = kSearchWidth / 2;  // sub-rounds: two reference warps per wave
@@ -1353,7 +1389,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
 #pragma unroll
                 for (int sr = 0; sr < SR; ++sr) {
                     const int rvc = __popc(half_bits(ballot(val[sr]), h));
-                    keep[sr] = tsk[sr] >= 0 ? keep_count_for_expander(static_cast<uint32_t>(an[sr]), theta, ctl.rho, false, 0) : 0;
+                    const int lim = an[sr] == an_full ? lim_full : lim_last;
+                    keep[sr] = tsk[sr] >= 0 ? lim : 0;
                     need[sr] = !(keep[sr] >= rvc);
                     FG_COUNT(c_est += static_cast<uint32_t>(__popcll(ballot(need[sr] && val[sr]))));
                 }
@@ -1384,12 +1421,20 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
                     bool kl = val[sr];
                     const bool any_need = __any(need[sr]);
                     if (any_need) {
-                        const uint32_t near = __popc(half_bits(ballot(val[sr] && kth_valid && est <= kth), h));
+                        const bool below = val[sr] && kth_valid && est <= kth;
+                        const uint32_t near = __popc(half_bits(ballot(below), h));
                         int eff = keep[sr];
-                        if (need[sr]) eff = keep_count_for_expander(static_cast<uint32_t>(an[sr]), theta, ctl.rho, kth_valid, near);
-                        const int maxk = uni(max(eff, __shfl_xor(eff, 32)));
+                        if (need[sr]) eff = keep_with_cutoff(keep[sr], kth_valid, near);
+                        // With a valid cutoff and 1 <= near <= keep the count is
+                        // near, and the near smallest (value, lane) pairs are the
+                        // ones at or below the cutoff: every such lane ranks
+                        // ahead of every lane above it.  No selection rounds.
+                        const bool by_cut = need[sr] && kth_valid && near >= 1u && static_cast<int>(near) <= keep[sr];
+                        const int rounds = (need[sr] && !by_cut) ? eff : 0;
+                        // uniform within each half: the larger of lanes 0 and 32
+                        const int maxk = max(__builtin_amdgcn_readlane(rounds, 0), __builtin_amdgcn_readlane(rounds, 32));
                         const bool sel = select_smallest(est, val[sr], eff, maxk);
-                        if (need[sr]) kl = val[sr] && eff > 0 && sel;
+                        if (need[sr]) kl = val[sr] && eff > 0 && (by_cut ? below : sel);
                     }
                     keepl[sr] = kl;
                     const uint64_t km = ballot(kl);
