@@ -234,16 +234,17 @@ struct Geo {
 
 // ------------------------------------------------------------ device helpers
 
-__device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & 63; }
-
-// The lane id through an empty asm: values derived from it are computed where
-// they are used instead of being hoisted out of the search loop, where they
-// would hold registers through every phase of every iteration.
-__device__ __forceinline__ int lane_id_opaque() {
-    int l = lane_id();
+// The lane id, through an empty asm: values derived from it (lane masks,
+// addresses) are computed where they are used instead of being hoisted out of
+// the search loop, where they would hold registers -- lane masks hold scalar
+// register pairs -- through every phase of every iteration.
+__device__ __forceinline__ int lane_id() {
+    int l = static_cast<int>(threadIdx.x) & 63;
     asm volatile("" : "+v"(l));
     return l;
 }
+
+__device__ __forceinline__ int lane_id_opaque() { return lane_id(); }
 
 __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
 
@@ -585,24 +586,22 @@ __device__ __forceinline__ void merge_path(const SearchParams &P, uint2 *bp, con
         bool live = false;
 #pragma unroll
         for (int k = 0; k < SPL; ++k) {
-            if (!done[k] && lo[k] > hi[k]) {  // loop exit: return low
-                res[k + 1] = lo[k];
-                done[k] = true;
-            }
+            // branch-free round: all four values are read (one LDS round
+            // trip, two ds_read2), then the reference's if / else-if / else
+            // picks the update
+            const bool exit_low = !done[k] && lo[k] > hi[k];  // loop exit: return low
+            res[k + 1] = exit_low ? lo[k] : res[k + 1];
+            done[k] = done[k] || exit_low;
             const int ai = done[k] ? 0 : (lo[k] + hi[k]) >> 1;
             const int bj = done[k] ? 0 : dg[k + 1] - ai;
             const float al = bk[2 * ai - 2], ar = bk[2 * ai];
             const float bl = mk[2 * bj - 2], br = mk[2 * bj];
-            if (!done[k]) {
-                if (al > br) {
-                    hi[k] = ai - 1;
-                } else if (bl > ar) {
-                    lo[k] = ai + 1;
-                } else {
-                    res[k + 1] = ai;
-                    done[k] = true;
-                }
-            }
+            const bool go_left = al > br, go_right = !go_left && bl > ar;
+            const bool found = !done[k] && !go_left && !go_right;
+            hi[k] = (!done[k] && go_left) ? ai - 1 : hi[k];
+            lo[k] = (!done[k] && go_right) ? ai + 1 : lo[k];
+            res[k + 1] = found ? ai : res[k + 1];
+            done[k] = done[k] || found;
             live |= !done[k];
         }
         if (!__any(live)) break;
@@ -694,8 +693,10 @@ __device__ __forceinline__ uint32_t hash_home(uint32_t key, uint32_t nb) {
 
 __device__ __forceinline__ uint32_t hash_next(uint32_t b, uint32_t nb) { return b + 1u == nb ? 0u : b + 1u; }
 
+// (min of the four XORs is zero iff one slot equals the key: integer ops the
+// compiler keeps as such, where four compares became packed 16-bit flags)
 __device__ __forceinline__ bool bucket_has(uint4 s, uint32_t key) {
-    return s.x == key || s.y == key || s.z == key || s.w == key;
+    return min(min(s.x ^ key, s.y ^ key), min(s.z ^ key, s.w ^ key)) == 0u;
 }
 
 __device__ __forceinline__ bool bucket_open(uint4 s) { return static_cast<int32_t>(s.x | s.y | s.z | s.w) < 0; }
@@ -1345,7 +1346,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
                 const float *prw[SR];
                 float tx[SR], fdq[SR], fvq[SR];
                 uint32_t code[SR][WTR];
-                // (a) neighbour ids of the round's 8 tasks, loads issued together
+                // (a) neighbour ids of the round's 8 tasks, then their factors and
+                // codes: all loads issued together (one HBM round trip), ids first
+                // so the visited test can start when they arrive.  Loads are
+                // unconditional (an inactive lane reads a valid slot of parent 0
+                // or of its own parent's last neighbour); inactive lanes' ids are
+                // replaced after.
+                bool lact[SR];
+                int nsafe[SR];
 #pragma unroll
                 for (int sr = 0; sr < SR; ++sr) {
                     const int task = rbase + 2 * sr + h;
@@ -1353,32 +1361,30 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
                     const int pidx = tact ? task / tiles : 0;
                     const int tile = tact ? task - pidx * tiles : 0;
                     const int nidx = tile * 32 + nl;
+                    lact[sr] = tact && nidx < deg;
+                    nsafe[sr] = nidx < deg ? nidx : deg - 1;
                     tsk[sr] = tact ? tile * 32 : -1;
                     pix[sr] = pidx;
                     prw[sr] = data + static_cast<uint64_t>(pnode[pidx]) * g.row;
-                    cid[sr] = (tact && nidx < deg) ? reinterpret_cast<const uint32_t *>(prw[sr] + g.nbr)[nidx]
-                                                   : kMaxIndex;
-                    // the neighbour's factors and code are issued with its id: their addresses
-                    // do not depend on it, and most lanes need them (one HBM round trip)
-                    tx[sr] = FLT_MAX;
-                    fdq[sr] = 0.0f;
-                    fvq[sr] = 0.0f;
-#pragma unroll
-                    for (int w = 0; w < WTR; ++w) code[sr][w] = 0u;
-                    if (tact && nidx < deg) {
-                        const float *factors = prw[sr] + g.factor;
-                        tx[sr] = factors[nidx];
-                        fdq[sr] = factors[deg + nidx];
-                        fvq[sr] = factors[2 * deg + nidx];
-                        if constexpr (WT > 0)
-                            load_code<WT>(reinterpret_cast<const uint32_t *>(prw[sr] + g.code) +
-                                              static_cast<uint64_t>(nidx) * WT,
-                                          vec_ok, code[sr]);
-                    }
+                    cid[sr] = reinterpret_cast<const uint32_t *>(prw[sr] + g.nbr)[nsafe[sr]];
                     int a = tact ? deg - tile * 32 : 0;
                     an[sr] = a > 32 ? 32 : a;
-                    FG_COUNT(c_ids += static_cast<uint32_t>(__popcll(ballot(tact && nidx < deg))));
+                    FG_COUNT(c_ids += static_cast<uint32_t>(__popcll(ballot(lact[sr]))));
                 }
+#pragma unroll
+                for (int sr = 0; sr < SR; ++sr) {
+                    const float *factors = prw[sr] + g.factor;
+                    tx[sr] = factors[nsafe[sr]];
+                    fdq[sr] = factors[deg + nsafe[sr]];
+                    fvq[sr] = factors[2 * deg + nsafe[sr]];
+                    if constexpr (WT > 0)
+                        load_code<WT>(reinterpret_cast<const uint32_t *>(prw[sr] + g.code) +
+                                          static_cast<uint64_t>(nsafe[sr]) * WT,
+                                      vec_ok, code[sr]);
+                }
+#pragma unroll
+                for (int sr = 0; sr < SR; ++sr)
+                    if (!lact[sr]) cid[sr] = kMaxIndex;
                 // (b) visited test against the table as it stood at the round's start
 #pragma unroll
                 for (int sr = 0; sr < SR; ++sr) val[sr] = cid[sr] != kMaxIndex && cid[sr] < P.npoints;
