@@ -246,7 +246,10 @@ __device__ __forceinline__ int lane_id() {
 
 __device__ __forceinline__ int lane_id_opaque() { return lane_id(); }
 
-__device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
+// Lane masks straight from a bool (HIP's __ballot / __any take an int, which
+// costs a mask -> 0/1 -> mask round trip per use).
+__device__ __forceinline__ uint64_t ballot(bool p) { return __builtin_amdgcn_ballot_w64(p); }
+__device__ __forceinline__ bool any_lane(bool p) { return ballot(p) != 0ull; }
 
 __device__ __forceinline__ uint32_t half_bits(uint64_t m, int h) {
     return static_cast<uint32_t>(m >> (32 * h));
@@ -266,6 +269,14 @@ __host__ __device__ constexpr uint64_t lane_bit_mask(int v) {
 // A uniform lane mask as this lane's bool (no instructions: the mask is the
 // condition register).
 __device__ __forceinline__ bool lane_in(uint64_t mask) { return __builtin_amdgcn_inverse_ballot_w64(mask); }
+
+// Set bits in this lane's 32-lane half of a ballot: two scalar counts and
+// one select, instead of a per-lane 64-bit shift and count.
+__device__ __forceinline__ uint32_t half_popc(uint64_t m) {
+    const uint32_t lo = static_cast<uint32_t>(__popc(static_cast<uint32_t>(m)));
+    const uint32_t hi = static_cast<uint32_t>(__popc(static_cast<uint32_t>(m >> 32)));
+    return lane_in(0xFFFFFFFF00000000ull) ? hi : lo;
+}
 
 // Lane i reads lane i ^ m, all lanes active.  m < 16 stays inside a 16-lane
 // row: DPP quad_perm (1, 2), half-row mirror then quad reverse
@@ -299,20 +310,30 @@ __device__ __forceinline__ uint32_t xshfl(uint32_t v, int m) {
     return static_cast<uint32_t>(xshfl(static_cast<int>(v), m));
 }
 
+// Reductions over all 64 lanes (xor distances 32 .. 1, written out).
 __device__ __forceinline__ float wave_min(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fminf(v, xshfl(v, m));
-    return v;
+    v = fminf(v, xshfl(v, 32));
+    v = fminf(v, xshfl(v, 16));
+    v = fminf(v, xshfl(v, 8));
+    v = fminf(v, xshfl(v, 4));
+    v = fminf(v, xshfl(v, 2));
+    return fminf(v, xshfl(v, 1));
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, xshfl(v, m));
-    return v;
+    v = fmaxf(v, xshfl(v, 32));
+    v = fmaxf(v, xshfl(v, 16));
+    v = fmaxf(v, xshfl(v, 8));
+    v = fmaxf(v, xshfl(v, 4));
+    v = fmaxf(v, xshfl(v, 2));
+    return fmaxf(v, xshfl(v, 1));
 }
 __device__ __forceinline__ int wave_sum(int v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += xshfl(v, m);
-    return v;
+    v += xshfl(v, 32);
+    v += xshfl(v, 16);
+    v += xshfl(v, 8);
+    v += xshfl(v, 4);
+    v += xshfl(v, 2);
+    return v + xshfl(v, 1);
 }
 
 // uniform value -> scalar register
@@ -604,7 +625,7 @@ __device__ __forceinline__ void merge_path(const SearchParams &P, uint2 *bp, con
             done[k] = done[k] || found;
             live |= !done[k];
         }
-        if (!__any(live)) break;
+        if (!any_lane(live)) break;
     }
     res[0] = __shfl_up(res[SPL], 1);
     if (lane == 0) res[0] = 0;
@@ -897,86 +918,119 @@ __device__ __forceinline__ int32_t raw_regs(const uint32_t (&c)[WT], const uint3
     return static_cast<int32_t>(raw);
 }
 
+// One pass of exact distances over children e0 .. e0 + 2 PB - 1 (child
+// e0 + 2 j + h on half h): PB row loads per lane issued together, then a
+// reduce-scatter over the half.  At distance 16 lanes keep children
+// j < PB/2 (lower) / j + PB/2 (upper), at 8 the same on what is left, and so
+// on until one child per lane group remains; the remaining distances are
+// butterflies.  Every step adds lane l and lane l ^ m of the same child, in
+// the order 16, 8, 4, 2, 1, so each child's sum is the shfl_down tree of
+// utils.cuh:277-281 up to operand order.
+template <int PB, int DPL, class G>
+__device__ __forceinline__ void exact_pass(const SearchParams &P, const G &g, int e0, int n, const uint32_t *slot_list,
+                                           float *cd, const uint32_t *ci, const float (&qr)[DPL], bool ip) {
+    const int lane = lane_id();
+    const int h = lane >> 5, nl = lane & 31;
+    float v[PB][DPL];
+    int slot[PB];
+#pragma unroll
+    for (int j = 0; j < PB; ++j) {
+        const int e = e0 + 2 * j + h;
+        const bool act = e < n;
+        slot[j] = act ? static_cast<int>(slot_list ? slot_list[e] : static_cast<uint32_t>(e)) : -1;
+        const uint32_t child = act ? ci[slot[j]] : 0u;
+        const float *row = P.data + static_cast<uint64_t>(child) * g.row;
+#pragma unroll
+        for (int k = 0; k < DPL; ++k) {
+            const int i = nl + 32 * k;
+            v[j][k] = (act && i < g.dim) ? row[i] : 0.0f;
+        }
+    }
+    float acc[PB];
+#pragma unroll
+    for (int j = 0; j < PB; ++j) {
+        acc[j] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < DPL; ++k) {
+            const int i = nl + 32 * k;
+            if (i < g.dim) {
+                if (ip) {
+                    acc[j] = fmaf(qr[k], v[j][k], acc[j]);
+                } else {
+                    const float d = qr[k] - v[j][k];
+                    acc[j] = fmaf(d, d, acc[j]);
+                }
+            }
+        }
+    }
+    // reduce-scatter while more than one child is left per lane
+    int c = 0;  // index of the child this lane's value belongs to
+    constexpr int L16 = PB >= 2 ? PB / 2 : 1;
+    float r16[L16];
+    if constexpr (PB >= 2) {
+        const bool b = (nl & 16) != 0;
+#pragma unroll
+        for (int j = 0; j < L16; ++j) {
+            const float send = b ? acc[j] : acc[j + L16];
+            const float own = b ? acc[j + L16] : acc[j];
+            r16[j] = own + xshfl(send, 16);
+        }
+        c += b ? L16 : 0;
+    } else {
+        r16[0] = acc[0] + xshfl(acc[0], 16);
+    }
+    constexpr int L8 = L16 >= 2 ? L16 / 2 : 1;
+    float r8[L8];
+    if constexpr (L16 >= 2) {
+        const bool b = (nl & 8) != 0;
+#pragma unroll
+        for (int j = 0; j < L8; ++j) {
+            const float send = b ? r16[j] : r16[j + L8];
+            const float own = b ? r16[j + L8] : r16[j];
+            r8[j] = own + xshfl(send, 8);
+        }
+        c += b ? L8 : 0;
+    } else {
+        r8[0] = r16[0] + xshfl(r16[0], 8);
+    }
+    float r4;
+    if constexpr (L8 >= 2) {
+        const bool b = (nl & 4) != 0;
+        const float send = b ? r8[0] : r8[1];
+        const float own = b ? r8[1] : r8[0];
+        r4 = own + xshfl(send, 4);
+        c += b ? 1 : 0;
+    } else {
+        r4 = r8[0] + xshfl(r8[0], 4);
+    }
+    r4 += xshfl(r4, 2);
+    r4 += xshfl(r4, 1);
+    // lanes holding child c: one writer per child (the lowest lane of its group)
+    constexpr int kGroup = PB >= 8 ? 4 : PB >= 4 ? 8 : PB >= 2 ? 16 : 32;
+    int my_slot = -1;
+#pragma unroll
+    for (int j = 0; j < PB; ++j)
+        if (j == c) my_slot = slot[j];
+    if (my_slot >= 0 && (nl & (kGroup - 1)) == 0) cd[my_slot] = ip ? -r4 : r4;
+}
+
 // Exact distances for n children held in cd/ci at slots slot_list[0..n)
-// (or 0..n when slot_list is null): two children per pass, PB passes with
-// their row loads issued together (DPL > 0: dims per lane known at compile
-// time; DPL == 0: generic loop).
+// (or 0..n when slot_list is null): passes of 16 children, the last one
+// sized to what is left (DPL > 0: dims per lane known at compile time;
+// DPL == 0: generic loop, two children per pass).
 template <int DPL, class G>
-__device__ void exact_batch(const SearchParams &P, const G &g, int n, const uint32_t *slot_list, float *cd,
+__device__ __forceinline__ void exact_batch(const SearchParams &P, const G &g, int n, const uint32_t *slot_list, float *cd,
                             const uint32_t *ci, const float (&qr)[DPL > 0 ? DPL : 1], const float *qv) {
     const int lane = lane_id();
     const int h = lane >> 5, nl = lane & 31;
     const bool ip = P.use_ip != 0;
     if constexpr (DPL > 0) {
-        constexpr int PB = 8;
-        for (int e0 = 0; e0 < n; e0 += 2 * PB) {
-            float v[PB][DPL];
-            int slot[PB];
-#pragma unroll
-            for (int j = 0; j < PB; ++j) {
-                const int e = e0 + 2 * j + h;
-                const bool act = e < n;
-                slot[j] = act ? static_cast<int>(slot_list ? slot_list[e] : static_cast<uint32_t>(e)) : -1;
-                const uint32_t child = act ? ci[slot[j]] : 0u;
-                const float *row = P.data + static_cast<uint64_t>(child) * g.row;
-#pragma unroll
-                for (int k = 0; k < DPL; ++k) {
-                    const int i = nl + 32 * k;
-                    v[j][k] = (act && i < g.dim) ? row[i] : 0.0f;
-                }
-            }
-            float acc[PB];
-#pragma unroll
-            for (int j = 0; j < PB; ++j) {
-                acc[j] = 0.0f;
-#pragma unroll
-                for (int k = 0; k < DPL; ++k) {
-                    const int i = nl + 32 * k;
-                    if (i < g.dim) {
-                        if (ip) {
-                            acc[j] = fmaf(qr[k], v[j][k], acc[j]);
-                        } else {
-                            const float d = qr[k] - v[j][k];
-                            acc[j] = fmaf(d, d, acc[j]);
-                        }
-                    }
-                }
-            }
-            // Reduce-scatter over the half: at distance 16 lanes keep children
-            // j (lower) / j+4 (upper), at 8 keep j / j+2, at 4 keep j / j+1, then
-            // butterflies at 2 and 1.  Every step adds lane l and lane l^m of
-            // the same child, so each child's sum is the shfl_down tree of
-            // utils.cuh:277-281 up to operand order.
-            float r16[4], r8[2];
-            const bool b16 = (nl & 16) != 0, b8 = (nl & 8) != 0, b4 = (nl & 4) != 0;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float send = b16 ? acc[j] : acc[j + 4];
-                const float own = b16 ? acc[j + 4] : acc[j];
-                r16[j] = own + xshfl(send, 16);
-            }
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const float send = b8 ? r16[j] : r16[j + 2];
-                const float own = b8 ? r16[j + 2] : r16[j];
-                r8[j] = own + xshfl(send, 8);
-            }
-            float r4;
-            {
-                const float send = b4 ? r8[0] : r8[1];
-                const float own = b4 ? r8[1] : r8[0];
-                r4 = own + xshfl(send, 4);
-            }
-            r4 += xshfl(r4, 2);
-            r4 += xshfl(r4, 1);
-            const int c = (b16 ? 4 : 0) + (b8 ? 2 : 0) + (b4 ? 1 : 0);
-            int my_slot = -1;
-#pragma unroll
-            for (int j = 0; j < PB; ++j)
-                if (j == c) my_slot = slot[j];
-            if (my_slot >= 0 && (nl & 3) == 0) cd[my_slot] = ip ? -r4 : r4;
-            if (2 * PB >= n - e0) break;
-        }
+        int e0 = 0;
+        for (; n - e0 > 8; e0 += 16) exact_pass<8, DPL>(P, g, e0, n, slot_list, cd, ci, qr, ip);
+        const int rem = n - e0;
+        if (rem > 4) exact_pass<4, DPL>(P, g, e0, n, slot_list, cd, ci, qr, ip);
+        else if (rem > 2) exact_pass<2, DPL>(P, g, e0, n, slot_list, cd, ci, qr, ip);
+        else if (rem > 0) exact_pass<1, DPL>(P, g, e0, n, slot_list, cd, ci, qr, ip);
     } else {
         for (int e0 = 0; e0 < n; e0 += 2) {
             const int e = e0 + h;
@@ -1051,7 +1105,7 @@ __device__ __forceinline__ void hash_contains_n(const uint32_t *t, uint32_t nb, 
             // codes and factors are live here too
             if (s & 1) __builtin_amdgcn_sched_barrier(0);
         }
-        if (!__any(anyp)) break;
+        if (!any_lane(anyp)) break;
     }
 }
 
@@ -1232,6 +1286,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
         const bool kth_valid = finite_below_max(kth);
         FG_PHASE(3);
 
+        // children to score exactly, set by either stage (one call site below)
+        int ex_n = 0;
+        const uint32_t *ex_list = nullptr;
         if (theta <= 1) {
             // ---------------- single expander (adaptive_search.cuh:221-343)
             const int cwc = deg < cbs ? deg : cbs;
@@ -1323,9 +1380,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
             __syncthreads();
             const int nins = __popc(ins_mask);
             FG_COUNT(c_exact += static_cast<uint32_t>(nins));
+            ex_n = nins;
+            ex_list = alist;
             FG_PHASE(4);
-            exact_batch<DPL>(P, g, nins, alist, cd, ci, qr, qv);
-            FG_PHASE(5);
         } else {
             // ---------------- speculative expansion (adaptive_search.cuh:344-444)
             FG_COUNT(if (c_st2 == kMaxIndex) c_st2 = static_cast<uint32_t>(iter));
@@ -1394,7 +1451,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
                 int keep[SR];
 #pragma unroll
                 for (int sr = 0; sr < SR; ++sr) {
-                    const int rvc = __popc(half_bits(ballot(val[sr]), h));
+                    const int rvc = static_cast<int>(half_popc(ballot(val[sr])));
                     const int lim = an[sr] == an_full ? lim_full : lim_last;
                     keep[sr] = tsk[sr] >= 0 ? lim : 0;
                     need[sr] = !(keep[sr] >= rvc);
@@ -1425,10 +1482,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
                         val[sr] = isfinite(est);
                     }
                     bool kl = val[sr];
-                    const bool any_need = __any(need[sr]);
+                    const bool any_need = any_lane(need[sr]);
                     if (any_need) {
                         const bool below = val[sr] && kth_valid && est <= kth;
-                        const uint32_t near = __popc(half_bits(ballot(below), h));
+                        const uint32_t near = half_popc(ballot(below));
                         int eff = keep[sr];
                         if (need[sr]) eff = keep_with_cutoff(keep[sr], kth_valid, near);
                         // With a valid cutoff and 1 <= near <= keep the count is
@@ -1474,7 +1531,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
                 const uint32_t key = mine ? alist[lane] : kMaxIndex;
                 const uint32_t got = mine ? hash_insert(H, nbk, key) : 0u;
                 bool acc = got != 0u;
-                if (__any(mine && !got)) {
+                if (any_lane(mine && !got)) {
                     const uint32_t members = half_bits(ballot(mine), 0);
                     acc = mine && !dup_of_earlier(key, members, nl, 0);
                 }
@@ -1491,10 +1548,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
             }
             if (compact > static_cast<uint32_t>(P.collect_cap)) compact = static_cast<uint32_t>(P.collect_cap);
             FG_COUNT(c_exact += compact);
+            ex_n = static_cast<int>(compact);
             FG_PHASE(7);
-            exact_batch<DPL>(P, g, static_cast<int>(compact), nullptr, cd, ci, qr, qv);
-            FG_PHASE(8);
         }
+        exact_batch<DPL>(P, g, ex_n, ex_list, cd, ci, qr, qv);
+        if (theta <= 1) FG_PHASE(5);
+        else FG_PHASE(8);
         __syncthreads();
     }
 
