@@ -935,15 +935,19 @@ __device__ __forceinline__ void exact_pass(const SearchParams &P, const G &g, in
     int slot[PB];
 #pragma unroll
     for (int j = 0; j < PB; ++j) {
+        // loads are unconditional: an inactive lane reads a valid list entry
+        // and candidate slot and then row 0; its sum is never written
         const int e = e0 + 2 * j + h;
         const bool act = e < n;
-        slot[j] = act ? static_cast<int>(slot_list ? slot_list[e] : static_cast<uint32_t>(e)) : -1;
-        const uint32_t child = act ? ci[slot[j]] : 0u;
+        const int ec = e < 32 ? e : 31;
+        const int sl = slot_list ? static_cast<int>(slot_list[ec] & 31u) : ec;  // entries past n may be stale
+        slot[j] = act ? sl : -1;
+        const uint32_t child = act ? ci[sl] : 0u;
         const float *row = P.data + static_cast<uint64_t>(child) * g.row;
 #pragma unroll
         for (int k = 0; k < DPL; ++k) {
             const int i = nl + 32 * k;
-            v[j][k] = (act && i < g.dim) ? row[i] : 0.0f;
+            v[j][k] = i < g.dim ? row[i] : 0.0f;
         }
     }
     float acc[PB];
@@ -1089,21 +1093,15 @@ __device__ __forceinline__ void hash_contains_n(const uint32_t *t, uint32_t nb, 
         bool anyp = false;
 #pragma unroll
         for (int s = 0; s < NK; ++s) {
-            if (pend[s]) {
-                const uint4 sl = t4[b[s]];
-                if (bucket_has(sl, key[s])) {
-                    pend[s] = false;  // contained: not a fresh child
-                    test[s] = false;
-                } else if (bucket_open(sl)) {
-                    pend[s] = false;  // absent
-                } else {
-                    b[s] = hash_next(b[s], nb);
-                }
-            }
+            // branch-free: every lane reads a bucket (its index is always
+            // in range) and the pending ones take the update
+            const uint4 sl = t4[b[s]];
+            const bool has = bucket_has(sl, key[s]);
+            const bool go_on = pend[s] && !has && !bucket_open(sl);
+            test[s] = (pend[s] && has) ? false : test[s];  // contained: not a fresh child
+            b[s] = go_on ? hash_next(b[s], nb) : b[s];
+            pend[s] = go_on;
             anyp |= pend[s];
-            // at most two buckets (8 VGPRs) in flight: the search loop's
-            // codes and factors are live here too
-            if (s & 1) __builtin_amdgcn_sched_barrier(0);
         }
         if (!any_lane(anyp)) break;
     }
@@ -1466,21 +1464,21 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
 #pragma unroll
                 for (int sr = 0; sr < SR; ++sr) {
                     float est = FLT_MAX;
-                    if (need[sr] && val[sr]) {
-                        if (tx[sr] != FLT_MAX) {
-                            int32_t raw;
-                            if constexpr (WT > 0) {
-                                raw = rawb[sr];
-                            } else {
-                                const int nidx = tsk[sr] + nl;
-                                raw = raw_partial(reinterpret_cast<const uint32_t *>(prw[sr] + g.code) +
-                                                      static_cast<uint64_t>(nidx) * W,
-                                                  0, W, planes, W);
-                            }
-                            est = estimate_formula(raw, sum_q, qwidth, qlow, tx[sr], fdq[sr], fvq[sr], pdist[pix[sr]]);
-                        }
-                        val[sr] = isfinite(est);
+                    const bool scored = need[sr] && val[sr];
+                    if constexpr (WT > 0) {
+                        // computed on every lane and selected (most lanes need it;
+                        // a branch would cost more than the few wasted lanes)
+                        const float e = estimate_formula(rawb[sr], sum_q, qwidth, qlow, tx[sr], fdq[sr], fvq[sr],
+                                                         pdist[pix[sr]]);
+                        est = (scored && tx[sr] != FLT_MAX) ? e : FLT_MAX;
+                    } else if (scored && tx[sr] != FLT_MAX) {
+                        const int nidx = tsk[sr] + nl;
+                        const int32_t raw = raw_partial(reinterpret_cast<const uint32_t *>(prw[sr] + g.code) +
+                                                            static_cast<uint64_t>(nidx) * W,
+                                                        0, W, planes, W);
+                        est = estimate_formula(raw, sum_q, qwidth, qlow, tx[sr], fdq[sr], fvq[sr], pdist[pix[sr]]);
                     }
+                    val[sr] = scored ? isfinite(est) : val[sr];
                     bool kl = val[sr];
                     const bool any_need = any_lane(need[sr]);
                     if (any_need) {
