@@ -1295,23 +1295,21 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
             const float *prow = data + static_cast<uint64_t>(parent) * g.row;
             const uint32_t *nbrs = reinterpret_cast<const uint32_t *>(prow + g.nbr);
             FG_COUNT(c_ids += static_cast<uint32_t>(cwc));
-            uint32_t child = kMaxIndex;
-            float tx = 0.0f, fdq = 0.0f, fvq = 0.0f;
+            // id, factors and code issued together (one HBM round trip);
+            // unconditional loads, lanes past cwc read the last slot
+            const int nsafe = nl < cwc ? nl : cwc - 1;
+            const float *factors = prow + g.factor;
+            uint32_t ck[1] = {nbrs[nsafe]};
+            const float tx = factors[nsafe];
+            const float fdq = factors[deg + nsafe];
+            const float fvq = factors[2 * deg + nsafe];
             uint32_t c1[1][WTR];
-#pragma unroll
-            for (int w = 0; w < WTR; ++w) c1[0][w] = 0u;
-            if (nl < cwc) {
-                // id, factors and code issued together (one HBM round trip)
-                const float *factors = prow + g.factor;
-                child = nbrs[nl];
-                tx = factors[nl];
-                fdq = factors[deg + nl];
-                fvq = factors[2 * deg + nl];
-                if constexpr (WT > 0)
-                    load_code<WT>(reinterpret_cast<const uint32_t *>(prow + g.code) + static_cast<uint64_t>(nl) * WT,
-                                  vec_ok, c1[0]);
-                if (child >= P.npoints || hash_contains(H, nbk, child)) child = kMaxIndex;
-            }
+            if constexpr (WT > 0)
+                load_code<WT>(reinterpret_cast<const uint32_t *>(prow + g.code) + static_cast<uint64_t>(nsafe) * WT,
+                              vec_ok, c1[0]);
+            bool fresh[1] = {nl < cwc && ck[0] < P.npoints};
+            hash_contains_n<1>(H, nbk, ck, fresh);
+            uint32_t child = fresh[0] ? ck[0] : kMaxIndex;
             const uint32_t vmask = half_bits(ballot(child != kMaxIndex), 0);
             const int valid_count = __popc(vmask);
             const int keep = keep_count_for_expander(static_cast<uint32_t>(cwc), 1, ctl.rho, false, 0);
@@ -1324,21 +1322,17 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
                 const bool valid = child != kMaxIndex;
                 float est = FLT_MAX;
                 int32_t r1[1] = {0};
-                if constexpr (WT > 0) raw_batch<1, WT>(c1, planes, any_wrap, r1);
-                if (valid) {
-                    int32_t raw;
-                    if constexpr (WT > 0) {
-                        raw = r1[0];
-                    } else {
-                        raw = raw_partial(codes + static_cast<uint64_t>(nl) * W, 0, W, planes, W);
-                    }
+                if constexpr (WT > 0) {
+                    // computed on every lane, selected for the valid ones
+                    raw_batch<1, WT>(c1, planes, any_wrap, r1);
+                    est = tx == FLT_MAX ? 0.0f : estimate_formula(r1[0], sum_q, qwidth, qlow, tx, fdq, fvq, pd0);
+                } else if (valid) {
+                    const int32_t raw = raw_partial(codes + static_cast<uint64_t>(nl) * W, 0, W, planes, W);
                     est = tx == FLT_MAX ? 0.0f : estimate_formula(raw, sum_q, qwidth, qlow, tx, fdq, fvq, pd0);
-                    if (!isfinite(est)) {
-                        child = kMaxIndex;
-                        est = FLT_MAX;
-                    }
-                    dist = est;
                 }
+                const bool fin = isfinite(est);
+                child = (valid && !fin) ? kMaxIndex : child;
+                dist = valid ? (fin ? est : FLT_MAX) : dist;
                 uint32_t near = 0;
                 if (kth_valid)
                     near = __popc(half_bits(ballot(child != kMaxIndex && isfinite(dist) && dist <= kth), 0));
