@@ -1240,10 +1240,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
         FG_PHASE(2);
         if (iter >= P.max_iter) break;
         for (int i = beam_sz + lane; i < pbeam; i += 64) bp[i] = kEmpty;
-        if (lane < 32) {
-            cd[lane] = FLT_MAX;
-            ci[lane] = kMaxIndex;
-        }
+        cd[nl] = FLT_MAX;  // both halves store the same values: no branch
+        ci[nl] = kMaxIndex;
         __syncthreads();
         float kth = FLT_MAX;  // adaptive_search_utils.cuh:25-30
         if (bp[beam_sz - 1].y != kMaxIndex) kth = __uint_as_float(bp[(P.K < beam_sz ? P.K : beam_sz) - 1].x);
@@ -1257,8 +1255,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
         uint32_t nexp = 0;
         for (int base = 0; base < beam_sz; base += 64) {
             const int j = base + lane;
-            const uint2 e = j < beam_sz ? bp[j] : make_uint2(0u, kMsb);
-            const bool fresh = (e.y & kMsb) == 0;
+            const uint2 e = bp[j < pbeam ? j : pbeam];  // unconditional read; bp[pbeam] is a sentinel
+            const bool fresh = j < beam_sz && (e.y & kMsb) == 0;
             const uint64_t m = ballot(fresh);
             if (fresh) {
                 const uint32_t r = static_cast<uint32_t>(__popcll(m & ((1ull << lane) - 1ull))) + nexp;
