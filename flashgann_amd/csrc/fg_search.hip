@@ -701,14 +701,24 @@ __device__ __forceinline__ void merge_beam(const SearchParams &P, uint2 *bp, uin
 // ------------------------------------------------------------ visited table
 
 // Visited set (the reference's utils.cuh:682-750 table, same membership
-// semantics): an exact set of node ids in LDS, open addressing over 4-slot
-// buckets, one 16-byte read per probe.  A key goes to the first bucket of its
-// probe sequence (home, home+1, .. wrapping) with an empty slot, so a lookup
-// stops at the first bucket that holds the key or an empty slot.  Empty slots
-// are 0xFFFFFFFF; keys (node ids, and 0x7FFFFFFF for the restore of an empty
-// beam slot, utils.cuh:747-748) have the top bit clear.
+// semantics): an exact set of node ids in LDS in 4-slot buckets, one 16-byte
+// read per bucket.  Each key has two buckets, its home and its alternate; it
+// is added to whichever of the two has more empty slots (the home on a tie),
+// and only when both are full to the first bucket with an empty slot after
+// the alternate (wrapping).  Slots of a bucket fill in order and stay filled
+// until the reset, so a bucket is full iff its last slot is taken and a full
+// bucket stays full: a lookup reads both buckets and walks on only when both
+// are full, stopping at the first bucket that holds the key or has room.
+// Empty slots are 0xFFFFFFFF; keys (node ids, and 0x7FFFFFFF for the restore
+// of an empty beam slot, utils.cuh:747-748) have the top bit clear.
 __device__ __forceinline__ uint32_t hash_home(uint32_t key, uint32_t nb) {
     const uint32_t h16 = (key ^ (key >> 13)) & 0xFFFFu;
+    return __umul24(h16, nb) >> 16;
+}
+
+// bits 8..23 of a 24-bit product of the key: mixed independently of the home
+__device__ __forceinline__ uint32_t hash_alt(uint32_t key, uint32_t nb) {
+    const uint32_t h16 = (__umul24(key, 0x9E3779u) >> 8) & 0xFFFFu;
     return __umul24(h16, nb) >> 16;
 }
 
@@ -720,27 +730,42 @@ __device__ __forceinline__ bool bucket_has(uint4 s, uint32_t key) {
     return min(min(s.x ^ key, s.y ^ key), min(s.z ^ key, s.w ^ key)) == 0u;
 }
 
-__device__ __forceinline__ bool bucket_open(uint4 s) { return static_cast<int32_t>(s.x | s.y | s.z | s.w) < 0; }
+__device__ __forceinline__ bool bucket_open(uint4 s) { return static_cast<int32_t>(s.w) < 0; }
+
+__device__ __forceinline__ bool both_full(uint4 a, uint4 b) { return static_cast<int32_t>(a.w | b.w) >= 0; }
+
+// number of empty slots (the empty ones are the last)
+__device__ __forceinline__ uint32_t bucket_free(uint4 s) { return (s.x >> 31) + (s.y >> 31) + (s.z >> 31) + (s.w >> 31); }
 
 // 1 if the key was added, 0 if it was present (utils.cuh:697-716).
 __device__ __forceinline__ uint32_t hash_insert(uint32_t *t, uint32_t nb, uint32_t key) {
     const uint4 *t4 = reinterpret_cast<const uint4 *>(t);
-    uint32_t b = hash_home(key, nb);
+    const uint32_t ba = hash_home(key, nb), bb = hash_alt(key, nb);
+    // a failed CAS means another lane filled a slot of one of the two
+    // buckets: at most 8 passes before both are full
+    for (int pass = 0; pass < 9; ++pass) {
+        const uint4 sa = t4[ba], sb = t4[bb];
+        if (bucket_has(sa, key) || bucket_has(sb, key)) return 0;
+        const uint32_t fa = bucket_free(sa), fb = bucket_free(sb);
+        if (fa == 0u && fb == 0u) break;
+        const bool alt = fb > fa;
+        const uint32_t slot = 4u * (alt ? bb : ba) + 4u - (alt ? fb : fa);
+        const uint32_t old = atomicCAS(&t[slot], kMaxIndex, key);
+        if (old == kMaxIndex) return 1;
+        if (old == key) return 0;
+    }
+    uint32_t b = hash_next(bb, nb);
     // each pass either moves to the next bucket or retries after another
     // lane filled a slot of this one: at most 5 passes per bucket
     for (uint32_t i = 0; i < 5u * nb; ++i) {
         const uint4 sl = t4[b];
         if (bucket_has(sl, key)) return 0;
-        const int j = static_cast<int32_t>(sl.x) < 0   ? 0
-                      : static_cast<int32_t>(sl.y) < 0 ? 1
-                      : static_cast<int32_t>(sl.z) < 0 ? 2
-                      : static_cast<int32_t>(sl.w) < 0 ? 3
-                                                         : -1;
-        if (j < 0) {
+        const uint32_t f = bucket_free(sl);
+        if (f == 0u) {
             b = hash_next(b, nb);
             continue;
         }
-        const uint32_t old = atomicCAS(&t[4u * b + static_cast<uint32_t>(j)], kMaxIndex, key);
+        const uint32_t old = atomicCAS(&t[4u * b + 4u - f], kMaxIndex, key);
         if (old == kMaxIndex) return 1;
         if (old == key) return 0;
     }
@@ -749,7 +774,11 @@ __device__ __forceinline__ uint32_t hash_insert(uint32_t *t, uint32_t nb, uint32
 
 __device__ __forceinline__ bool hash_contains(const uint32_t *t, uint32_t nb, uint32_t key) {
     const uint4 *t4 = reinterpret_cast<const uint4 *>(t);
-    uint32_t b = hash_home(key, nb);
+    const uint32_t bb = hash_alt(key, nb);
+    const uint4 sa = t4[hash_home(key, nb)], sb = t4[bb];
+    if (bucket_has(sa, key) || bucket_has(sb, key)) return true;
+    if (!both_full(sa, sb)) return false;
+    uint32_t b = hash_next(bb, nb);
     for (uint32_t i = 0; i < nb; ++i) {
         const uint4 sl = t4[b];
         if (bucket_has(sl, key)) return true;
@@ -1077,30 +1106,35 @@ __device__ __forceinline__ bool select_smallest(float value, bool valid, int kee
     return kept;
 }
 
-// Visited test for up to four keys per lane, probes advanced together.
+// Visited test for up to four keys per lane: both buckets of every key are
+// read at once; the rare keys whose two buckets are full walk on together.
 template <int NK>
 __device__ __forceinline__ void hash_contains_n(const uint32_t *t, uint32_t nb, const uint32_t (&key)[NK],
                                                 bool (&test)[NK]) {
     const uint4 *t4 = reinterpret_cast<const uint4 *>(t);
     uint32_t b[NK];
     bool pend[NK];
+    bool anyp = false;
 #pragma unroll
     for (int s = 0; s < NK; ++s) {
-        b[s] = hash_home(key[s], nb);
-        pend[s] = test[s];
+        // branch-free: every lane reads both buckets (indices always in range)
+        b[s] = hash_alt(key[s], nb);
+        const uint4 sa = t4[hash_home(key[s], nb)], sb = t4[b[s]];
+        const bool has = bucket_has(sa, key[s]) || bucket_has(sb, key[s]);
+        pend[s] = test[s] && !has && both_full(sa, sb);
+        test[s] = test[s] && !has;  // contained: not a fresh child
+        anyp |= pend[s];
     }
+    if (!any_lane(anyp)) return;
     for (uint32_t step = 0; step < nb; ++step) {
-        bool anyp = false;
+        anyp = false;
 #pragma unroll
         for (int s = 0; s < NK; ++s) {
-            // branch-free: every lane reads a bucket (its index is always
-            // in range) and the pending ones take the update
+            b[s] = pend[s] ? hash_next(b[s], nb) : b[s];
             const uint4 sl = t4[b[s]];
             const bool has = bucket_has(sl, key[s]);
-            const bool go_on = pend[s] && !has && !bucket_open(sl);
-            test[s] = (pend[s] && has) ? false : test[s];  // contained: not a fresh child
-            b[s] = go_on ? hash_next(b[s], nb) : b[s];
-            pend[s] = go_on;
+            test[s] = (pend[s] && has) ? false : test[s];
+            pend[s] = pend[s] && !has && !bucket_open(sl);
             anyp |= pend[s];
         }
         if (!any_lane(anyp)) break;
