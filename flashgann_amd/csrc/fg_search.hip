@@ -979,17 +979,24 @@ __device__ __forceinline__ void exact_pass(const SearchParams &P, const G &g, in
             v[j][k] = i < g.dim ? row[i] : 0.0f;
         }
     }
+    // the metric test sits outside the loops: inside, each dimension became
+    // both updates and a select
     float acc[PB];
+    if (ip) {
 #pragma unroll
-    for (int j = 0; j < PB; ++j) {
-        acc[j] = 0.0f;
+        for (int j = 0; j < PB; ++j) {
+            acc[j] = 0.0f;
 #pragma unroll
-        for (int k = 0; k < DPL; ++k) {
-            const int i = nl + 32 * k;
-            if (i < g.dim) {
-                if (ip) {
-                    acc[j] = fmaf(qr[k], v[j][k], acc[j]);
-                } else {
+            for (int k = 0; k < DPL; ++k)
+                if (nl + 32 * k < g.dim) acc[j] = fmaf(qr[k], v[j][k], acc[j]);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < PB; ++j) {
+            acc[j] = 0.0f;
+#pragma unroll
+            for (int k = 0; k < DPL; ++k) {
+                if (nl + 32 * k < g.dim) {
                     const float d = qr[k] - v[j][k];
                     acc[j] = fmaf(d, d, acc[j]);
                 }
