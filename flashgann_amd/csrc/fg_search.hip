@@ -960,24 +960,34 @@ __device__ __forceinline__ void exact_pass(const SearchParams &P, const G &g, in
                                            float *cd, const uint32_t *ci, const float (&qr)[DPL], bool ip) {
     const int lane = lane_id();
     const int h = lane >> 5, nl = lane & 31;
+    // loads are unconditional: an inactive lane reads a valid list entry
+    // and candidate slot and then row 0; its sum is never written.  Slots,
+    // then ids, then rows, each group issued together.
+    int sl[PB];
+    if (slot_list) {
+#pragma unroll
+        for (int j = 0; j < PB; ++j) {
+            const int e = e0 + 2 * j + h;
+            sl[j] = static_cast<int>(slot_list[e < 32 ? e : 31] & 31u);  // entries past n may be stale
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < PB; ++j) {
+            const int e = e0 + 2 * j + h;
+            sl[j] = e < 32 ? e : 31;
+        }
+    }
+    uint32_t cid[PB];
+#pragma unroll
+    for (int j = 0; j < PB; ++j) cid[j] = ci[sl[j]];
     float v[PB][DPL];
-    int slot[PB];
+    const float *dl = P.data + nl;  // this lane's first dimension of row 0
 #pragma unroll
     for (int j = 0; j < PB; ++j) {
-        // loads are unconditional: an inactive lane reads a valid list entry
-        // and candidate slot and then row 0; its sum is never written
-        const int e = e0 + 2 * j + h;
-        const bool act = e < n;
-        const int ec = e < 32 ? e : 31;
-        const int sl = slot_list ? static_cast<int>(slot_list[ec] & 31u) : ec;  // entries past n may be stale
-        slot[j] = act ? sl : -1;
-        const uint32_t child = act ? ci[sl] : 0u;
-        const float *row = P.data + static_cast<uint64_t>(child) * g.row;
+        const uint32_t child = e0 + 2 * j + h < n ? cid[j] : 0u;
+        const float *row = dl + static_cast<uint64_t>(child) * g.row;
 #pragma unroll
-        for (int k = 0; k < DPL; ++k) {
-            const int i = nl + 32 * k;
-            v[j][k] = i < g.dim ? row[i] : 0.0f;
-        }
+        for (int k = 0; k < DPL; ++k) v[j][k] = nl + 32 * k < g.dim ? row[32 * k] : 0.0f;
     }
     // the metric test sits outside the loops: inside, each dimension became
     // both updates and a select
@@ -1047,11 +1057,11 @@ __device__ __forceinline__ void exact_pass(const SearchParams &P, const G &g, in
     r4 += xshfl(r4, 1);
     // lanes holding child c: one writer per child (the lowest lane of its group)
     constexpr int kGroup = PB >= 8 ? 4 : PB >= 4 ? 8 : PB >= 2 ? 16 : 32;
-    int my_slot = -1;
-#pragma unroll
-    for (int j = 0; j < PB; ++j)
-        if (j == c) my_slot = slot[j];
-    if (my_slot >= 0 && (nl & (kGroup - 1)) == 0) cd[my_slot] = ip ? -r4 : r4;
+    const int e = e0 + 2 * c + h;
+    if (e < n && (nl & (kGroup - 1)) == 0) {
+        const int sl = slot_list ? static_cast<int>(slot_list[e] & 31u) : e;
+        cd[sl] = ip ? -r4 : r4;
+    }
 }
 
 // Exact distances for n children held in cd/ci at slots slot_list[0..n)
