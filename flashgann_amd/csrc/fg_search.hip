@@ -282,17 +282,19 @@ __device__ __forceinline__ uint32_t half_popc(uint64_t m) {
 // row: DPP quad_perm (1, 2), half-row mirror then quad reverse
 // ((i^7)^3 = i^4), row mirror then half-row mirror ((i^15)^7 = i^8).  16 and
 // 32 use gfx950's permlane16/32 swaps (row pairs / wave halves exchanged
-// between two copies of the value) and keep the half this lane needs.
+// between two copies of the value) and keep the half this lane needs.  Every
+// DPP source lane lies inside the row, so bound_ctrl changes no value; set,
+// it lets the compiler fold the move into the ALU op that consumes it.
 __device__ __forceinline__ int xshfl(int v, int m) {
     switch (m) {
     case 1:
-        return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
+        return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true);
     case 2:
-        return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);
+        return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true);
     case 4:
-        return __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false), 0x1B, 0xF, 0xF, false);
+        return __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, true), 0x1B, 0xF, 0xF, true);
     case 8:
-        return __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, false), 0x141, 0xF, 0xF, false);
+        return __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, true), 0x141, 0xF, 0xF, true);
     case 16: {
         const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
         return lane_in(lane_bit_mask(16)) ? static_cast<int>(r[0]) : static_cast<int>(r[1]);
@@ -1110,10 +1112,10 @@ __device__ __forceinline__ bool select_smallest(float value, bool valid, int kee
         // minimum over the 32-lane half: quad (xor 1, xor 2), then the
         // half-row and row mirrors bring in the other quad and the other
         // half-row, then the neighbouring row
-        m = min(m, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(m), 0xB1, 0xF, 0xF, false)));
-        m = min(m, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(m), 0x4E, 0xF, 0xF, false)));
-        m = min(m, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(m), 0x141, 0xF, 0xF, false)));
-        m = min(m, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(m), 0x140, 0xF, 0xF, false)));
+        m = min(m, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(m), 0xB1, 0xF, 0xF, true)));
+        m = min(m, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(m), 0x4E, 0xF, 0xF, true)));
+        m = min(m, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(m), 0x141, 0xF, 0xF, true)));
+        m = min(m, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(m), 0x140, 0xF, 0xF, true)));
         m = min(m, xshfl(m, 16));
         const uint32_t cand = half_bits(ballot(remaining && key == m), h);
         const bool take = r < keep_k && cand != 0u && (lane & 31) == __builtin_ctz(cand | (cand == 0u ? 1u : 0u));
@@ -1555,13 +1557,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
                 }
 #pragma unroll
                 for (int sr = 0; sr < SR; ++sr) {
-                    // task 2 sr + h: selects between the two halves' uniform
-                    // values (a lane-dependent array index would put the
-                    // arrays in scratch memory)
-                    const uint32_t bt = h ? base_t[2 * sr + 1] : base_t[2 * sr];
-                    const uint32_t km = h ? kept_mask[2 * sr + 1] : kept_mask[2 * sr];
+                    // tasks 2 sr and 2 sr + 1 are the two halves and follow
+                    // each other in the list: a kept lane's place is the base of
+                    // task 2 sr plus its rank among the kept lanes of the wave
                     if (keepl[sr]) {
-                        const uint32_t e = bt + static_cast<uint32_t>(__popc(km & ((1u << nl) - 1u)));
+                        const uint32_t e = __builtin_amdgcn_mbcnt_hi(kept_mask[2 * sr + 1],
+                                                                     __builtin_amdgcn_mbcnt_lo(kept_mask[2 * sr], base_t[2 * sr]));
                         if (e < 32) alist[e] = cid[sr];
                     }
                 }
