@@ -280,7 +280,7 @@ __device__ __forceinline__ uint32_t half_popc(uint64_t m) {
 
 // Lane i reads lane i ^ m, all lanes active.  m < 16 stays inside a 16-lane
 // row: DPP quad_perm (1, 2), half-row mirror then quad reverse
-// ((i^7)^3 = i^4), row mirror then half-row mirror ((i^15)^7 = i^8).  16 and
+// ((i^7)^3 = i^4), row rotate by 8 (i + 8 mod 16 = i^8).  16 and
 // 32 use gfx950's permlane16/32 swaps (row pairs / wave halves exchanged
 // between two copies of the value) and keep the half this lane needs.  Every
 // DPP source lane lies inside the row, so bound_ctrl changes no value; set,
@@ -294,7 +294,7 @@ __device__ __forceinline__ int xshfl(int v, int m) {
     case 4:
         return __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, true), 0x1B, 0xF, 0xF, true);
     case 8:
-        return __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, true), 0x141, 0xF, 0xF, true);
+        return __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, true);  // row rotate by 8 = xor 8 in a 16-lane row
     case 16: {
         const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
         return lane_in(lane_bit_mask(16)) ? static_cast<int>(r[0]) : static_cast<int>(r[1]);
@@ -312,26 +312,63 @@ __device__ __forceinline__ uint32_t xshfl(uint32_t v, int m) {
     return static_cast<uint32_t>(xshfl(static_cast<int>(v), m));
 }
 
+// The two values a lane pairs with across 16-lane rows or 32-lane halves.
+// One permlane swap of (a, b) leaves in the first result a's even row and
+// b's even row interleaved as (a.R0, b.R0, a.R2, b.R2), in the second
+// (a.R1, b.R1, a.R3, b.R3) (rows of 16 lanes); the 32-lane form does the same
+// with halves.  Adding the two results is a reduce-scatter step: rows with
+// bit 16 clear get a's pair sum, the others b's.  With a == b it is the
+// xor-16 (xor-32) combine of a symmetric op, with no select: every lane sees
+// (even, odd) in the same order, which for a commutative op equals
+// (own, partner).
+struct Pair {
+    float lo, hi;
+};
+__device__ __forceinline__ Pair swap16(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return {__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+__device__ __forceinline__ Pair swap32(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return {__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+__device__ __forceinline__ uint32_t min16(uint32_t v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return min(static_cast<uint32_t>(r[0]), static_cast<uint32_t>(r[1]));
+}
+__device__ __forceinline__ int add32i(int v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(static_cast<uint32_t>(v), static_cast<uint32_t>(v), false, false);
+    return static_cast<int>(r[0]) + static_cast<int>(r[1]);
+}
+__device__ __forceinline__ int add16i(int v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(static_cast<uint32_t>(v), static_cast<uint32_t>(v), false, false);
+    return static_cast<int>(r[0]) + static_cast<int>(r[1]);
+}
+
 // Reductions over all 64 lanes (xor distances 32 .. 1, written out).
 __device__ __forceinline__ float wave_min(float v) {
-    v = fminf(v, xshfl(v, 32));
-    v = fminf(v, xshfl(v, 16));
+    Pair p = swap32(v, v);
+    v = fminf(p.lo, p.hi);
+    p = swap16(v, v);
+    v = fminf(p.lo, p.hi);
     v = fminf(v, xshfl(v, 8));
     v = fminf(v, xshfl(v, 4));
     v = fminf(v, xshfl(v, 2));
     return fminf(v, xshfl(v, 1));
 }
 __device__ __forceinline__ float wave_max(float v) {
-    v = fmaxf(v, xshfl(v, 32));
-    v = fmaxf(v, xshfl(v, 16));
+    Pair p = swap32(v, v);
+    v = fmaxf(p.lo, p.hi);
+    p = swap16(v, v);
+    v = fmaxf(p.lo, p.hi);
     v = fmaxf(v, xshfl(v, 8));
     v = fmaxf(v, xshfl(v, 4));
     v = fmaxf(v, xshfl(v, 2));
     return fmaxf(v, xshfl(v, 1));
 }
 __device__ __forceinline__ int wave_sum(int v) {
-    v += xshfl(v, 32);
-    v += xshfl(v, 16);
+    v = add32i(v);
+    v = add16i(v);
     v += xshfl(v, 8);
     v += xshfl(v, 4);
     v += xshfl(v, 2);
@@ -462,7 +499,8 @@ __device__ __forceinline__ float half_distance(const float *__restrict__ row, co
             }
         }
     }
-    val += xshfl(val, 16);
+    const Pair p16 = swap16(val, val);
+    val = p16.lo + p16.hi;
     val += xshfl(val, 8);
     val += xshfl(val, 4);
     val += xshfl(val, 2);
@@ -629,7 +667,7 @@ __device__ __forceinline__ void merge_path(const SearchParams &P, uint2 *bp, con
         }
         if (!any_lane(live)) break;
     }
-    res[0] = __shfl_up(res[SPL], 1);
+    res[0] = __builtin_amdgcn_update_dpp(0, res[SPL], 0x138, 0xF, 0xF, false);  // DPP wave_shr:1; lane 0 reads 0
     if (lane == 0) res[0] = 0;
     // Each segment's na beam entries and nb candidates (na + nb <= 4) are
     // read into 4 slots: slot s is beam entry tb + s for s < na, candidate
@@ -1020,16 +1058,16 @@ __device__ __forceinline__ void exact_pass(const SearchParams &P, const G &g, in
     constexpr int L16 = PB >= 2 ? PB / 2 : 1;
     float r16[L16];
     if constexpr (PB >= 2) {
-        const bool b = (nl & 16) != 0;
+        // rows with bit 16 clear keep child j, the others child j + L16
 #pragma unroll
         for (int j = 0; j < L16; ++j) {
-            const float send = b ? acc[j] : acc[j + L16];
-            const float own = b ? acc[j + L16] : acc[j];
-            r16[j] = own + xshfl(send, 16);
+            const Pair q = swap16(acc[j], acc[j + L16]);
+            r16[j] = q.lo + q.hi;
         }
-        c += b ? L16 : 0;
+        c += (nl & 16) ? L16 : 0;
     } else {
-        r16[0] = acc[0] + xshfl(acc[0], 16);
+        const Pair q = swap16(acc[0], acc[0]);
+        r16[0] = q.lo + q.hi;
     }
     constexpr int L8 = L16 >= 2 ? L16 / 2 : 1;
     float r8[L8];
@@ -1116,7 +1154,7 @@ __device__ __forceinline__ bool select_smallest(float value, bool valid, int kee
         m = min(m, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(m), 0x4E, 0xF, 0xF, true)));
         m = min(m, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(m), 0x141, 0xF, 0xF, true)));
         m = min(m, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(m), 0x140, 0xF, 0xF, true)));
-        m = min(m, xshfl(m, 16));
+        m = min16(m);
         const uint32_t cand = half_bits(ballot(remaining && key == m), h);
         const bool take = r < keep_k && cand != 0u && (lane & 31) == __builtin_ctz(cand | (cand == 0u ? 1u : 0u));
         kept |= take;
@@ -1684,7 +1722,7 @@ __global__ __launch_bounds__(64) void fg_score_kernel(ScoreParams S) {
     // words (theta > 1 layout): the integer sums must agree.
     const int hw = W >> 1;
     const int32_t part = raw_partial(code, h * hw, (h + 1) * hw, planes, W);
-    const int32_t raw_split = part + __shfl_xor(part, 32);
+    const int32_t raw_split = add32i(part);
     const int32_t raw_full = raw_partial(code, 0, W, planes, W);
     const float el = tx == FLT_MAX ? 0.0f : estimate_formula(raw_split, sq, w, lo, tx, fdq, fvq, pd);
     const float es = tx == FLT_MAX ? FLT_MAX : estimate_formula(raw_full, sq, w, lo, tx, fdq, fvq, pd);
