@@ -1610,18 +1610,23 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
                 const bool mine = lane < static_cast<int>(total);
                 const uint32_t key = mine ? alist[lane] : kMaxIndex;
                 const uint32_t got = mine ? hash_insert(H, nbk, key) : 0u;
+                // Every listed child was absent from the table when this
+                // round's visited tests ran, so an insert that finds its key
+                // present met a repeat within the list, added by another lane
+                // of this batch: of each such group the earliest lane is kept.
                 bool acc = got != 0u;
-                if (any_lane(mine && !got)) {
-                    const uint32_t members = half_bits(ballot(mine), 0);
-                    acc = mine && !dup_of_earlier(key, members, nl, 0);
+                uint64_t lost = ballot(mine && !got);
+                while (lost != 0ull) {
+                    const uint32_t kr = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(key), __builtin_ctzll(lost)));
+                    const uint64_t same = ballot(mine && key == kr);
+                    acc = lane_in(same) ? (lane == __builtin_ctzll(same)) : acc;
+                    lost &= ~same;
                 }
                 const uint32_t accm = half_bits(ballot(acc), 0);
                 if (acc) {
-                    const uint32_t slot = compact + static_cast<uint32_t>(__popc(accm & ((1u << lane) - 1u)));
-                    if (slot < static_cast<uint32_t>(P.collect_cap)) {
-                        ci[slot] = key;
-                        cd[slot] = FLT_MAX;
-                    }
+                    // (cd was reset at the iteration's start; the exact pass fills it)
+                    const uint32_t slot = __builtin_amdgcn_mbcnt_lo(accm, compact);
+                    if (slot < static_cast<uint32_t>(P.collect_cap)) ci[slot] = key;
                 }
                 compact += static_cast<uint32_t>(__popc(accm));
                 __syncthreads();
