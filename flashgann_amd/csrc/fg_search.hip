@@ -1135,18 +1135,16 @@ __device__ __forceinline__ void exact_batch(const SearchParams &P, const G &g, i
 
 // The keep_k smallest valid (value, lane) pairs of each 32-lane half, as
 // warp_keep_topk_smallest_f32 (utils.cuh:251-267) selects them, found by
-// keep_k rounds of half-wave argmin instead of a 32-step rank count.
-__device__ __forceinline__ bool select_smallest(float value, bool valid, int keep_k, int max_k) {
-    const int lane = lane_id();
-    const int h = lane >> 5, nl = lane & 31;
+// keep_k rounds of half-wave argmin instead of a 32-step rank count.  keep_k
+// is uniform within each half; valid lanes and the result are lane masks.
+__device__ __forceinline__ uint64_t select_smallest(float value, uint64_t valid, int keep_k, int max_k) {
     // order-preserving unsigned image of the float; -0 joins +0 so equal
     // values tie exactly as in the float comparison
     const uint32_t bits = __float_as_uint(value == 0.0f ? 0.0f : value);
     const uint32_t key = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
-    bool remaining = valid;
-    bool kept = false;
+    uint64_t remaining = valid, kept = 0ull;
     for (int r = 0; r < max_k; ++r) {
-        uint32_t m = remaining ? key : 0xFFFFFFFFu;
+        uint32_t m = lane_in(remaining) ? key : 0xFFFFFFFFu;
         // minimum over the 32-lane half: quad (xor 1, xor 2), then the
         // half-row and row mirrors bring in the other quad and the other
         // half-row, then the neighbouring row
@@ -1155,10 +1153,14 @@ __device__ __forceinline__ bool select_smallest(float value, bool valid, int kee
         m = min(m, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(m), 0x141, 0xF, 0xF, true)));
         m = min(m, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(m), 0x140, 0xF, 0xF, true)));
         m = min16(m);
-        const uint32_t cand = half_bits(ballot(remaining && key == m), h);
-        const bool take = r < keep_k && cand != 0u && (lane & 31) == __builtin_ctz(cand | (cand == 0u ? 1u : 0u));
+        // the lowest lane of each half holding its half's minimum (x & -x on
+        // each 32-bit half of the mask), taken while the half keeps more
+        const uint64_t cand = ballot(key == m) & remaining;
+        const uint32_t c0 = static_cast<uint32_t>(cand), c1 = static_cast<uint32_t>(cand >> 32);
+        const uint64_t first = (static_cast<uint64_t>(c1 & (0u - c1)) << 32) | (c0 & (0u - c0));
+        const uint64_t take = first & ballot(r < keep_k);
         kept |= take;
-        remaining &= !take;
+        remaining &= ~take;
     }
     return kept;
 }
@@ -1527,82 +1529,85 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
 #pragma unroll
                 for (int sr = 0; sr < SR; ++sr) val[sr] = cid[sr] != kMaxIndex && cid[sr] < P.npoints;
                 hash_contains_n<SR>(H, nbk, cid, val);
-                // (c) which tasks need estimates; their codes and factors, loads issued together
-                bool need[SR];
+                // (c) which tasks need estimates.  Lane predicates from here on
+                // are masks taken straight from compares.  A task without
+                // children has no valid lane, so it never needs estimates and
+                // its keep limit is never read.
+                uint64_t valm[SR], needm[SR];
                 int keep[SR];
 #pragma unroll
                 for (int sr = 0; sr < SR; ++sr) {
-                    const int rvc = static_cast<int>(half_popc(ballot(val[sr])));
-                    const int lim = an[sr] == an_full ? lim_full : lim_last;
-                    keep[sr] = tsk[sr] >= 0 ? lim : 0;
-                    need[sr] = !(keep[sr] >= rvc);
-                    FG_COUNT(c_est += static_cast<uint32_t>(__popcll(ballot(need[sr] && val[sr]))));
+                    valm[sr] = ballot(val[sr]);
+                    const int rvc = static_cast<int>(half_popc(valm[sr]));
+                    keep[sr] = an[sr] == an_full ? lim_full : lim_last;
+                    needm[sr] = ballot(keep[sr] < rvc);
+                    FG_COUNT(c_est += static_cast<uint32_t>(__popcll(needm[sr] & valm[sr])));
                 }
                 FG_PHASE(6);
                 // (d) estimates, kth-near counts, keep decisions
-                uint32_t kept_mask[kSearchWidth];
-                bool keepl[SR];
+                uint64_t klm[SR];
                 int32_t rawb[SR];
                 if constexpr (WT > 0) raw_batch<SR, WT>(code, planes, any_wrap, rawb);
 #pragma unroll
                 for (int sr = 0; sr < SR; ++sr) {
                     float est = FLT_MAX;
-                    const bool scored = need[sr] && val[sr];
+                    const uint64_t scored = needm[sr] & valm[sr];
                     if constexpr (WT > 0) {
                         // computed on every lane and selected (most lanes need it;
                         // a branch would cost more than the few wasted lanes)
                         const float e = estimate_formula(rawb[sr], sum_q, qwidth, qlow, tx[sr], fdq[sr], fvq[sr],
                                                          pdist[pix[sr]]);
-                        est = (scored && tx[sr] != FLT_MAX) ? e : FLT_MAX;
-                    } else if (scored && tx[sr] != FLT_MAX) {
+                        est = (lane_in(scored) && tx[sr] != FLT_MAX) ? e : FLT_MAX;
+                    } else if (lane_in(scored) && tx[sr] != FLT_MAX) {
                         const int nidx = tsk[sr] + nl;
                         const int32_t raw = raw_partial(reinterpret_cast<const uint32_t *>(prw[sr] + g.code) +
                                                             static_cast<uint64_t>(nidx) * W,
                                                         0, W, planes, W);
                         est = estimate_formula(raw, sum_q, qwidth, qlow, tx[sr], fdq[sr], fvq[sr], pdist[pix[sr]]);
                     }
-                    val[sr] = scored ? isfinite(est) : val[sr];
-                    bool kl = val[sr];
-                    const bool any_need = any_lane(need[sr]);
-                    if (any_need) {
-                        const bool below = val[sr] && kth_valid && est <= kth;
-                        const uint32_t near = half_popc(ballot(below));
-                        int eff = keep[sr];
-                        if (need[sr]) eff = keep_with_cutoff(keep[sr], kth_valid, near);
+                    // a scored child with a non-finite estimate is dropped
+                    // (finiteness as an integer compare on opaque bits, which
+                    // the ballot takes as it is; a float class test would pass
+                    // through a vector register on its way to the mask)
+                    uint32_t eb = __float_as_uint(est);
+                    asm volatile("" : "+v"(eb));
+                    const uint64_t finm = ballot((eb & 0x7F800000u) != 0x7F800000u);
+                    valm[sr] = (valm[sr] & ~scored) | (scored & finm);
+                    uint64_t kl = valm[sr];
+                    if (needm[sr] != 0ull) {
+                        const uint64_t belowm = kth_valid ? (valm[sr] & ballot(est <= kth)) : 0ull;
+                        const uint32_t near = half_popc(belowm);
+                        const int kp = keep[sr];
+                        const bool nd = lane_in(needm[sr]);
+                        const int eff = nd ? keep_with_cutoff(kp, kth_valid, near) : kp;
                         // With a valid cutoff and 1 <= near <= keep the count is
                         // near, and the near smallest (value, lane) pairs are the
                         // ones at or below the cutoff: every such lane ranks
                         // ahead of every lane above it.  No selection rounds.
-                        const bool by_cut = need[sr] && kth_valid && near >= 1u && static_cast<int>(near) <= keep[sr];
-                        const int rounds = (need[sr] && !by_cut) ? eff : 0;
+                        const uint64_t cutm =
+                            kth_valid ? (needm[sr] & ballot(near >= 1u) & ballot(static_cast<int>(near) <= kp)) : 0ull;
+                        const int rounds = (nd && !lane_in(cutm)) ? eff : 0;
                         // uniform within each half: the larger of lanes 0 and 32
                         const int maxk = max(__builtin_amdgcn_readlane(rounds, 0), __builtin_amdgcn_readlane(rounds, 32));
-                        const bool sel = select_smallest(est, val[sr], eff, maxk);
-                        if (need[sr]) kl = val[sr] && eff > 0 && (by_cut ? below : sel);
+                        const uint64_t selm = select_smallest(est, valm[sr], eff, maxk);
+                        const uint64_t effm = ballot(eff > 0);
+                        kl = (valm[sr] & ~needm[sr]) | (needm[sr] & valm[sr] & effm & ((cutm & belowm) | (selm & ~cutm)));
                     }
-                    keepl[sr] = kl;
-                    const uint64_t km = ballot(kl);
-                    kept_mask[2 * sr] = uni(half_bits(km, 0));
-                    kept_mask[2 * sr + 1] = uni(half_bits(km, 1));
+                    klm[sr] = kl;
                 }
                 // (e) kept children listed in (task, lane) order
-                uint32_t base_t[kSearchWidth];
                 uint32_t total = 0;
-#pragma unroll
-                for (int t = 0; t < kSearchWidth; ++t) {
-                    base_t[t] = total;
-                    total += static_cast<uint32_t>(__popc(kept_mask[t]));
-                }
 #pragma unroll
                 for (int sr = 0; sr < SR; ++sr) {
                     // tasks 2 sr and 2 sr + 1 are the two halves and follow
-                    // each other in the list: a kept lane's place is the base of
-                    // task 2 sr plus its rank among the kept lanes of the wave
-                    if (keepl[sr]) {
-                        const uint32_t e = __builtin_amdgcn_mbcnt_hi(kept_mask[2 * sr + 1],
-                                                                     __builtin_amdgcn_mbcnt_lo(kept_mask[2 * sr], base_t[2 * sr]));
+                    // each other in the list: a kept lane's place is the running
+                    // total plus its rank among the kept lanes of the wave
+                    if (lane_in(klm[sr])) {
+                        const uint32_t e = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(klm[sr] >> 32),
+                                                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(klm[sr]), total));
                         if (e < 32) alist[e] = cid[sr];
                     }
+                    total += static_cast<uint32_t>(__popcll(klm[sr]));
                 }
                 __syncthreads();
                 if (total > 32) total = 32;  // <= 4 kept per task at theta = 8
