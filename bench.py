@@ -31,6 +31,21 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 
+# BASELINE.json configurations (generator, shape, default K, beams).  C2 is
+# the headline; the others run with --config for coverage measurements.
+CONFIGS = {
+    "c1": dict(n=100_000, nq=1000, dim=128, components=64, degree=32, K=10, beams="64",
+               gen="integer_mixture", cfg=1),
+    "c2": dict(n=1_000_000, nq=10_000, dim=128, components=1024, degree=32, K=100,
+               beams="100,128,256,384,512,640,768,896,1024", gen="integer_mixture", cfg=2),
+    "c3": dict(n=1_000_000, nq=10_000, dim=96, components=1024, degree=32, K=100,
+               beams="16,32,64,96,128,256,384,512", gen="normalized_mixture", cfg=3),
+    "c4": dict(n=1_000_000, nq=1000, dim=960, components=256, degree=32, K=100,
+               beams="128,256,384,512,640,768,896,1024", gen="unit_box_mixture", cfg=4),
+    "c5": dict(n=10_000_000, nq=10_000, dim=1536, components=4096, degree=32, K=100,
+               beams="128,256,384,512,640,768,896,1024", gen="anisotropic_unit_mixture", cfg=5),
+}
+
 
 def log(msg: str) -> None:
     print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
@@ -41,21 +56,31 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--n", type=int, default=1_000_000, help="base points (C2: 1M)")
-    ap.add_argument("--nq", type=int, default=10_000)
-    ap.add_argument("--components", type=int, default=1024)
-    ap.add_argument("--degree", type=int, default=32)
-    ap.add_argument("--K", type=int, default=100)
-    ap.add_argument("--beams", type=str, default="100,128,256,384,512,640,768,896,1024")
+    ap.add_argument("--config", type=str, default="c2", choices=sorted(CONFIGS),
+                    help="BASELINE configuration (c2 = the headline; the others for coverage)")
+    ap.add_argument("--n", type=int, default=0, help="base points (default: the configuration's)")
+    ap.add_argument("--nq", type=int, default=0)
+    ap.add_argument("--components", type=int, default=0)
+    ap.add_argument("--degree", type=int, default=0)
+    ap.add_argument("--K", type=int, default=0)
+    ap.add_argument("--beams", type=str, default="")
     ap.add_argument("--target-recall", type=float, default=0.95)
     ap.add_argument("--beam", type=int, default=0, help="skip the sweep and use this beam")
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="CPU-oracle work budget")
-    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle (baseline and id checks)")
+    ap.add_argument("--full-sweep", action="store_true",
+                    help="time every beam of --beams instead of stopping at the first that reaches the target")
+    ap.add_argument("--parity-sample", type=int, default=500,
+                    help="queries per swept beam whose GPU ids are compared with the CPU oracle's")
     ap.add_argument("--traffic", type=str, default=os.path.join(ROOT, "profiles", "search_c2_traffic.json"))
     ap.add_argument("--cache", type=str, default="", help="directory to reuse the built index and ground truth")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run one plain 1 GiB device copy (counter calibration for profiling)")
     args = ap.parse_args()
+    conf = CONFIGS[args.config]
+    for key in ("n", "nq", "components", "degree", "K", "beams"):
+        if not getattr(args, key):
+            setattr(args, key, conf[key])
 
     if args.gpus != 1:
         print(f"bench.py: this search runs on one GPU only (queries are independent; a multi-GPU "
@@ -75,16 +100,16 @@ def main() -> int:
         return 2
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    dim = 128
+    dim = conf["dim"]
     B = padded_dim_for(dim)
 
     from flashgann_amd.codebook import read_codebook
 
     t0 = time.time()
-    base, queries = datasets.integer_mixture(args.n, args.nq, dim, args.components, config=2)
-    signs = datasets.signs_for(B, 2)
+    base, queries = getattr(datasets, conf["gen"])(args.n, args.nq, dim, args.components, config=conf["cfg"])
+    signs = datasets.signs_for(B, conf["cfg"])
     log(f"data {args.n}x{dim} + {args.nq} queries in {time.time() - t0:.1f}s")
-    tag = f"c2_{args.n}_{args.nq}_{args.components}_{args.degree}_{args.K}"
+    tag = f"{args.config}_{args.n}_{args.nq}_{args.components}_{args.degree}_{args.K}"
     cb_path = os.path.join(args.cache, tag + ".index") if args.cache else ""
     gt_path = os.path.join(args.cache, tag + ".gt.npy") if args.cache else ""
     if cb_path and os.path.exists(cb_path) and os.path.exists(gt_path):
@@ -128,25 +153,51 @@ def main() -> int:
             hit += np.isin(ids[i], gt[i, : args.K]).sum()
         return hit / float(ids.size)
 
+    # Oracle handle for the per-beam id checks (bounded samples) and the CPU
+    # baseline; built once.
+    oix = None
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    threads = max(1, min(threads or 1, 16))
+    if not args.no_cpu:
+        from oracle import oracle as O
+        oix = O.OracleIndex.from_codebook(cb)
+
+    # Beam sweep (the reference README's QPS-recall list): per beam one
+    # counting launch, then timed launches (HIP events), recall@K against the
+    # ground truth, and the GPU ids compared with the CPU oracle's on the first
+    # `--parity-sample` queries.
     sweep = []
     beams = [args.beam] if args.beam else [int(b) for b in args.beams.split(",")]
     chosen = None
     for beam in beams:
         launch(beam, counters=True)
         torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        launch(beam)
-        e1.record(stream)
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1)
+        ms = []
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            launch(beam)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            ms.append(e0.elapsed_time(e1))
+        kms = min(ms)
         ids = dres.cpu().numpy().view(np.uint32)
         r = recall_of(ids)
-        sweep.append({"beam": beam, "recall": round(float(r), 5), "qps": round(args.nq / (ms / 1e3), 1)})
-        log(f"beam {beam}: recall@{args.K} {r:.4f}, {args.nq / (ms / 1e3):.0f} QPS ({ms:.2f} ms)")
+        row = {"beam": beam, "recall": round(float(r), 5), "qps": round(args.nq / (kms / 1e3), 1),
+               "kernel_ms": round(kms, 4)}
+        if oix is not None and args.parity_sample > 0:
+            m = min(args.nq, args.parity_sample)
+            pids, _ = oix.search(queries[:m], args.K, beam, threads=threads)
+            row["oracle_ids_identical"] = float((pids == ids[:m]).all(1).mean())
+            row["oracle_sample"] = m
+        sweep.append(row)
+        log(f"beam {beam}: recall@{args.K} {r:.4f}, {row['qps']:.0f} QPS ({kms:.3f} ms)"
+            + (f", ids identical to the oracle on {row['oracle_ids_identical'] * 100:.2f}% of {row['oracle_sample']}"
+               if "oracle_sample" in row else ""))
         if chosen is None and r >= args.target_recall:
             chosen = beam
-            break
+            if not args.full_sweep:
+                break
     if chosen is None:
         chosen = beams[-1]
         log(f"no beam reached recall {args.target_recall}; reporting beam {chosen}")
@@ -193,17 +244,14 @@ def main() -> int:
     if os.path.exists(args.traffic):
         try:
             t = json.load(open(args.traffic))
-            if t.get("n") == args.n and t.get("nq") == args.nq and t.get("beam") == chosen:
+            if (t.get("config", "c2") == args.config and t.get("n") == args.n and t.get("nq") == args.nq
+                    and t.get("beam") == chosen):
                 traffic = t.get("hbm_bytes_per_launch")
         except Exception:
             traffic = None
 
     cpu = None
-    if not args.no_cpu:
-        from oracle import oracle as O
-        threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-        threads = max(1, min(threads or 1, 16))
-        oix = O.OracleIndex.from_codebook(cb)
+    if oix is not None:
         probe = min(args.nq, max(threads * 4, 64))
         t1 = time.perf_counter()
         pids, _ = oix.search(queries[:probe], args.K, chosen, threads=threads)
@@ -226,7 +274,8 @@ def main() -> int:
             f"of the sample")
 
     line = {
-        "metric": "queries/sec at recall@100>=0.95 (1M x 128 fp32, deg 32)",
+        "metric": ("queries/sec at recall@100>=0.95 (1M x 128 fp32, deg 32)" if args.config == "c2" else
+                   f"queries/sec at recall@{args.K}>={args.target_recall} ({args.n} x {dim} fp32, deg {args.degree})"),
         "value": round(qps, 1),
         "unit": "queries/s",
         "n_gpus": 1,
@@ -237,8 +286,10 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic: seeded integer Gaussian mixture (1024 components), graph and codes built in-run",
-        "config": {"workload": f"C2 {args.n}x{dim} deg {args.degree}, K={args.K}, nq={args.nq}, beam={chosen}",
+        "data": f"synthetic: seeded {conf['gen'].replace('_', ' ')} ({args.components} components), "
+                "graph and codes built in-run",
+        "config": {"workload": f"{args.config.upper()} {args.n}x{dim} deg {args.degree}, K={args.K}, nq={args.nq}, "
+                               f"beam={chosen}",
                    "beam": chosen, "recall": round(float(recall), 5), "beam_sweep": sweep,
                    "host_buffers_qps": round(host_qps, 1),
                    "lds_bytes": fg.lds_bytes(dim, chosen, args.degree)},

@@ -192,8 +192,15 @@ def build_graph(x: torch.Tensor, degree: int, random_links: int | None = None,
     # sort each list by (distance, id)
     big = torch.iinfo(torch.int64).max
     valid = merged >= 0
-    mv = x[merged.clamp(min=0)]
-    dist = _sqnorm(mv - x[:, None, :]).to(torch.float64)
+    # distances to the kept neighbours, in row blocks of at most 2^32 gathered
+    # elements (the unblocked gather of 1M x 32 x 960 floats alone is 123 GB)
+    step = max(1, (1 << 32) // max(1, degree * x.shape[1]))
+    dist = torch.empty(merged.shape, dtype=torch.float64, device=dev)
+    for s in range(0, n, step):
+        e = min(n, s + step)
+        mv = x[merged[s:e].clamp(min=0)]
+        dist[s:e] = _sqnorm(mv - x[s:e, None, :]).to(torch.float64)
+        del mv
     dist = torch.where(valid, dist, torch.full_like(dist, float("inf")))
     o = torch.argsort(torch.where(valid, merged, torch.full_like(merged, big)), dim=1)
     merged = torch.gather(merged, 1, o)

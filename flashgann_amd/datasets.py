@@ -10,6 +10,9 @@ version), seeded as 0xF1A50000 + 16*config + stream with streams
   C3  N x 96 unit vectors: 1024 components, means ~ N(0,1), x = mu + 0.3 z,
       normalised; queries = base point + N(0, 0.05), renormalised.
   C4  N x 960 in [0,1]: 256 components, means ~ U[0,1], x = clip(mu+0.1 z).
+  C5  N x 1536 unit vectors: 4096 anisotropic components, means ~ N(0,1),
+      per-component per-dimension scales s = 0.05 + 0.45 u (u ~ U[0,1]),
+      x = mu + s * z, normalised; queries from the same mixture.
 """
 from __future__ import annotations
 
@@ -64,6 +67,28 @@ def unit_box_mixture(n: int, nq: int, dim: int = 960, components: int = 256, con
         comp = r.integers(0, components, size=count)
         z = r.standard_normal(size=(count, dim), dtype=np.float32)
         return np.clip(means[comp] + 0.1 * z, 0.0, 1.0).astype(np.float32)
+
+    return draw(n, 1), draw(nq, 2)
+
+
+def anisotropic_unit_mixture(n: int, nq: int, dim: int = 1536, components: int = 4096, config: int = 5):
+    """C5 generator: unit-normalised anisotropic mixture (each component has
+    its own per-dimension spread), queries drawn from the same mixture."""
+    r0 = _rng(config, 0)
+    means = r0.standard_normal(size=(components, dim)).astype(np.float32)
+    scales = (0.05 + 0.45 * r0.uniform(0.0, 1.0, size=(components, dim))).astype(np.float32)
+
+    def draw(count: int, stream: int) -> np.ndarray:
+        r = _rng(config, stream)
+        comp = r.integers(0, components, size=count)
+        out = np.empty((count, dim), dtype=np.float32)
+        step = 1 << 14
+        for s in range(0, count, step):
+            e = min(count, s + step)
+            z = r.standard_normal(size=(e - s, dim), dtype=np.float32)
+            x = means[comp[s:e]] + scales[comp[s:e]] * z
+            out[s:e] = x / np.linalg.norm(x, axis=1, keepdims=True)
+        return out
 
     return draw(n, 1), draw(nq, 2)
 

@@ -29,6 +29,8 @@ def small_index(n=3000, nq=24, dim=128, comps=16, degree=32, kind="int", use_ip=
         base, q = datasets.normalized_mixture(n, nq, dim, comps, config=3)
     elif kind == "box":
         base, q = datasets.unit_box_mixture(n, nq, dim, comps, config=4)
+    elif kind == "aniso":
+        base, q = datasets.anisotropic_unit_mixture(n, nq, dim, comps, config=5)
     else:
         raise ValueError(kind)
     signs = datasets.signs_for(padded_dim_for(dim), config)

@@ -62,6 +62,32 @@ def test_search_dim960(gpu_available):
     _assert_equal(ids, cnt, rids, rcnt, "box960")
 
 
+def test_search_dim1536(gpu_available):
+    """C5's row shape: 1536-d unit vectors, rotation padded to 2048 (the
+    largest padded dimension the kernel takes)."""
+    cb, q, _ = small_index(n=1200, nq=8, dim=1536, comps=8, kind="aniso")
+    ids, cnt, rids, rcnt = _run(cb, q, 100, 128)
+    _assert_equal(ids, cnt, rids, rcnt, "aniso1536")
+    ids, cnt, rids, rcnt = _run(cb, q, 10, 32)
+    _assert_equal(ids, cnt, rids, rcnt, "aniso1536 beam 32")
+
+
+def test_empty_batch(gpu_available):
+    """nq = 0 is a no-op through both entry points (no launch, outputs untouched)."""
+    import torch
+    from flashgann_amd import Index
+    cb, q, _ = small_index()
+    ix = Index.from_codebook(cb)
+    ids, st, cnt = ix.search(q[:0], 10, 64, counters=True)
+    assert ids.shape == (0, 10) and cnt.shape == (0, 6)
+    res = torch.full((4, 10), 7, dtype=torch.int32, device="cuda")
+    dq = torch.as_tensor(q[:4], device="cuda")
+    ix.search_device(dq.data_ptr(), 0, 10, 64, res.data_ptr())
+    torch.cuda.synchronize()
+    assert (res.cpu() == 7).all()
+    ix.close()
+
+
 def test_search_entry_auto(gpu_available):
     from flashgann_amd import Index
     from oracle import oracle as O

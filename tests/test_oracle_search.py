@@ -21,6 +21,18 @@ def test_recall_against_brute_force():
     assert compute_recall(out10, gt[:, :10], 10) >= 0.95
 
 
+def test_recall_dim1536_against_brute_force():
+    """C5's shape (1536-d unit vectors, padded dimension 2048) end to end on
+    the oracle: recall@10 against exact search."""
+    from flashgann_amd import builder
+    from flashgann_amd.metrics import compute_recall
+    cb, q, base = small_index(n=1200, nq=8, dim=1536, comps=8, kind="aniso")
+    assert cb.layout.padded_dim == 2048 and cb.layout.row_offset == 3712
+    gt = builder.ground_truth(base, q, 10)
+    out, _ = O.OracleIndex.from_codebook(cb).search(q, 10, 64)
+    assert compute_recall(out, gt, 10) >= 0.95
+
+
 def test_invariants_and_counters():
     cb, q, _ = small_index()
     ix = O.OracleIndex.from_codebook(cb)
