@@ -473,6 +473,59 @@ __device__ __forceinline__ int32_t raw_partial(const uint32_t *__restrict__ code
     return static_cast<int32_t>(raw - 256u * wraps);
 }
 
+// raw for one neighbour code of W words (W a power of two >= 8: padded
+// dimension >= 256), the same sum as raw_partial over [0, W): the code words
+// are loaded 16 at a time (four 16-byte loads when the row layout keeps codes
+// 16-byte aligned), issued together, and each plane's matching words come
+// from LDS as 16-byte reads.
+__device__ __forceinline__ int32_t raw_words(const uint32_t *__restrict__ code, const uint32_t *planes, int W,
+                                             bool vec_ok, bool any_wrap) {
+    uint32_t acc[kPlanes];
+#pragma unroll
+    for (int p = 0; p < kPlanes; ++p) acc[p] = 0;
+    uint32_t wraps = 0;
+    const int nb = W < 16 ? W : 16;  // words per batch: 8 or 16
+    for (int w0 = 0; w0 < W; w0 += nb) {
+        uint32_t c[16];
+        if (vec_ok) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint4 v = j * 4 < nb ? reinterpret_cast<const uint4 *>(code + w0)[j] : make_uint4(0u, 0u, 0u, 0u);
+                c[4 * j] = v.x; c[4 * j + 1] = v.y; c[4 * j + 2] = v.z; c[4 * j + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) c[j] = j < nb ? code[w0 + j] : 0u;
+        }
+#pragma unroll
+        for (int p = 0; p < kPlanes; ++p) {
+            const uint4 *pl = reinterpret_cast<const uint4 *>(planes + p * W + w0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (j * 4 < nb) {
+                    const uint4 q = pl[j];
+                    acc[p] += __popc(c[4 * j] & q.x) + __popc(c[4 * j + 1] & q.y) + __popc(c[4 * j + 2] & q.z) +
+                              __popc(c[4 * j + 3] & q.w);
+                }
+            }
+        }
+        if (any_wrap) {
+            const uint32_t *wp = planes + kPlanes * W + w0;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                if (j < nb) {
+                    const uint32_t x = c[j] & wp[j];
+                    wraps += __popc(x & (x >> 1) & (x >> 2) & (x >> 3) & 0x11111111u);
+                }
+            }
+        }
+    }
+    uint32_t raw = 0;
+#pragma unroll
+    for (int p = 0; p < kPlanes; ++p) raw += acc[p] << p;
+    return static_cast<int32_t>(raw - 256u * wraps);
+}
+
 // utils.cuh:989-993 with nvcc's contraction of the two multiply-adds.
 __device__ __forceinline__ float estimate_formula(int32_t raw, int32_t sum_q, float width, float low,
                                                   float tx, float fdq, float fvq, float pdist) {
@@ -506,6 +559,79 @@ __device__ __forceinline__ float half_distance(const float *__restrict__ row, co
     val += xshfl(val, 2);
     val += xshfl(val, 1);
     return use_ip ? -val : val;
+}
+
+// The reduction of half_distance on its own: every lane of the half gets
+// the shfl_down tree's sum of the half's 32 partial sums.
+__device__ __forceinline__ float half_reduce(float val) {
+    const Pair p16 = swap16(val, val);
+    val = p16.lo + p16.hi;
+    val += xshfl(val, 8);
+    val += xshfl(val, 4);
+    val += xshfl(val, 2);
+    val += xshfl(val, 1);
+    return val;
+}
+
+// Exact distances of the generic geometry, PB children per 32-lane half
+// (child e0 + 2 j + h): lane nl accumulates dimensions nl, nl + 32, ... of
+// each child in that order (the reference's per-lane order, as
+// half_distance), with the loads of KB consecutive steps of every child
+// issued together.  Indices past the row's dimension are clamped to its last
+// dimension and their terms skipped.
+template <int PB, int KB>
+__device__ __forceinline__ void exact_generic_pass(const SearchParams &P, uint64_t row_floats, int dim, int e0, int n,
+                                                   const uint32_t *slot_list, float *cd, const uint32_t *ci,
+                                                   const float *qv, bool ip) {
+    const int lane = lane_id();
+    const int h = lane >> 5, nl = lane & 31;
+    const float *rows[PB];
+#pragma unroll
+    for (int j = 0; j < PB; ++j) {
+        const int e = e0 + 2 * j + h;
+        const int slot = e < n ? static_cast<int>(slot_list ? slot_list[e] : static_cast<uint32_t>(e)) : 0;
+        const uint32_t child = e < n ? ci[slot] : 0u;
+        rows[j] = P.data + static_cast<uint64_t>(child) * row_floats;
+    }
+    float acc[PB];
+#pragma unroll
+    for (int j = 0; j < PB; ++j) acc[j] = 0.0f;
+    const int steps = (dim + 31) >> 5;
+    for (int k0 = 0; k0 < steps; k0 += KB) {
+        float q[KB], v[PB][KB];
+        bool ok[KB];
+#pragma unroll
+        for (int kk = 0; kk < KB; ++kk) {
+            const int i = nl + 32 * (k0 + kk);
+            ok[kk] = i < dim;
+            const int is = ok[kk] ? i : dim - 1;
+            q[kk] = qv[is];
+#pragma unroll
+            for (int j = 0; j < PB; ++j) v[j][kk] = rows[j][is];
+        }
+#pragma unroll
+        for (int kk = 0; kk < KB; ++kk)
+#pragma unroll
+            for (int j = 0; j < PB; ++j) {
+                float t;
+                if (ip) {
+                    t = fmaf(q[kk], v[j][kk], acc[j]);
+                } else {
+                    const float d = q[kk] - v[j][kk];
+                    t = fmaf(d, d, acc[j]);
+                }
+                acc[j] = ok[kk] ? t : acc[j];
+            }
+    }
+#pragma unroll
+    for (int j = 0; j < PB; ++j) {
+        const float r = half_reduce(acc[j]);
+        const int e = e0 + 2 * j + h;
+        if (e < n && nl == 0) {
+            const int slot = static_cast<int>(slot_list ? slot_list[e] : static_cast<uint32_t>(e));
+            cd[slot] = ip ? -r : r;
+        }
+    }
 }
 
 // ------------------------------------------------------------ sorting networks
@@ -1107,7 +1233,7 @@ __device__ __forceinline__ void exact_pass(const SearchParams &P, const G &g, in
 // Exact distances for n children held in cd/ci at slots slot_list[0..n)
 // (or 0..n when slot_list is null): passes of 16 children, the last one
 // sized to what is left (DPL > 0: dims per lane known at compile time;
-// DPL == 0: generic loop, two children per pass).
+// DPL == 0: generic geometry, exact_generic_pass).
 template <int DPL, class G>
 __device__ __forceinline__ void exact_batch(const SearchParams &P, const G &g, int n, const uint32_t *slot_list, float *cd,
                             const uint32_t *ci, const float (&qr)[DPL > 0 ? DPL : 1], const float *qv) {
@@ -1122,14 +1248,10 @@ __device__ __forceinline__ void exact_batch(const SearchParams &P, const G &g, i
         else if (rem > 2) exact_pass<2, DPL>(P, g, e0, n, slot_list, cd, ci, qr, ip);
         else if (rem > 0) exact_pass<1, DPL>(P, g, e0, n, slot_list, cd, ci, qr, ip);
     } else {
-        for (int e0 = 0; e0 < n; e0 += 2) {
-            const int e = e0 + h;
-            const bool act = e < n;
-            const int slot = act ? static_cast<int>(slot_list ? slot_list[e] : static_cast<uint32_t>(e)) : 0;
-            const uint32_t child = act ? ci[slot] : 0u;
-            const float d = half_distance(P.data + static_cast<uint64_t>(child) * g.row, qv, g.dim, nl, ip, act);
-            if (act && nl == 0) cd[slot] = d;
-        }
+        // four children per pass (two per half), 8 dimension steps per load batch
+        int e0 = 0;
+        for (; n - e0 > 2; e0 += 4) exact_generic_pass<2, 8>(P, g.row, g.dim, e0, n, slot_list, cd, ci, qv, ip);
+        if (e0 < n) exact_generic_pass<1, 8>(P, g.row, g.dim, e0, n, slot_list, cd, ci, qv, ip);
     }
 }
 
@@ -1267,12 +1389,18 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
     prepare_query(P.queries + static_cast<uint64_t>(qid) * g.dim, P.signs, g.dim, B, reinterpret_cast<float *>(H),
                   qv, planes, qlow, qhigh, qwidth, sum_q, nullptr);
     constexpr int WTR = WT > 0 ? WT : 1;
+    // whether any chunk of the quantized query wraps the reference's uint8
+    // LUT entry (then the estimates subtract the wrapped chunks)
     bool any_wrap = false;
     if constexpr (WT > 0) {
         uint32_t wor = 0;
 #pragma unroll
         for (int w = 0; w < WT; ++w) wor |= planes[kPlanes * WT + w];
         any_wrap = uni(wor) != 0u;
+    } else {
+        uint32_t wor = 0;
+        for (int w = lane; w < W; w += 64) wor |= planes[kPlanes * W + w];
+        any_wrap = any_lane(wor != 0u);
     }
     constexpr int DPLR = DPL > 0 ? DPL : 1;
     float qr[DPLR];
@@ -1418,7 +1546,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
                     raw_batch<1, WT>(c1, planes, any_wrap, r1);
                     est = tx == FLT_MAX ? 0.0f : estimate_formula(r1[0], sum_q, qwidth, qlow, tx, fdq, fvq, pd0);
                 } else if (valid) {
-                    const int32_t raw = raw_partial(codes + static_cast<uint64_t>(nl) * W, 0, W, planes, W);
+                    const int32_t raw = raw_words(codes + static_cast<uint64_t>(nsafe) * W, planes, W, vec_ok, any_wrap);
                     est = tx == FLT_MAX ? 0.0f : estimate_formula(raw, sum_q, qwidth, qlow, tx, fdq, fvq, pd0);
                 }
                 const bool fin = isfinite(est);
@@ -1560,9 +1688,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
                         est = (lane_in(scored) && tx[sr] != FLT_MAX) ? e : FLT_MAX;
                     } else if (lane_in(scored) && tx[sr] != FLT_MAX) {
                         const int nidx = tsk[sr] + nl;
-                        const int32_t raw = raw_partial(reinterpret_cast<const uint32_t *>(prw[sr] + g.code) +
-                                                            static_cast<uint64_t>(nidx) * W,
-                                                        0, W, planes, W);
+                        const int32_t raw = raw_words(reinterpret_cast<const uint32_t *>(prw[sr] + g.code) +
+                                                          static_cast<uint64_t>(nidx) * W,
+                                                      planes, W, vec_ok, any_wrap);
                         est = estimate_formula(raw, sum_q, qwidth, qlow, tx[sr], fdq[sr], fvq[sr], pdist[pix[sr]]);
                     }
                     // a scored child with a non-finite estimate is dropped
