@@ -210,6 +210,9 @@ def main() -> int:
     recall = recall_of(ids)
     ids_read, estimates, exact = cnt[:, 2].sum(), cnt[:, 3].sum(), cnt[:, 4].sum()
     alg_bytes = int(args.nq * 4 * dim + 4 * ids_read + estimates * (B // 8 + 12) + exact * 4 * dim)
+    work = {k: round(float(cnt[:, i].mean()), 2) for i, k in
+            enumerate(("iterations", "expansions", "ids_read", "estimates", "exact"))}
+    log(f"beam {chosen}: per query {work}")
 
     # timed region: K launches bracketed by synchronisation
     for _ in range(args.warmup):
@@ -291,7 +294,7 @@ def main() -> int:
         "config": {"workload": f"{args.config.upper()} {args.n}x{dim} deg {args.degree}, K={args.K}, nq={args.nq}, "
                                f"beam={chosen}",
                    "beam": chosen, "recall": round(float(recall), 5), "beam_sweep": sweep,
-                   "host_buffers_qps": round(host_qps, 1),
+                   "host_buffers_qps": round(host_qps, 1), "work_per_query": work,
                    "lds_bytes": fg.lds_bytes(dim, chosen, args.degree)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,

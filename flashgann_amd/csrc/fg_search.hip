@@ -689,19 +689,24 @@ __device__ __forceinline__ void bitonic_stage(float (&k)[E], uint32_t (&v)[E]) {
     if constexpr (J > 1) bitonic_stage<E, HALF, KK, J / 2>(k, v);
 }
 
-// Block sizes KK, 2 KK, .. 32 on the HALF layout.
-template <int KK>
+// Block sizes KK, 2 KK, .. TOP on the HALF layout.
+template <int KK, int TOP = 32>
 __device__ __forceinline__ void sort32_from(float (&k)[1], uint32_t (&v)[1]) {
     bitonic_stage<1, true, KK, KK / 2>(k, v);
-    if constexpr (KK < 32) sort32_from<KK * 2>(k, v);
+    if constexpr (KK < TOP) sort32_from<KK * 2, TOP>(k, v);
 }
 
 // warp_sort<1> on 32 positions (utils.cuh:409-414): position = lane & 31, both
-// halves sort the same data.
+// halves sort the same data.  With TOP < 32 only the stages of block sizes up
+// to TOP run.  That equals the full network when positions TOP..31 all hold
+// the same (FLT_MAX, MAX_INDEX) pair and no key below them exceeds FLT_MAX:
+// block 0 then ends sorted ascending, every later compare-exchange meets
+// either that pair or equal or ordered keys, and none of them swaps.
+template <int TOP = 32>
 __device__ __forceinline__ void sort32(float &key, uint32_t &val) {
     float k[1] = {key};
     uint32_t v[1] = {val};
-    sort32_from<2>(k, v);
+    sort32_from<2, TOP>(k, v);
     key = k[0];
     val = v[0];
 }
@@ -838,15 +843,21 @@ __device__ __forceinline__ void merge_path(const SearchParams &P, uint2 *bp, con
 
 // Beam merge (utils.cuh:1369-1399 dispatch for a <= 32-entry buffer): the
 // candidates are sorted (warp_sort<1>), staged in `ms`, and merged into the
-// beam in place.
+// beam in place.  `span`: slots at or past it hold (FLT_MAX, MAX_INDEX), so a
+// candidate buffer filled only in its first 8 or 16 slots is sorted with the
+// stages that reach that block size (sort32<TOP>).
 __device__ __forceinline__ void merge_beam(const SearchParams &P, uint2 *bp, uint2 *ms, const float *cd,
-                                           const uint32_t *ci) {
+                                           const uint32_t *ci, int span) {
     const int lane = lane_id_opaque();
     const int nl = lane & 31, h = lane >> 5;
     const int cbs = P.cbs, pbeam = P.pbeam;
     float ck = nl < cbs ? cd[nl] : FLT_MAX;
     uint32_t cv = nl < cbs ? ci[nl] : kMaxIndex;
-    sort32(ck, cv);
+    // every key of the span at most FLT_MAX (never inf or NaN)
+    const bool short_ok = !any_lane(nl < span && !(ck <= FLT_MAX));
+    if (short_ok && span <= 8) sort32<8>(ck, cv);
+    else if (short_ok && span <= 16) sort32<16>(ck, cv);
+    else sort32(ck, cv);
     if (h == 0) ms[nl] = make_uint2(__float_as_uint(ck), cv);
     __syncthreads();
     if (pbeam == 128) {
@@ -1438,6 +1449,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
     uint32_t c_iters = 0, c_exp = 0, c_ids = 0, c_est = 0, c_exact = 1, c_st2 = kMaxIndex;
     const int beam_sz = P.beam, pbeam = P.pbeam;
     const int cbs = P.cbs;
+    // candidate slots the next merge may find filled (the rest hold the
+    // reset pair): the entry point's slot 0 first, then what each stage fills
+    int cand_span = 1;
     const float *data = P.data;
 
     FG_PHASE(0);
@@ -1457,7 +1471,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
         // adaptive_search.cuh:447-451).  A search that stops because no beam entry is left to
         // expand has merged them already: its final merge sees an empty
         // candidate buffer and leaves the beam as it is.
-        merge_beam(P, bp, ms, cd, ci);
+        merge_beam(P, bp, ms, cd, ci, cand_span);
         FG_PHASE(2);
         if (iter >= P.max_iter) break;
         for (int i = beam_sz + lane; i < pbeam; i += 64) bp[i] = kEmpty;
@@ -1593,6 +1607,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
             FG_COUNT(c_exact += static_cast<uint32_t>(nins));
             ex_n = nins;
             ex_list = alist;
+            cand_span = 32;  // single-expander children sit at their lane's slot
             FG_PHASE(4);
         } else {
             // ---------------- speculative expansion (adaptive_search.cuh:344-444)
@@ -1767,6 +1782,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg
             if (compact > static_cast<uint32_t>(P.collect_cap)) compact = static_cast<uint32_t>(P.collect_cap);
             FG_COUNT(c_exact += compact);
             ex_n = static_cast<int>(compact);
+            cand_span = ex_n;  // compacted into slots 0 .. compact - 1
             FG_PHASE(7);
         }
         exact_batch<DPL>(P, g, ex_n, ex_list, cd, ci, qr, qv);

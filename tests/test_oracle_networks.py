@@ -268,3 +268,35 @@ def test_merge_path_partition_valid_split():
         right = np.concatenate([a[got:], b[bi:]])
         if left.size and right.size:
             assert left.max() <= right.min()
+
+
+@pytest.mark.parametrize("top", [8, 16])
+def test_short_candidate_sort_equals_full_network(top):
+    """A 32-entry candidate buffer whose slots from `span` on hold the reset
+    pair (FLT_MAX, MAX_INDEX), with no key above FLT_MAX, sorts the same
+    under the stages up to block size 8 / 16 as under the full 32-entry
+    network (the kernel sorts such buffers with the shorter networks)."""
+    rng = np.random.default_rng(top)
+    fmax = np.finfo(np.float32).max
+    for _ in range(3000):
+        span = int(rng.integers(0, top + 1))
+        k = np.full(32, fmax, np.float32)
+        v = np.full(32, 0xFFFFFFFF, np.uint32)
+        k[:span] = rng.integers(0, 5, span).astype(np.float32)  # heavy ties
+        if span and rng.random() < 0.25:
+            k[rng.integers(0, span)] = fmax  # a real child at exactly FLT_MAX
+        v[:span] = rng.permutation(4096)[:span]
+        k1, v1, k2, v2 = k.copy(), v.copy(), k.copy(), v.copy()
+        O.lib().fgo_bitonic_sort(O.ptr(k1, C.c_float), O.ptr(v1, C.c_uint32), 32)
+        O.lib().fgo_bitonic_sort(O.ptr(k2, C.c_float), O.ptr(v2, C.c_uint32), top)
+        assert np.array_equal(k1, k2) and np.array_equal(v1, v2), (span, k, v)
+    # an infinite key inside the span breaks the equivalence: the kernel
+    # checks for it and falls back to the full network
+    k = np.full(32, fmax, np.float32)
+    v = np.full(32, 0xFFFFFFFF, np.uint32)
+    k[:3] = [1.0, np.inf, 2.0]
+    v[:3] = [7, 8, 9]
+    k1, v1, k2, v2 = k.copy(), v.copy(), k.copy(), v.copy()
+    O.lib().fgo_bitonic_sort(O.ptr(k1, C.c_float), O.ptr(v1, C.c_uint32), 32)
+    O.lib().fgo_bitonic_sort(O.ptr(k2, C.c_float), O.ptr(v2, C.c_uint32), top)
+    assert not (np.array_equal(k1, k2) and np.array_equal(v1, v2))
