@@ -161,8 +161,10 @@ def hadamard_rotation(signs: np.ndarray, device) -> torch.Tensor:
 
 def build_graph(x: torch.Tensor, degree: int, random_links: int | None = None,
                 seed: int = 0x5EED, alpha: float = 1.0, candidates: int | None = None,
-                fill_random: bool = True, verbose: bool = False) -> torch.Tensor:
-    """Returns (n, degree) int64 neighbour ids (-1 = padding)."""
+                fill_random: bool = True, verbose: bool = False, dist_block_elems: int = 1 << 32) -> torch.Tensor:
+    """Returns (n, degree) int64 neighbour ids (-1 = padding).  The final
+    neighbour distances are gathered in row blocks of at most
+    `dist_block_elems` floats."""
     n = x.shape[0]
     dev = x.device
     kc = min(candidates or 2 * degree, n - 1)
@@ -192,9 +194,9 @@ def build_graph(x: torch.Tensor, degree: int, random_links: int | None = None,
     # sort each list by (distance, id)
     big = torch.iinfo(torch.int64).max
     valid = merged >= 0
-    # distances to the kept neighbours, in row blocks of at most 2^32 gathered
-    # elements (the unblocked gather of 1M x 32 x 960 floats alone is 123 GB)
-    step = max(1, (1 << 32) // max(1, degree * x.shape[1]))
+    # distances to the kept neighbours, in row blocks (the unblocked gather of
+    # 1M x 32 x 960 floats alone is 123 GB)
+    step = max(1, dist_block_elems // max(1, degree * x.shape[1]))
     dist = torch.empty(merged.shape, dtype=torch.float64, device=dev)
     for s in range(0, n, step):
         e = min(n, s + step)

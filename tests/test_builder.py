@@ -90,3 +90,15 @@ def test_truncated_codebook_rejected(tmp_path):
     h = C.c_void_p()
     rc = _lib.lib().fg_index_load(p.encode(), 100, cb.layout.dim, cb.layout.degree, 0, C.byref(h))
     assert rc == _lib.FG_EIO
+
+
+def test_graph_blocked_distances_identical():
+    """The neighbour lists do not depend on the row blocking of the final
+    distance pass (blocks of 7 rows against one block)."""
+    import torch
+    from flashgann_amd import builder, datasets
+    base, _ = datasets.unit_box_mixture(400, 1, 40, 4)
+    x = torch.as_tensor(base)
+    a = builder.build_graph(x, 8)
+    b = builder.build_graph(x, 8, dist_block_elems=7 * 8 * 40)
+    assert torch.equal(a, b)
