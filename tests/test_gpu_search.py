@@ -112,3 +112,59 @@ def test_timed_instantiation_matches_counting_one(gpu_available, dim, degree, ki
         b, _, _ = ix.search(q, K, beam, counters=False)
         assert np.array_equal(a, b), (dim, degree, K, beam)
     ix.close()
+
+
+def _degree_case(degree):
+    """Degree 4 (stage-II keep rate rho2 = 0, the reference's deg <= 4 rule)
+    and degree 64 (the largest the kernel takes: two 32-neighbour tiles per
+    parent)."""
+    cb, q, _ = small_index(n=1500, nq=16, degree=degree)
+    ids, cnt, rids, rcnt = _run(cb, q, 100, 128)
+    _assert_equal(ids, cnt, rids, rcnt, f"degree={degree}")
+
+
+def test_search_degree_4(gpu_available):
+    _degree_case(4)
+
+
+def test_search_degree_64(gpu_available):
+    _degree_case(64)
+
+
+def test_search_inner_product_generic(gpu_available):
+    """Inner product on the generic geometry (300-d: padded dimension 512)."""
+    cb, q, _ = small_index(n=1200, nq=8, dim=300, comps=8, kind="unit", use_ip=True)
+    ids, cnt, rids, rcnt = _run(cb, q, 10, 64, metric=1)
+    _assert_equal(ids, cnt, rids, rcnt, "ip300")
+
+
+def test_cli_end_to_end(gpu_available, tmp_path):
+    """The gpu_flashgann CLI (main.cu's interface) on files written in the
+    reference's formats: printed recall equals the oracle's recall of the
+    same search, and the CSV row has the reference's columns."""
+    import os
+    import re
+    import subprocess
+    from flashgann_amd import builder
+    from flashgann_amd.codebook import write_fvecs, write_ivecs
+    from flashgann_amd.metrics import compute_recall
+    from oracle import oracle as O
+    cb, q, base = small_index()
+    gt = builder.ground_truth(base, q, 10)
+    paths = {k: str(tmp_path / k) for k in ("base.fvecs", "query.fvecs", "gt.ivecs", "cb.index", "out.csv")}
+    write_fvecs(paths["base.fvecs"], base)
+    write_fvecs(paths["query.fvecs"], q)
+    write_ivecs(paths["gt.ivecs"], gt)
+    cb.save(paths["cb.index"])
+    cli = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "flashgann_amd", "bin",
+                       "gpu_flashgann")
+    r = subprocess.run([cli, paths["base.fvecs"], paths["query.fvecs"], paths["gt.ivecs"], paths["cb.index"],
+                        "10", "64", "32", "-csv", paths["out.csv"]], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    m = re.search(r"Recall@10: ([0-9.]+)", r.stdout)
+    assert m, r.stdout
+    ref_ids, _ = O.OracleIndex.from_codebook(cb).search(q, 10, 64)
+    assert abs(float(m.group(1)) - 100.0 * compute_recall(ref_ids, gt, 10)) < 1e-3
+    rows = open(paths["out.csv"]).read().strip().splitlines()
+    assert rows[0] == "TopK,Beam_size,Runtime,Latency,Throughput,Recall"
+    assert rows[1].split(",")[:2] == ["10", "64"]
