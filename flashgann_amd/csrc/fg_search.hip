@@ -475,33 +475,33 @@ __device__ __forceinline__ int32_t raw_partial(const uint32_t *__restrict__ code
 
 // raw for one neighbour code of W words (W a power of two >= 8: padded
 // dimension >= 256), the same sum as raw_partial over [0, W): the code words
-// are loaded 16 at a time (four 16-byte loads when the row layout keeps codes
-// 16-byte aligned), issued together, and each plane's matching words come
-// from LDS as 16-byte reads.
+// are loaded 32 at a time (eight 16-byte loads when the row layout keeps
+// codes 16-byte aligned), issued together, and each plane's matching words
+// come from LDS as 16-byte reads.
 __device__ __forceinline__ int32_t raw_words(const uint32_t *__restrict__ code, const uint32_t *planes, int W,
                                              bool vec_ok, bool any_wrap) {
     uint32_t acc[kPlanes];
 #pragma unroll
     for (int p = 0; p < kPlanes; ++p) acc[p] = 0;
     uint32_t wraps = 0;
-    const int nb = W < 16 ? W : 16;  // words per batch: 8 or 16
+    const int nb = W < 32 ? W : 32;  // words per batch: 8, 16 or 32
     for (int w0 = 0; w0 < W; w0 += nb) {
-        uint32_t c[16];
+        uint32_t c[32];
         if (vec_ok) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < 8; ++j) {
                 const uint4 v = j * 4 < nb ? reinterpret_cast<const uint4 *>(code + w0)[j] : make_uint4(0u, 0u, 0u, 0u);
                 c[4 * j] = v.x; c[4 * j + 1] = v.y; c[4 * j + 2] = v.z; c[4 * j + 3] = v.w;
             }
         } else {
 #pragma unroll
-            for (int j = 0; j < 16; ++j) c[j] = j < nb ? code[w0 + j] : 0u;
+            for (int j = 0; j < 32; ++j) c[j] = j < nb ? code[w0 + j] : 0u;
         }
 #pragma unroll
         for (int p = 0; p < kPlanes; ++p) {
             const uint4 *pl = reinterpret_cast<const uint4 *>(planes + p * W + w0);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < 8; ++j) {
                 if (j * 4 < nb) {
                     const uint4 q = pl[j];
                     acc[p] += __popc(c[4 * j] & q.x) + __popc(c[4 * j + 1] & q.y) + __popc(c[4 * j + 2] & q.z) +
@@ -512,7 +512,7 @@ __device__ __forceinline__ int32_t raw_words(const uint32_t *__restrict__ code, 
         if (any_wrap) {
             const uint32_t *wp = planes + kPlanes * W + w0;
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
+            for (int j = 0; j < 32; ++j) {
                 if (j < nb) {
                     const uint32_t x = c[j] & wp[j];
                     wraps += __popc(x & (x >> 1) & (x >> 2) & (x >> 3) & 0x11111111u);
@@ -1259,10 +1259,10 @@ __device__ __forceinline__ void exact_batch(const SearchParams &P, const G &g, i
         else if (rem > 2) exact_pass<2, DPL>(P, g, e0, n, slot_list, cd, ci, qr, ip);
         else if (rem > 0) exact_pass<1, DPL>(P, g, e0, n, slot_list, cd, ci, qr, ip);
     } else {
-        // four children per pass (two per half), 8 dimension steps per load batch
+        // four children per pass (two per half), 16 dimension steps per load batch
         int e0 = 0;
-        for (; n - e0 > 2; e0 += 4) exact_generic_pass<2, 8>(P, g.row, g.dim, e0, n, slot_list, cd, ci, qv, ip);
-        if (e0 < n) exact_generic_pass<1, 8>(P, g.row, g.dim, e0, n, slot_list, cd, ci, qv, ip);
+        for (; n - e0 > 2; e0 += 4) exact_generic_pass<2, 16>(P, g.row, g.dim, e0, n, slot_list, cd, ci, qv, ip);
+        if (e0 < n) exact_generic_pass<1, 16>(P, g.row, g.dim, e0, n, slot_list, cd, ci, qv, ip);
     }
 }
 
@@ -1351,9 +1351,12 @@ __device__ __forceinline__ void hash_contains_n(const uint32_t *t, uint32_t nb, 
 
 // One wave per workgroup; the register budget targets 5 waves per SIMD
 // (<= 96 VGPRs), which LDS also allows for beams up to 256 (21 workgroups per
-// CU at 6,960 bytes).
+// CU at 6,960 bytes).  The generic-geometry instantiation (padded dimension
+// >= 256) gets 4 (<= 128 VGPRs) for its wider load batches: at padded
+// dimension 1024 and up its LDS (raw query, planes, rotation scratch) holds
+// it to fewer waves than that anyway.
 template <int WT, int DPL, int DIM_T, int DEG_T, bool COUNT, bool PROF>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void fg_search_kernel(SearchParams P) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 : 5))) void fg_search_kernel(SearchParams P) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int qid = blockIdx.x;
     if (qid >= P.nq) return;
