@@ -1259,10 +1259,12 @@ __device__ __forceinline__ void exact_batch(const SearchParams &P, const G &g, i
         else if (rem > 2) exact_pass<2, DPL>(P, g, e0, n, slot_list, cd, ci, qr, ip);
         else if (rem > 0) exact_pass<1, DPL>(P, g, e0, n, slot_list, cd, ci, qr, ip);
     } else {
-        // four children per pass (two per half), 16 dimension steps per load batch
+        // six children per pass (three per half), 16 dimension steps per
+        // load batch; the last pass sized to what is left
         int e0 = 0;
-        for (; n - e0 > 2; e0 += 4) exact_generic_pass<2, 16>(P, g.row, g.dim, e0, n, slot_list, cd, ci, qv, ip);
-        if (e0 < n) exact_generic_pass<1, 16>(P, g.row, g.dim, e0, n, slot_list, cd, ci, qv, ip);
+        for (; n - e0 > 4; e0 += 6) exact_generic_pass<3, 16>(P, g.row, g.dim, e0, n, slot_list, cd, ci, qv, ip);
+        if (n - e0 > 2) exact_generic_pass<2, 16>(P, g.row, g.dim, e0, n, slot_list, cd, ci, qv, ip);
+        else if (e0 < n) exact_generic_pass<1, 16>(P, g.row, g.dim, e0, n, slot_list, cd, ci, qv, ip);
     }
 }
 
