@@ -1882,7 +1882,9 @@ __global__ __launch_bounds__(64) void fg_score_kernel(ScoreParams S) {
     const int hw = W >> 1;
     const int32_t part = raw_partial(code, h * hw, (h + 1) * hw, planes, W);
     const int32_t raw_split = add32i(part);
-    const int32_t raw_full = raw_partial(code, 0, W, planes, W);
+    // the search kernel's own routine for the generic geometry (W >= 8)
+    const bool vec_ok = S.row_offset % 4 == 0 && S.code_offset % 4 == 0;
+    const int32_t raw_full = W >= 8 ? raw_words(code, planes, W, vec_ok, true) : raw_partial(code, 0, W, planes, W);
     const float el = tx == FLT_MAX ? 0.0f : estimate_formula(raw_split, sq, w, lo, tx, fdq, fvq, pd);
     const float es = tx == FLT_MAX ? FLT_MAX : estimate_formula(raw_full, sq, w, lo, tx, fdq, fvq, pd);
     const uint32_t child = reinterpret_cast<const uint32_t *>(prow + (S.factor_offset + 3 * S.deg))[slot];

@@ -12,11 +12,14 @@ from conftest import small_index
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("kind,dim", [("int", 128), ("unit", 96), ("box", 960)])
-def test_query_prepare_matches_oracle(gpu_available, kind, dim):
+STAGE_CASES = [("int", 128, 1500), ("unit", 96, 1500), ("box", 960, 1500), ("aniso", 1536, 1200)]
+
+
+@pytest.mark.parametrize("kind,dim,n", STAGE_CASES)
+def test_query_prepare_matches_oracle(gpu_available, kind, dim, n):
     from flashgann_amd import Index
     from oracle import oracle as O
-    cb, q, _ = small_index(n=1500, nq=8, dim=dim, comps=8, kind=kind)
+    cb, q, _ = small_index(n=n, nq=8, dim=dim, comps=8, kind=kind)
     ix = Index.from_codebook(cb)
     rot, qt, lhw, sq = ix.query_prepare(q)
     B = cb.layout.padded_dim
@@ -29,11 +32,11 @@ def test_query_prepare_matches_oracle(gpu_available, kind, dim):
     ix.close()
 
 
-@pytest.mark.parametrize("kind,dim", [("int", 128), ("unit", 96), ("box", 960)])
-def test_scores_match_oracle(gpu_available, kind, dim):
+@pytest.mark.parametrize("kind,dim,n", STAGE_CASES)
+def test_scores_match_oracle(gpu_available, kind, dim, n):
     from flashgann_amd import Index
     from oracle import oracle as O
-    cb, q, _ = small_index(n=1500, nq=8, dim=dim, comps=8, kind=kind)
+    cb, q, _ = small_index(n=n, nq=8, dim=dim, comps=8, kind=kind)
     ix = Index.from_codebook(cb)
     rng = np.random.default_rng(5)
     n = 300
