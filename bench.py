@@ -74,6 +74,8 @@ def main() -> int:
                     help="queries per swept beam whose GPU ids are compared with the CPU oracle's")
     ap.add_argument("--traffic", type=str, default=os.path.join(ROOT, "profiles", "search_c2_traffic.json"))
     ap.add_argument("--cache", type=str, default="", help="directory to reuse the built index and ground truth")
+    ap.add_argument("--serve-batches", type=int, default=8,
+                    help="batches of nq queries in the serving measurement (0 = skip)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run one plain 1 GiB device copy (counter calibration for profiling)")
     args = ap.parse_args()
@@ -243,6 +245,46 @@ def main() -> int:
     host_qps = 3 * args.nq / (time.perf_counter() - t_host)
     log(f"beam {chosen}: {host_qps:.0f} QPS through fg_search (host buffers, PCIe included)")
 
+    # Serving measurement (reported beside `value`, never as it): R batches of
+    # the nq queries back to back, (a) one launch per batch on one stream (the
+    # reference's one-launch-per-call pattern), (b) fg_search_stream with the
+    # batches spread over two streams, (c) one launch over all R*nq queries.
+    serving = None
+    if args.serve_batches > 0:
+        R = args.serve_batches
+        dqr = dq.repeat(R, 1).contiguous()
+        drr = torch.empty((R * args.nq, args.K), dtype=torch.int32, device=dev)
+
+        def timed(fn, reps=3):
+            fn()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                fn()
+            torch.cuda.synchronize()
+            return (time.perf_counter() - t0) / reps
+
+        def serial():
+            for r in range(R):
+                index.search_device(dqr[r * args.nq].data_ptr(), args.nq, args.K, chosen,
+                                    drr[r * args.nq].data_ptr(), 0, stream.cuda_stream)
+
+        def streamed():
+            index.search_stream(dqr.data_ptr(), R * args.nq, args.K, chosen, drr.data_ptr(), args.nq, 2,
+                                stream.cuda_stream)
+
+        def single():
+            index.search_device(dqr.data_ptr(), R * args.nq, args.K, chosen, drr.data_ptr(), 0, stream.cuda_stream)
+
+        t_serial, t_stream, t_single = timed(serial), timed(streamed), timed(single)
+        same = bool((drr[: args.nq].cpu().numpy().view(np.uint32) == ids).all())
+        serving = {"batches": R, "batch": args.nq, "serial_qps": round(R * args.nq / t_serial, 1),
+                   "two_stream_qps": round(R * args.nq / t_stream, 1),
+                   "one_launch_qps": round(R * args.nq / t_single, 1), "ids_identical": same}
+        log(f"serving {R} x {args.nq} queries at beam {chosen}: one stream {serving['serial_qps']:.0f} QPS, "
+            f"two streams {serving['two_stream_qps']:.0f} QPS, one launch {serving['one_launch_qps']:.0f} QPS")
+        del dqr, drr
+
     traffic = None
     if os.path.exists(args.traffic):
         try:
@@ -294,7 +336,7 @@ def main() -> int:
         "config": {"workload": f"{args.config.upper()} {args.n}x{dim} deg {args.degree}, K={args.K}, nq={args.nq}, "
                                f"beam={chosen}",
                    "beam": chosen, "recall": round(float(recall), 5), "beam_sweep": sweep,
-                   "host_buffers_qps": round(host_qps, 1), "work_per_query": work,
+                   "host_buffers_qps": round(host_qps, 1), "work_per_query": work, "serving": serving,
                    "lds_bytes": fg.lds_bytes(dim, chosen, args.degree)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,

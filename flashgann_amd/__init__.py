@@ -115,6 +115,14 @@ class Index:
                                      C.c_void_p(results_ptr), C.c_void_p(counters_ptr or None),
                                      C.c_void_p(stream or None)))
 
+    def search_stream(self, queries_ptr: int, nq: int, K: int, beam: int, results_ptr: int,
+                      batch: int, nstreams: int = 2, stream: int = 0) -> None:
+        """Device pointers; the nq queries searched as batches of `batch` on
+        `nstreams` internal streams (fg_search_stream), ordered after prior
+        work on `stream` and before its later work."""
+        check(lib().fg_search_stream(self._h, C.c_void_p(queries_ptr), nq, K, beam, C.c_void_p(results_ptr),
+                                     batch, nstreams, C.c_void_p(stream or None)))
+
     def search_profile(self, queries_ptr: int, nq: int, K: int, beam: int, results_ptr: int,
                        phase_ptr: int, stream: int = 0) -> None:
         """Profiling build of the search: per query, 10 uint64 phase-cycle sums

@@ -23,7 +23,7 @@ FG_PROFILE_SLOTS = 12
 
 EXPORTED = (
     "fg_index_create", "fg_index_load", "fg_index_destroy", "fg_index_get_info", "fg_search",
-    "fg_search_device", "fg_search_profile", "fg_lds_bytes", "fg_query_prepare", "fg_score_edges", "fg_last_error",
+    "fg_search_device", "fg_search_stream", "fg_search_profile", "fg_lds_bytes", "fg_query_prepare", "fg_score_edges", "fg_last_error",
     "fg_version",
 )
 
@@ -71,6 +71,7 @@ def lib():
                                 C.POINTER(Stats)]
         L.fg_search_device.argtypes = [vp, vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp, vp]
         L.fg_search_profile.argtypes = [vp, vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp, vp]
+        L.fg_search_stream.argtypes = [vp, vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, C.c_uint32, C.c_uint32, vp]
         L.fg_lds_bytes.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32]
         L.fg_lds_bytes.restype = C.c_uint32
         L.fg_query_prepare.argtypes = [vp, f32p, C.c_uint32, f32p, u8p, f32p, i32p]

@@ -1918,6 +1918,12 @@ struct fg_index {
     uint32_t *d_cnt = nullptr;
     size_t cnt_cap = 0;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    // serving streams of fg_search_stream (created on first use, default priority)
+    static constexpr int kMaxServeStreams = 8;
+    hipStream_t serve[kMaxServeStreams] = {};
+    hipEvent_t serve_done[kMaxServeStreams] = {};
+    hipEvent_t serve_start = nullptr;
+    int serve_count = 0;
 };
 
 namespace {
@@ -2187,6 +2193,12 @@ void fg_index_destroy(fg_index *ix) {
     if (ix->d_cnt) (void)hipFree(ix->d_cnt);
     if (ix->ev0) (void)hipEventDestroy(ix->ev0);
     if (ix->ev1) (void)hipEventDestroy(ix->ev1);
+    for (int i = 0; i < ix->serve_count; ++i) {
+        (void)hipStreamSynchronize(ix->serve[i]);
+        (void)hipStreamDestroy(ix->serve[i]);
+        (void)hipEventDestroy(ix->serve_done[i]);
+    }
+    if (ix->serve_start) (void)hipEventDestroy(ix->serve_start);
     delete ix;
 }
 
@@ -2216,6 +2228,51 @@ int fg_search_device(fg_index *ix, const float *d_queries, uint32_t nq, uint32_t
     P.counters = d_counters;
     P.phase = nullptr;
     return launch(ix, P, reinterpret_cast<hipStream_t>(stream));
+}
+
+int fg_search_stream(fg_index *ix, const float *d_queries, uint32_t nq, uint32_t K, uint32_t beam,
+                     uint32_t *d_results, uint32_t batch, uint32_t nstreams, void *stream) {
+    if (!ix) return fail(FG_EINVAL, "index is NULL");
+    if (batch == 0) return fail(FG_EINVAL, "batch must be >= 1");
+    if (nstreams < 1 || nstreams > static_cast<uint32_t>(fg_index::kMaxServeStreams))
+        return fail(FG_EINVAL, "nstreams must be in [1, 8]");
+    if (nq && (!d_queries || !d_results)) return fail(FG_EINVAL, "NULL device buffer");
+    SearchParams P;
+    if (int rc = make_params(ix, batch < nq ? batch : nq, K, beam, P)) return rc;
+    if (nq == 0) return FG_OK;
+    hipStream_t caller = reinterpret_cast<hipStream_t>(stream);
+    while (ix->serve_count < static_cast<int>(nstreams)) {
+        const int i = ix->serve_count;
+        FG_HIP(hipStreamCreateWithFlags(&ix->serve[i], hipStreamNonBlocking), "serving stream");
+        if (hipEventCreateWithFlags(&ix->serve_done[i], hipEventDisableTiming) != hipSuccess) {
+            (void)hipStreamDestroy(ix->serve[i]);
+            return fail(FG_EDEVICE, "serving event");
+        }
+        ix->serve_count = i + 1;
+    }
+    if (!ix->serve_start) FG_HIP(hipEventCreateWithFlags(&ix->serve_start, hipEventDisableTiming), "serving event");
+    // every batch runs after the work already queued on the caller's stream
+    FG_HIP(hipEventRecord(ix->serve_start, caller), "event record");
+    const uint32_t nbatch = (nq + batch - 1) / batch;
+    const uint32_t used = nbatch < nstreams ? nbatch : nstreams;
+    for (uint32_t i = 0; i < used; ++i) FG_HIP(hipStreamWaitEvent(ix->serve[i], ix->serve_start, 0), "stream wait");
+    for (uint32_t b = 0; b < nbatch; ++b) {
+        const uint64_t q0 = static_cast<uint64_t>(b) * batch;
+        const uint32_t n = static_cast<uint32_t>(nq - q0 < batch ? nq - q0 : batch);
+        SearchParams Pb = P;
+        Pb.nq = static_cast<int>(n);
+        Pb.queries = d_queries + q0 * ix->dim;
+        Pb.results = d_results + q0 * K;
+        Pb.counters = nullptr;
+        Pb.phase = nullptr;
+        if (int rc = launch(ix, Pb, ix->serve[b % nstreams])) return rc;
+    }
+    // and the caller's later work runs after every batch
+    for (uint32_t i = 0; i < used; ++i) {
+        FG_HIP(hipEventRecord(ix->serve_done[i], ix->serve[i]), "event record");
+        FG_HIP(hipStreamWaitEvent(caller, ix->serve_done[i], 0), "stream wait");
+    }
+    return FG_OK;
 }
 
 int fg_search_profile(fg_index *ix, const float *d_queries, uint32_t nq, uint32_t K, uint32_t beam,

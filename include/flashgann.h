@@ -99,6 +99,20 @@ int fg_search(fg_index *index, const float *queries, uint32_t nq, uint32_t K, ui
 int fg_search_device(fg_index *index, const float *d_queries, uint32_t nq, uint32_t K,
                      uint32_t beam, uint32_t *d_results, uint32_t *d_counters, void *stream);
 
+/* Serving form of fg_search_device for a stream of query batches (the
+ * reference has no counterpart: its gpu_search_adaptive.cu:99-103 launches
+ * one kernel per call and synchronises).  The nq device-resident queries are
+ * searched as consecutive batches of `batch` queries, batch b on internal
+ * stream b % nstreams (1 <= nstreams <= 8, created on first use and owned by
+ * the index), so one batch's last, partly filled wave slots overlap the next
+ * batch's start.  Results land in query order in d_results (nq x K); each
+ * query's ids are those fg_search_device returns.  All batches run after the
+ * work already queued on `stream` and that stream's later work waits for
+ * all of them; the call returns without synchronising.  Calls on one index
+ * share its internal streams: issue them from one host thread. */
+int fg_search_stream(fg_index *index, const float *d_queries, uint32_t nq, uint32_t K, uint32_t beam,
+                     uint32_t *d_results, uint32_t batch, uint32_t nstreams, void *stream);
+
 /* Diagnostics: the same search as fg_search_device, built with phase timers.
  * d_phase receives FG_PROFILE_SLOTS uint64 per query: shader-clock cycles
  * spent in query preparation + set-up, visited-table restore, beam merge,

@@ -55,3 +55,10 @@ def test_header_constants_match_binding():
     for name in ("FG_OK", "FG_EINVAL", "FG_ENOMEM", "FG_EDEVICE", "FG_EIO", "FG_METRIC_L2", "FG_METRIC_IP",
                  "FG_ENTRY_AUTO", "FG_COUNTERS_PER_QUERY", "FG_PROFILE_SLOTS"):
         assert defs[name] == getattr(_lib, name), name
+
+
+def test_search_stream_rejects_null_index():
+    from flashgann_amd import _lib
+    L = _lib.lib()
+    rc = L.fg_search_stream(None, None, 0, 10, 64, None, 16, 2, None)
+    assert rc == _lib.FG_EINVAL and b"NULL" in L.fg_last_error()

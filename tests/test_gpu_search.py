@@ -168,3 +168,23 @@ def test_cli_end_to_end(gpu_available, tmp_path):
     rows = open(paths["out.csv"]).read().strip().splitlines()
     assert rows[0] == "TopK,Beam_size,Runtime,Latency,Throughput,Recall"
     assert rows[1].split(",")[:2] == ["10", "64"]
+
+
+@pytest.mark.parametrize("batch,nstreams", [(5, 1), (5, 2), (7, 3), (24, 2), (100, 4)])
+def test_search_stream_matches_single_launch(gpu_available, batch, nstreams):
+    """fg_search_stream (batches on internal streams) returns, in query order,
+    the ids of one fg_search_device launch over the same queries, and the
+    caller's stream sees them complete."""
+    import torch
+    from flashgann_amd import Index
+    cb, q, _ = small_index()
+    ix = Index.from_codebook(cb)
+    dq = torch.as_tensor(q, device="cuda")
+    ref = torch.zeros((q.shape[0], 100), dtype=torch.int32, device="cuda")
+    out = torch.full((q.shape[0], 100), -1, dtype=torch.int32, device="cuda")
+    s = torch.cuda.current_stream()
+    ix.search_device(dq.data_ptr(), q.shape[0], 100, 128, ref.data_ptr(), 0, s.cuda_stream)
+    ix.search_stream(dq.data_ptr(), q.shape[0], 100, 128, out.data_ptr(), batch, nstreams, s.cuda_stream)
+    got = out.cpu()  # ordered after the batches on the caller's stream
+    assert torch.equal(got, ref.cpu())
+    ix.close()
