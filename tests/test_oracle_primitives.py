@@ -36,7 +36,8 @@ def test_sizing_helpers():
     lib = L()
     assert [lib.fgo_effective_sort_beam_size(b) for b in (1, 16, 32, 33, 64, 100, 128, 129, 384, 1024)] == \
         [32, 32, 32, 64, 64, 128, 128, 129, 384, 1024]
-    # hash bitlen is 11 at every benchmark configuration
+    # hash bitlen is 11 at every benchmark beam (pbeam 32..1024, buffer 32,
+    # reset interval 16: utils.cuh:137-151)
     for pb in (32, 64, 128, 256, 512, 1024):
         assert lib.fgo_hash_bitlen(pb, 32, 16) == 11
     assert [lib.fgo_candidate_buffer_capacity(d) for d in (1, 2, 3, 4, 16, 32, 64)] == [8, 16, 24, 32, 32, 32, 32]
