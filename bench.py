@@ -58,6 +58,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=str, default="c2", choices=sorted(CONFIGS),
                     help="BASELINE configuration (c2 = the headline; the others for coverage)")
+    ap.add_argument("--metric", type=str, default="l2", choices=("l2", "ip"),
+                    help="distance (ip: inner product, the reference's Text2Image path; codes, graph and "
+                         "ground truth built for it)")
     ap.add_argument("--n", type=int, default=0, help="base points (default: the configuration's)")
     ap.add_argument("--nq", type=int, default=0)
     ap.add_argument("--components", type=int, default=0)
@@ -111,7 +114,8 @@ def main() -> int:
     base, queries = getattr(datasets, conf["gen"])(args.n, args.nq, dim, args.components, config=conf["cfg"])
     signs = datasets.signs_for(B, conf["cfg"])
     log(f"data {args.n}x{dim} + {args.nq} queries in {time.time() - t0:.1f}s")
-    tag = f"{args.config}_{args.n}_{args.nq}_{args.components}_{args.degree}_{args.K}"
+    use_ip = args.metric == "ip"
+    tag = f"{args.config}_{args.n}_{args.nq}_{args.components}_{args.degree}_{args.K}" + ("_ip" if use_ip else "")
     cb_path = os.path.join(args.cache, tag + ".index") if args.cache else ""
     gt_path = os.path.join(args.cache, tag + ".gt.npy") if args.cache else ""
     if cb_path and os.path.exists(cb_path) and os.path.exists(gt_path):
@@ -120,10 +124,10 @@ def main() -> int:
         log(f"codebook and ground truth loaded from {args.cache}")
     else:
         t0 = time.time()
-        cb = builder.build_codebook(base, args.degree, signs, device=dev)
+        cb = builder.build_codebook(base, args.degree, signs, use_ip=use_ip, device=dev)
         log(f"codebook built on GPU in {time.time() - t0:.1f}s (entry {cb.entry})")
         t0 = time.time()
-        gt = builder.ground_truth(base, queries, args.K, device=dev)
+        gt = builder.ground_truth(base, queries, args.K, device=dev, use_ip=use_ip)
         log(f"ground truth in {time.time() - t0:.1f}s")
         if cb_path:
             os.makedirs(args.cache, exist_ok=True)
@@ -139,7 +143,7 @@ def main() -> int:
         log("copy probe: 1 GiB read + 1 GiB written by one device copy")
         del src, dst
 
-    index = fg.Index.from_codebook(cb)
+    index = fg.Index.from_codebook(cb, metric=fg.METRIC_IP if use_ip else fg.METRIC_L2)
     dq = torch.as_tensor(queries, device=dev)
     dres = torch.empty((args.nq, args.K), dtype=torch.int32, device=dev)
     dcnt = torch.empty((args.nq, fg.FG_COUNTERS_PER_QUERY), dtype=torch.int32, device=dev)
@@ -162,7 +166,7 @@ def main() -> int:
     threads = max(1, min(threads or 1, 16))
     if not args.no_cpu:
         from oracle import oracle as O
-        oix = O.OracleIndex.from_codebook(cb)
+        oix = O.OracleIndex.from_codebook(cb, use_ip=use_ip)
 
     # Beam sweep (the reference README's QPS-recall list): per beam one
     # counting launch, then timed launches (HIP events), recall@K against the
@@ -319,8 +323,9 @@ def main() -> int:
             f"of the sample")
 
     line = {
-        "metric": ("queries/sec at recall@100>=0.95 (1M x 128 fp32, deg 32)" if args.config == "c2" else
-                   f"queries/sec at recall@{args.K}>={args.target_recall} ({args.n} x {dim} fp32, deg {args.degree})"),
+        "metric": ("queries/sec at recall@100>=0.95 (1M x 128 fp32, deg 32)" if args.config == "c2" and not use_ip
+                   else f"queries/sec at recall@{args.K}>={args.target_recall} ({args.n} x {dim} fp32, deg {args.degree}"
+                        f"{', inner product' if use_ip else ''})"),
         "value": round(qps, 1),
         "unit": "queries/s",
         "n_gpus": 1,
@@ -334,7 +339,7 @@ def main() -> int:
         "data": f"synthetic: seeded {conf['gen'].replace('_', ' ')} ({args.components} components), "
                 "graph and codes built in-run",
         "config": {"workload": f"{args.config.upper()} {args.n}x{dim} deg {args.degree}, K={args.K}, nq={args.nq}, "
-                               f"beam={chosen}",
+                               f"beam={chosen}" + (", inner product" if use_ip else ""),
                    "beam": chosen, "recall": round(float(recall), 5), "beam_sweep": sweep,
                    "host_buffers_qps": round(host_qps, 1), "work_per_query": work, "serving": serving,
                    "lds_bytes": fg.lds_bytes(dim, chosen, args.degree)},

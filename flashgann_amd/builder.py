@@ -308,9 +308,9 @@ def ground_truth(base: np.ndarray, queries: np.ndarray, k: int,
     for s in range(0, q.shape[0], 1024):
         d = -(q[s : s + 1024] @ b.T)
         dv, di = torch.topk(d, min(b.shape[0], k + 16), dim=1, largest=False)
-        o = torch.argsort(di, 1)
+        o = torch.argsort(di, dim=1)
         di, dv = torch.gather(di, 1, o), torch.gather(dv, 1, o)
-        o = torch.argsort(dv, 1, stable=True)
+        o = torch.argsort(dv, dim=1, stable=True)
         out.append(torch.gather(di, 1, o)[:, :k].cpu().numpy())
     return np.concatenate(out).astype(np.int32)
 

@@ -102,3 +102,15 @@ def test_graph_blocked_distances_identical():
     a = builder.build_graph(x, 8)
     b = builder.build_graph(x, 8, dist_block_elems=7 * 8 * 40)
     assert torch.equal(a, b)
+
+
+def test_ground_truth_inner_product_brute_force():
+    """Exact top-k by inner product (ties by id) against numpy brute force."""
+    from flashgann_amd import builder, datasets
+    base, q = datasets.normalized_mixture(600, 9, 24, 6)
+    gt = builder.ground_truth(base, q, 10, use_ip=True)
+    s = q.astype(np.float64) @ base.astype(np.float64).T
+    for i in range(q.shape[0]):
+        order = sorted(range(base.shape[0]), key=lambda j: (-s[i, j], j))[:10]
+        assert set(gt[i]) == set(order)
+        assert np.all(np.diff(-s[i, gt[i]]) >= -1e-6)
