@@ -202,6 +202,7 @@ struct SearchParams {
     int use_ip;
     int dup_free;
     int vec_ok;
+    int runtime_geo;  // host only: run the runtime-geometry kernels
     uint32_t entry;
     int nq;
     LdsLayout lds;
@@ -220,6 +221,10 @@ struct Geo {
     static constexpr int kFactor = DIM_T + kB / 64 * 2 * DEG_T;
     static constexpr int kNbr = kFactor + 3 * DEG_T;
     static constexpr int kRow = kNbr + DEG_T;
+    // byte offsets of the fixed geometry: the host runs it only when every
+    // row starts below 4 GiB, so a row's byte offset is node * kRowB in 32
+    // bits (node < 2^24) and loads take a uniform base plus a 32-bit offset
+    static constexpr uint32_t kRowB = 4u * kRow, kCodeB = 4u * DIM_T, kFactorB = 4u * kFactor, kNbrB = 4u * kNbr;
     int dim, deg, B;
     uint64_t row, code, factor, nbr;
     __device__ __forceinline__ explicit Geo(const SearchParams &P)
@@ -233,6 +238,14 @@ struct Geo {
 };
 
 // ------------------------------------------------------------ device helpers
+
+// A T at byte offset `off` of `base` (a kernel argument, so uniform): the
+// address is a scalar base plus a 32-bit vector offset, with no 64-bit
+// per-lane address arithmetic.
+template <class T>
+__device__ __forceinline__ T ld_at(const float *base, uint32_t off) {
+    return *reinterpret_cast<const T *>(reinterpret_cast<const char *>(base) + off);
+}
 
 // The lane id, through an empty asm: values derived from it (lane masks,
 // addresses) are computed where they are used instead of being hoisted out of
@@ -1158,13 +1171,24 @@ __device__ __forceinline__ void exact_pass(const SearchParams &P, const G &g, in
 #pragma unroll
     for (int j = 0; j < PB; ++j) cid[j] = ci[sl[j]];
     float v[PB][DPL];
-    const float *dl = P.data + nl;  // this lane's first dimension of row 0
+    if constexpr (G::kFixed) {
+        const uint32_t lo = static_cast<uint32_t>(nl) * 4u;  // this lane's first dimension
 #pragma unroll
-    for (int j = 0; j < PB; ++j) {
-        const uint32_t child = e0 + 2 * j + h < n ? cid[j] : 0u;
-        const float *row = dl + static_cast<uint64_t>(child) * g.row;
+        for (int j = 0; j < PB; ++j) {
+            const uint32_t child = e0 + 2 * j + h < n ? cid[j] : 0u;
+            const uint32_t off = __umul24(child, G::kRowB) + lo;
 #pragma unroll
-        for (int k = 0; k < DPL; ++k) v[j][k] = nl + 32 * k < g.dim ? row[32 * k] : 0.0f;
+            for (int k = 0; k < DPL; ++k) v[j][k] = nl + 32 * k < g.dim ? ld_at<float>(P.data, off + 128u * k) : 0.0f;
+        }
+    } else {
+        const float *dl = P.data + nl;  // this lane's first dimension of row 0
+#pragma unroll
+        for (int j = 0; j < PB; ++j) {
+            const uint32_t child = e0 + 2 * j + h < n ? cid[j] : 0u;
+            const float *row = dl + static_cast<uint64_t>(child) * g.row;
+#pragma unroll
+            for (int k = 0; k < DPL; ++k) v[j][k] = nl + 32 * k < g.dim ? row[32 * k] : 0.0f;
+        }
     }
     // the metric test sits outside the loops: inside, each dimension became
     // both updates and a select
@@ -1632,6 +1656,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
                 bool val[SR];
                 int an[SR], tsk[SR], pix[SR];
                 const float *prw[SR];
+                uint32_t rof[SR];  // fixed geometry: the parents' row byte offsets
                 float tx[SR], fdq[SR], fvq[SR];
                 uint32_t code[SR][WTR];
                 // (a) neighbour ids of the round's 8 tasks, then their factors and
@@ -1653,22 +1678,47 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
                     nsafe[sr] = nidx < deg ? nidx : deg - 1;
                     tsk[sr] = tact ? tile * 32 : -1;
                     pix[sr] = pidx;
-                    prw[sr] = data + static_cast<uint64_t>(pnode[pidx]) * g.row;
-                    cid[sr] = reinterpret_cast<const uint32_t *>(prw[sr] + g.nbr)[nsafe[sr]];
+                    if constexpr (kFixedGeo) {
+                        rof[sr] = __umul24(pnode[pidx], Geo<DIM_T, DEG_T>::kRowB);
+                        cid[sr] = ld_at<uint32_t>(data, rof[sr] + Geo<DIM_T, DEG_T>::kNbrB + 4u * nsafe[sr]);
+                    } else {
+                        prw[sr] = data + static_cast<uint64_t>(pnode[pidx]) * g.row;
+                        cid[sr] = reinterpret_cast<const uint32_t *>(prw[sr] + g.nbr)[nsafe[sr]];
+                    }
                     int a = tact ? deg - tile * 32 : 0;
                     an[sr] = a > 32 ? 32 : a;
                     FG_COUNT(c_ids += static_cast<uint32_t>(__popcll(ballot(lact[sr]))));
                 }
 #pragma unroll
                 for (int sr = 0; sr < SR; ++sr) {
-                    const float *factors = prw[sr] + g.factor;
-                    tx[sr] = factors[nsafe[sr]];
-                    fdq[sr] = factors[deg + nsafe[sr]];
-                    fvq[sr] = factors[2 * deg + nsafe[sr]];
-                    if constexpr (WT > 0)
-                        load_code<WT>(reinterpret_cast<const uint32_t *>(prw[sr] + g.code) +
-                                          static_cast<uint64_t>(nsafe[sr]) * WT,
-                                      vec_ok, code[sr]);
+                    if constexpr (kFixedGeo) {
+                        using GF = Geo<DIM_T, DEG_T>;
+                        const uint32_t fo = rof[sr] + GF::kFactorB + 4u * nsafe[sr];
+                        tx[sr] = ld_at<float>(data, fo);
+                        fdq[sr] = ld_at<float>(data, fo + 4u * DEG_T);
+                        fvq[sr] = ld_at<float>(data, fo + 8u * DEG_T);
+                        const uint32_t co = rof[sr] + GF::kCodeB + 4u * WT * nsafe[sr];
+                        if constexpr (WT == 4) {
+                            // 16-byte aligned: the fixed rows and code blocks are multiples of 16 bytes
+                            const uint4 c4 = ld_at<uint4>(data, co);
+                            code[sr][0] = c4.x;
+                            code[sr][1] = c4.y;
+                            code[sr][2] = c4.z;
+                            code[sr][3] = c4.w;
+                        } else {
+#pragma unroll
+                            for (int w = 0; w < WTR; ++w) code[sr][w] = ld_at<uint32_t>(data, co + 4u * w);
+                        }
+                    } else {
+                        const float *factors = prw[sr] + g.factor;
+                        tx[sr] = factors[nsafe[sr]];
+                        fdq[sr] = factors[deg + nsafe[sr]];
+                        fvq[sr] = factors[2 * deg + nsafe[sr]];
+                        if constexpr (WT > 0)
+                            load_code<WT>(reinterpret_cast<const uint32_t *>(prw[sr] + g.code) +
+                                              static_cast<uint64_t>(nsafe[sr]) * WT,
+                                          vec_ok, code[sr]);
+                    }
                 }
 #pragma unroll
                 for (int sr = 0; sr < SR; ++sr)
@@ -1911,6 +1961,7 @@ struct fg_index {
     uint64_t code_offset = 0, factor_offset = 0, neighbor_offset = 0, row_offset = 0;
     int metric = FG_METRIC_L2;
     int dup_free = 0;
+    int runtime_geo = 0;  // FG_FORCE_RUNTIME_GEOMETRY at creation (a test knob)
     float *d_q = nullptr;
     size_t q_cap = 0;
     uint32_t *d_res = nullptr;
@@ -2042,6 +2093,8 @@ int make_params(fg_index *ix, uint32_t nq, uint32_t K, uint32_t beam, SearchPara
     P.use_ip = ix->metric == FG_METRIC_IP ? 1 : 0;
     P.dup_free = ix->dup_free;
     P.vec_ok = (ix->row_offset % 4 == 0 && ix->code_offset % 4 == 0) ? 1 : 0;
+    // the fixed-geometry kernels address rows with 32-bit byte offsets
+    P.runtime_geo = ix->runtime_geo || ix->npoints * ix->row_offset * 4ull > 0xFFFFFFFFull ? 1 : 0;
     P.entry = ix->entry;
     P.nq = static_cast<int>(nq);
     P.lds = lds_layout(ix->dim, ix->padded_dim, static_cast<uint32_t>(P.pbeam), static_cast<uint32_t>(P.buckets));
@@ -2061,17 +2114,19 @@ void launch_geo(const SearchParams &P, hipStream_t stream, bool count, bool prof
 }
 
 // Shape classes: the benchmark shapes (d 128 / deg 32; d 96 / deg 32 and 16)
-// get fully compile-time geometry; other shapes use runtime offsets.
+// get fully compile-time geometry while the codebook is under 4 GiB; other
+// shapes and larger codebooks use runtime offsets.
 template <bool PROF>
 int launch_t(const SearchParams &P, hipStream_t stream) {
     if (P.nq == 0) return FG_OK;
     const bool count = P.counters != nullptr;
     const int W = P.padded_dim / 32;
-    if (P.dim == 128 && P.degree == 32) {
+    const bool fixed = !P.runtime_geo;
+    if (fixed && P.dim == 128 && P.degree == 32) {
         launch_geo<4, 4, 128, 32>(P, stream, count, PROF);
-    } else if (P.dim == 96 && P.degree == 32) {
+    } else if (fixed && P.dim == 96 && P.degree == 32) {
         launch_geo<4, 3, 96, 32>(P, stream, count, PROF);
-    } else if (P.dim == 96 && P.degree == 16) {
+    } else if (fixed && P.dim == 96 && P.degree == 16) {
         launch_geo<4, 3, 96, 16>(P, stream, count, PROF);
     } else if (W == 2 && P.dim <= 64) {
         launch_geo<2, 2, 0, 0>(P, stream, count, PROF);
@@ -2134,6 +2189,10 @@ int fg_index_create(const float *rows, uint64_t npoints, uint32_t dim, uint32_t 
     }
     ix->entry = entry;
     ix->dup_free = rows_dup_free(rows, npoints, degree, ix->neighbor_offset, ix->row_offset) ? 1 : 0;
+    {
+        const char *env = std::getenv("FG_FORCE_RUNTIME_GEOMETRY");
+        ix->runtime_geo = env && env[0] == '1' ? 1 : 0;
+    }
     const size_t bytes = static_cast<size_t>(npoints) * ix->row_offset * sizeof(float);
     size_t free_b = 0, total_b = 0;
     if (hipGetDevice(&ix->device) != hipSuccess || hipMemGetInfo(&free_b, &total_b) != hipSuccess) {

@@ -74,6 +74,10 @@ typedef struct {
  * (include/common.hpp:26-47, gpu_search_adaptive.cu:74-77). */
 int fg_index_create(const float *rows, uint64_t npoints, uint32_t dim, uint32_t degree,
                     const float *signs, uint32_t entry, int metric, fg_index **out);
+/* (The search has kernels specialised for d = 128 / degree 32 and d = 96 /
+ * degree 32 or 16 while the codebook is under 4 GiB; an index created with
+ * the environment variable FG_FORCE_RUNTIME_GEOMETRY=1 uses the general
+ * kernels instead.  Same results; a test knob.) */
 
 /* Same as fg_index_create but reads the reference's codebook file
  * (include/qg.hpp:17-42); a truncated file is FG_EIO instead of being read

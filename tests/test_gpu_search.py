@@ -188,3 +188,23 @@ def test_search_stream_matches_single_launch(gpu_available, batch, nstreams):
     got = out.cpu()  # ordered after the batches on the caller's stream
     assert torch.equal(got, ref.cpu())
     ix.close()
+
+
+@pytest.mark.parametrize("dim,degree,kind", [(128, 32, "int"), (96, 32, "unit"), (96, 16, "unit")])
+def test_fixed_geometry_matches_runtime_geometry(gpu_available, dim, degree, kind, monkeypatch):
+    """The kernels specialised for the benchmark shapes (32-bit row offsets,
+    compile-time field offsets) return the same ids and work counters as the
+    general kernels, which codebooks of 4 GiB and more use (forced here with
+    FG_FORCE_RUNTIME_GEOMETRY)."""
+    from flashgann_amd import Index
+    cb, q, _ = small_index(n=2500, dim=dim, degree=degree, kind=kind, comps=16)
+    fixed = Index.from_codebook(cb)
+    monkeypatch.setenv("FG_FORCE_RUNTIME_GEOMETRY", "1")
+    general = Index.from_codebook(cb)
+    monkeypatch.delenv("FG_FORCE_RUNTIME_GEOMETRY")
+    for K, beam in [(10, 64), (100, 256)]:
+        a, _, ca = fixed.search(q, K, beam, counters=True)
+        b, _, cb_ = general.search(q, K, beam, counters=True)
+        assert np.array_equal(a, b) and np.array_equal(ca, cb_), (dim, degree, K, beam)
+    fixed.close()
+    general.close()
