@@ -208,3 +208,13 @@ def test_fixed_geometry_matches_runtime_geometry(gpu_available, dim, degree, kin
         assert np.array_equal(a, b) and np.array_equal(ca, cb_), (dim, degree, K, beam)
     fixed.close()
     general.close()
+
+
+@pytest.mark.parametrize("dim,degree", [(33, 32), (128, 1), (128, 2), (40, 8)])
+def test_search_shape_limits(gpu_available, dim, degree):
+    """The smallest dimension the layout allows (33: padded 64, two code words
+    per edge) and one- and two-neighbour graphs (a candidate buffer of 8 / 16,
+    stage-II keep rate 0)."""
+    cb, q, _ = small_index(n=800, nq=12, dim=dim, degree=degree, comps=8)
+    ids, cnt, rids, rcnt = _run(cb, q, 10, 64)
+    _assert_equal(ids, cnt, rids, rcnt, f"dim={dim} degree={degree}")
