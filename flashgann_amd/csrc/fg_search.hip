@@ -962,22 +962,6 @@ __device__ __forceinline__ uint32_t hash_insert(uint32_t *t, uint32_t nb, uint32
     return 0;
 }
 
-__device__ __forceinline__ bool hash_contains(const uint32_t *t, uint32_t nb, uint32_t key) {
-    const uint4 *t4 = reinterpret_cast<const uint4 *>(t);
-    const uint32_t bb = hash_alt(key, nb);
-    const uint4 sa = t4[hash_home(key, nb)], sb = t4[bb];
-    if (bucket_has(sa, key) || bucket_has(sb, key)) return true;
-    if (!both_full(sa, sb)) return false;
-    uint32_t b = hash_next(bb, nb);
-    for (uint32_t i = 0; i < nb; ++i) {
-        const uint4 sl = t4[b];
-        if (bucket_has(sl, key)) return true;
-        if (bucket_open(sl)) return false;
-        b = hash_next(b, nb);
-    }
-    return false;
-}
-
 __device__ __forceinline__ void hash_reset(uint32_t *t, uint32_t nb) {
     uint4 *t4 = reinterpret_cast<uint4 *>(t);
     const uint4 e = make_uint4(kMaxIndex, kMaxIndex, kMaxIndex, kMaxIndex);
@@ -1101,40 +1085,6 @@ __device__ __forceinline__ void raw_batch(const uint32_t (&c)[NB][WT], const uin
     }
 #pragma unroll
     for (int b = 0; b < NB; ++b) raw[b] = static_cast<int32_t>(acc[b]);
-}
-
-template <int WT>
-__device__ __forceinline__ void load_planes(const uint32_t *planes, uint32_t (&pl)[kPlanes + 1][WT]) {
-#pragma unroll
-    for (int p = 0; p <= kPlanes; ++p)
-#pragma unroll
-        for (int w = 0; w < WT; ++w) pl[p][w] = planes[p * WT + w];
-}
-
-// raw = sum_cb LUT[cb][nibble] from register-held planes (see raw_partial).
-template <int WT>
-__device__ __forceinline__ int32_t raw_regs(const uint32_t (&c)[WT], const uint32_t (&pl)[kPlanes + 1][WT],
-                                            bool any_wrap) {
-    uint32_t acc[kPlanes];
-#pragma unroll
-    for (int p = 0; p < kPlanes; ++p) acc[p] = 0;
-#pragma unroll
-    for (int w = 0; w < WT; ++w)
-#pragma unroll
-        for (int p = 0; p < kPlanes; ++p) acc[p] += __popc(c[w] & pl[p][w]);
-    uint32_t raw = 0;
-#pragma unroll
-    for (int p = 0; p < kPlanes; ++p) raw += acc[p] << p;
-    if (any_wrap) {
-        uint32_t wraps = 0;
-#pragma unroll
-        for (int w = 0; w < WT; ++w) {
-            const uint32_t x = c[w] & pl[kPlanes][w];
-            wraps += __popc(x & (x >> 1) & (x >> 2) & (x >> 3) & 0x11111111u);
-        }
-        raw -= 256u * wraps;
-    }
-    return static_cast<int32_t>(raw);
 }
 
 // One pass of exact distances over children e0 .. e0 + 2 PB - 1 (child
