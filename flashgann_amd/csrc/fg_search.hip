@@ -145,8 +145,8 @@ constexpr uint32_t kBeamPad = 4;
 // registers after preparation.
 __host__ __device__ constexpr bool query_in_lds(uint32_t padded_dim) { return padded_dim > 128u; }
 
-// Per-query LDS: visited table (aliased by the rotated query during
-// preparation), the beam, the 32-entry candidate buffer, the sorted-candidate
+// Per-query LDS: visited table and beam (aliased by the rotated query during
+// preparation), the 32-entry candidate buffer, the sorted-candidate
 // staging area, the raw query (aliased by the candidate buffer and staging
 // area when it is only read during set-up), 8 x B/32 plane words and a small
 // scratch area (32-entry child list + parent ids and distances).
@@ -172,8 +172,11 @@ __host__ __device__ constexpr LdsLayout lds_layout(uint32_t dim, uint32_t padded
     off += (32u + 2u * 8u) * 4u;
     off = (off + 15u) & ~15u;
     L.hash_off = off;
+    // during query preparation the rotated query (padded_dim floats) spans the
+    // visited table and the beam, which are initialised after it
     uint32_t hash_bytes = buckets * 16u;
-    if (hash_bytes < padded_dim * 4u) hash_bytes = padded_dim * 4u;
+    const uint32_t beam_bytes = (pbeam + 1u + kBeamPad) * 8u;
+    if (hash_bytes + beam_bytes < padded_dim * 4u) hash_bytes = (padded_dim * 4u - beam_bytes + 15u) & ~15u;
     off += hash_bytes;
     L.beam_off = off;
     off += (pbeam + 1u + kBeamPad) * 8u;
