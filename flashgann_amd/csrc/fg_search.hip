@@ -140,16 +140,13 @@ constexpr uint32_t kMsortPairs = 38;
 // slots are written to pbeam + 2).
 constexpr uint32_t kBeamPad = 4;
 
-// Whether the search keeps the raw query in LDS: only the generic kernel
-// (padded dim > 128) reads it there in the loop; the others hold it in
-// registers after preparation.
-__host__ __device__ constexpr bool query_in_lds(uint32_t padded_dim) { return padded_dim > 128u; }
 
 // Per-query LDS: visited table and beam (aliased by the rotated query during
 // preparation), the 32-entry candidate buffer, the sorted-candidate
-// staging area, the raw query (aliased by the candidate buffer and staging
-// area when it is only read during set-up), 8 x B/32 plane words and a small
-// scratch area (32-entry child list + parent ids and distances).
+// staging area (which, for d <= 128, also holds the raw query during set-up:
+// the loop keeps it in registers; a larger query is read from global memory,
+// where it stays cached), 8 x B/32 plane words and a small scratch area
+// (32-entry child list + parent ids and distances).
 __host__ __device__ constexpr LdsLayout lds_layout(uint32_t dim, uint32_t padded_dim, uint32_t pbeam,
                                                    uint32_t buckets) {
     // fixed-size regions first (compile-time offsets for a fixed geometry),
@@ -160,12 +157,8 @@ __host__ __device__ constexpr LdsLayout lds_layout(uint32_t dim, uint32_t padded
     off += 32u * 8u;
     L.msort_off = off;
     off += kMsortPairs * 8u;
-    if (query_in_lds(padded_dim)) {
-        L.query_off = off;
-        off += ((dim + 3u) & ~3u) * 4u;
-    } else {
-        L.query_off = 0;  // set-up only: d <= 128 floats fit in the 560 bytes above
-    }
+    L.query_off = 0;  // set-up only: d <= 128 floats fit in the 560 bytes above
+    (void)dim;
     L.plane_off = off;
     off += 8u * (padded_dim / 32u) * 4u;
     L.scratch_off = off;
@@ -1380,7 +1373,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
     float qlow, qhigh, qwidth;
     int sum_q;
     prepare_query(P.queries + static_cast<uint64_t>(qid) * g.dim, P.signs, g.dim, B, reinterpret_cast<float *>(H),
-                  qv, planes, qlow, qhigh, qwidth, sum_q, nullptr);
+                  WT == 0 ? nullptr : qv, planes, qlow, qhigh, qwidth, sum_q, nullptr);
+    // the generic geometry reads the query from global memory (it stays
+    // cached), the others keep it in registers (qr below)
+    const float *qsrc = WT == 0 ? P.queries + static_cast<uint64_t>(qid) * g.dim : qv;
     constexpr int WTR = WT > 0 ? WT : 1;
     // whether any chunk of the quantized query wraps the reference's uint8
     // LUT entry (then the estimates subtract the wrapped chunks)
@@ -1403,7 +1399,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
         qr[k] = (DPL > 0 && i < g.dim) ? qv[i] : 0.0f;
     }
 
-    const float entry_d = uni(half_distance(P.data + static_cast<uint64_t>(P.entry) * g.row, qv, g.dim, nl,
+    const float entry_d = uni(half_distance(P.data + static_cast<uint64_t>(P.entry) * g.row, qsrc, g.dim, nl,
                                             P.use_ip != 0, true));
     // the query's LDS copy may share the candidate and staging area: every
     // lane is done reading it before that area is initialised
@@ -1793,7 +1789,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
             cand_span = ex_n;  // compacted into slots 0 .. compact - 1
             FG_PHASE(7);
         }
-        exact_batch<DPL>(P, g, ex_n, ex_list, cd, ci, qr, qv);
+        exact_batch<DPL>(P, g, ex_n, ex_list, cd, ci, qr, qsrc);
         if (theta <= 1) FG_PHASE(5);
         else FG_PHASE(8);
         __syncthreads();
