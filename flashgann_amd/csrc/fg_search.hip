@@ -462,6 +462,16 @@ __device__ void prepare_query(const float *__restrict__ query, const float *__re
     __syncthreads();
 }
 
+// popcount(x) + acc as one v_bcnt_u32_b32.  Written as an instruction so a
+// chain of them stays a chain: as plain additions the compiler splits it into
+// popcounts from zero joined by three-input adds, two more instructions per
+// plane and code block.
+__device__ __forceinline__ uint32_t bcnt_acc(uint32_t x, uint32_t acc) {
+    uint32_t r;
+    asm("v_bcnt_u32_b32 %0, %1, %2" : "=v"(r) : "v"(x), "v"(acc));
+    return r;
+}
+
 // raw = sum_cb LUT[cb][nibble] (utils.cuh:976-980) over code words [w0, w1).
 __device__ __forceinline__ int32_t raw_partial(const uint32_t *__restrict__ code, int w0, int w1,
                                                const uint32_t *planes, int W) {
@@ -489,9 +499,7 @@ __device__ __forceinline__ int32_t raw_partial(const uint32_t *__restrict__ code
 // come from LDS as 16-byte reads.
 __device__ __forceinline__ int32_t raw_words(const uint32_t *__restrict__ code, const uint32_t *planes, int W,
                                              bool vec_ok, bool any_wrap) {
-    uint32_t acc[kPlanes];
-#pragma unroll
-    for (int p = 0; p < kPlanes; ++p) acc[p] = 0;
+    uint32_t raw = 0;
     uint32_t wraps = 0;
     const int nb = W < 32 ? W : 32;  // words per batch: 8, 16 or 32
     for (int w0 = 0; w0 < W; w0 += nb) {
@@ -506,18 +514,26 @@ __device__ __forceinline__ int32_t raw_words(const uint32_t *__restrict__ code, 
 #pragma unroll
             for (int j = 0; j < 32; ++j) c[j] = j < nb ? code[w0 + j] : 0u;
         }
+        // this batch's sum_p 2^p popcount(c & plane_p), top plane first
+        // (Horner's rule, one accumulate chain)
+        uint32_t hb = 0;
 #pragma unroll
-        for (int p = 0; p < kPlanes; ++p) {
+        for (int p = kPlanes - 1; p >= 0; --p) {
             const uint4 *pl = reinterpret_cast<const uint4 *>(planes + p * W + w0);
+            uint32_t a = hb << 1;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 if (j * 4 < nb) {
                     const uint4 q = pl[j];
-                    acc[p] += __popc(c[4 * j] & q.x) + __popc(c[4 * j + 1] & q.y) + __popc(c[4 * j + 2] & q.z) +
-                              __popc(c[4 * j + 3] & q.w);
+                    a = bcnt_acc(c[4 * j] & q.x, a);
+                    a = bcnt_acc(c[4 * j + 1] & q.y, a);
+                    a = bcnt_acc(c[4 * j + 2] & q.z, a);
+                    a = bcnt_acc(c[4 * j + 3] & q.w, a);
                 }
             }
+            hb = a;
         }
+        raw += hb;
         if (any_wrap) {
             const uint32_t *wp = planes + kPlanes * W + w0;
 #pragma unroll
@@ -529,9 +545,6 @@ __device__ __forceinline__ int32_t raw_words(const uint32_t *__restrict__ code, 
             }
         }
     }
-    uint32_t raw = 0;
-#pragma unroll
-    for (int p = 0; p < kPlanes; ++p) raw += acc[p] << p;
     return static_cast<int32_t>(raw - 256u * wraps);
 }
 
@@ -1042,9 +1055,20 @@ __device__ __forceinline__ void load_code(const uint32_t *__restrict__ code, boo
     for (int w = 0; w < WT; ++w) c[w] = code[w];
 }
 
+// Horner step over the planes of WT words: 2 acc + sum_w popcount(c_w & pw_w)
+// (the top plane starts from zero).
+template <int WT>
+__device__ __forceinline__ uint32_t plane_step(const uint32_t *c, const uint32_t *pw, uint32_t acc, bool top) {
+    uint32_t a = top ? static_cast<uint32_t>(__popc(c[0] & pw[0])) : bcnt_acc(c[0] & pw[0], acc << 1);
+#pragma unroll
+    for (int w = 1; w < WT; ++w) a = bcnt_acc(c[w] & pw[w], a);
+    return a;
+}
+
 // raw for NB code blocks at once, walking the planes one at a time from LDS
-// (one plane's WT words live at a time): raw_b = sum_p 2^p popcount(code_b &
-// plane_p) - 256 * wraps_b.
+// (one plane's WT words live at a time), top plane first: raw_b = sum_p 2^p
+// popcount(code_b & plane_p) - 256 * wraps_b, the powers of two by Horner's
+// rule (one shift per plane and block).
 template <int NB, int WT>
 __device__ __forceinline__ void raw_batch(const uint32_t (&c)[NB][WT], const uint32_t *planes, bool any_wrap,
                                           int32_t (&raw)[NB]) {
@@ -1052,17 +1076,12 @@ __device__ __forceinline__ void raw_batch(const uint32_t (&c)[NB][WT], const uin
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[b] = 0;
 #pragma unroll
-    for (int p = 0; p < kPlanes; ++p) {
+    for (int p = kPlanes - 1; p >= 0; --p) {
         uint32_t pw[WT];
 #pragma unroll
         for (int w = 0; w < WT; ++w) pw[w] = planes[p * WT + w];
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            uint32_t t = 0;
-#pragma unroll
-            for (int w = 0; w < WT; ++w) t += __popc(c[b][w] & pw[w]);
-            acc[b] += t << p;
-        }
+        for (int b = 0; b < NB; ++b) acc[b] = plane_step<WT>(c[b], pw, acc[b], p == kPlanes - 1);
     }
     if (any_wrap) {
         uint32_t pw[WT];
