@@ -2026,6 +2026,12 @@ int make_params(fg_index *ix, uint32_t nq, uint32_t K, uint32_t beam, SearchPara
     if (K < 1) return fail(FG_EINVAL, "K must be >= 1");
     if (beam < 1 || beam > static_cast<uint32_t>(kMaxBeam))
         return fail(FG_EINVAL, "beam must be in [1, 1024]");
+    if (nq > static_cast<uint32_t>(INT32_MAX)) return fail(FG_EINVAL, "nq must be at most 2^31 - 1 (one workgroup per query)");
+    int cur = -1;
+    FG_HIP(hipGetDevice(&cur), "current device");
+    if (cur != ix->device)
+        return fail(FG_EINVAL, "the index lives on device " + std::to_string(ix->device) + " but device " +
+                                   std::to_string(cur) + " is current");
     P.data = ix->d_rows;
     P.signs = ix->d_signs;
     P.npoints = ix->npoints;

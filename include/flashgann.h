@@ -16,6 +16,12 @@
  *
  * Every function returns 0 on success and a negative FG_E* code on failure;
  * fg_last_error() then describes the failure (thread-local string).
+ *
+ * An index lives on the device that was current when it was created, and its
+ * searches must be called with that device current (FG_EINVAL otherwise).
+ * fg_search keeps its staging buffers in the index: calls on one index come
+ * from one host thread at a time; different indices are independent.  One
+ * search covers at most 2^31 - 1 queries (one workgroup each).
  */
 #ifndef FLASHGANN_H
 #define FLASHGANN_H

@@ -88,6 +88,26 @@ def test_empty_batch(gpu_available):
     ix.close()
 
 
+def test_oversized_batch_rejected(gpu_available):
+    """nq above 2^31 - 1 is FG_EINVAL before any launch (one workgroup per
+    query; the grid size is a signed 32-bit count), on every search entry."""
+    import ctypes as C
+    import torch
+    from flashgann_amd import Index, _lib
+    cb, q, _ = small_index()
+    ix = Index.from_codebook(cb)
+    res = torch.full((4, 10), 7, dtype=torch.int32, device="cuda")
+    dq = torch.as_tensor(q[:4], device="cuda")
+    L = _lib.lib()
+    qp, rp = C.c_void_p(dq.data_ptr()), C.c_void_p(res.data_ptr())
+    assert L.fg_search_device(ix._h, qp, 2 ** 31, 10, 64, rp, None, None) == -1
+    assert b"2^31" in L.fg_last_error()
+    assert L.fg_search_stream(ix._h, qp, 2 ** 31, 10, 64, rp, 2 ** 31, 2, None) == -1
+    torch.cuda.synchronize()
+    assert (res.cpu() == 7).all()
+    ix.close()
+
+
 def test_search_entry_auto(gpu_available):
     from flashgann_amd import Index
     from oracle import oracle as O
