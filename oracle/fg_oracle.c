@@ -32,9 +32,17 @@
  *   whole search                 recall vs brute-force ground truth, plus
  *                                internal invariants (sorted beam, unique
  *                                expansions, counters)
- * The speculative-round visibility rule and the fp-contraction sites cannot be
- * pinned without running the reference (no CUDA toolchain here): they are the
- * oracle's stated choices, recorded as "parity unpinned" in the design notes.
+ * Parity unpinned -- these cannot be pinned without running the reference
+ * (no CUDA toolchain here), so they are the oracle's stated choices:
+ *   - the fp-contraction sites (fmaf exactly where nvcc's default --fmad=true
+ *     would contract; every other operation unfused);
+ *   - the speculative round's visibility rule (every task of a round sees the
+ *     visited set as it stood at the round's start; inserts resolve in
+ *     (task, lane) order) and theta = 1 duplicates resolving by slot order;
+ *   - a query whose rotated vector is constant (width == 0): the reference
+ *     computes lroundf(NaN); here every level is 0;
+ *   - the codebook factors, whose builder (SymphonyQG) is not in the
+ *     reference: the search only consumes them.
  */
 #include "fg_oracle.h"
 
