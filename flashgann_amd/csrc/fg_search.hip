@@ -771,11 +771,23 @@ __device__ __forceinline__ void small_merge(int pbeam, uint2 *bp, const uint2 *m
 // binary search (utils.cuh:588-616); inside a segment beam entries go first
 // on ties (utils.cuh:652-671).  Lane l owns segments l*SPL .. l*SPL+SPL-1.
 // It searches its right boundaries; the left one is its neighbour's.  The
-// search reads the sentinel-padded arrays, so no bound needs a branch:
+// searches read the sentinel-padded arrays, so no bound needs a branch:
 // bp[-1], ms[-1] = -FLT_MAX and bp[pbeam], ms[32] = FLT_MAX stand for the
 // reference's out-of-range values.
+//
+// The splits valid at a diagonal d (i beam entries and d - i candidates,
+// with beam[i-1] <= cand[d-i] and cand[d-i-1] <= beam[i]) form an interval
+// [L, R], and R - 1 is valid only if beam[R-1] and cand[d-R] have equal keys.
+// When no boundary has such a pair the split is unique, and the reference's
+// bisection, which returns some valid split, returns R: then R is found by a
+// plain binary search for the last i with beam[i-1] <= cand[d-i] (steps of
+// 32 .. 1 over at most 33 values).  An equal pair at the key FLT_MAX is two
+// empty (FLT_MAX, MAX_INDEX) entries when `fast_ok` (no other pair with a key
+// outside (-FLT_MAX, FLT_MAX) has been merged into this beam), and every
+// split of such a tie gives the same output.  Any other equal pair sends the
+// whole wave through the reference's bisection, replayed step by step.
 template <int SPL>
-__device__ __forceinline__ void merge_path(const SearchParams &P, uint2 *bp, const uint2 *ms) {
+__device__ __forceinline__ void merge_path(const SearchParams &P, uint2 *bp, const uint2 *ms, bool fast_ok) {
     const int lane = lane_id_opaque();
     const int cbs = P.cbs, pbeam = P.pbeam, active = P.seg_active;
     const int t0 = lane * SPL;
@@ -787,38 +799,73 @@ __device__ __forceinline__ void merge_path(const SearchParams &P, uint2 *bp, con
         const int t = min(t0 + k, active);
         dg[k] = static_cast<int>(__umulhi(static_cast<uint32_t>(t * pbeam), P.seg_magic));
     }
-    int lo[SPL], hi[SPL];
-    bool done[SPL];
-#pragma unroll
-    for (int k = 0; k < SPL; ++k) {
-        lo[k] = max(dg[k + 1] - cbs, 0);
-        hi[k] = min(dg[k + 1], pbeam);
-        done[k] = t0 + k + 1 > active;
-        res[k + 1] = 0;
-    }
-    for (;;) {
-        bool live = false;
+    bool replay = !fast_ok;
+    if (fast_ok) {
+        // pos holds a split with beam[pos-1] <= cand[d-pos] (true at lo0);
+        // steps of 32, 16, .. 1 move it to the last such split up to hi,
+        // testing min(pos + s, hi) so that every read stays in range
+        int pos[SPL], hi[SPL], lo0[SPL], dd[SPL];
 #pragma unroll
         for (int k = 0; k < SPL; ++k) {
-            // branch-free round: all four values are read (one LDS round
-            // trip, two ds_read2), then the reference's if / else-if / else
-            // picks the update
-            const bool exit_low = !done[k] && lo[k] > hi[k];  // loop exit: return low
-            res[k + 1] = exit_low ? lo[k] : res[k + 1];
-            done[k] = done[k] || exit_low;
-            const int ai = done[k] ? 0 : (lo[k] + hi[k]) >> 1;
-            const int bj = done[k] ? 0 : dg[k + 1] - ai;
-            const float al = bk[2 * ai - 2], ar = bk[2 * ai];
-            const float bl = mk[2 * bj - 2], br = mk[2 * bj];
-            const bool go_left = al > br, go_right = !go_left && bl > ar;
-            const bool found = !done[k] && !go_left && !go_right;
-            hi[k] = (!done[k] && go_left) ? ai - 1 : hi[k];
-            lo[k] = (!done[k] && go_right) ? ai + 1 : lo[k];
-            res[k + 1] = found ? ai : res[k + 1];
-            done[k] = done[k] || found;
-            live |= !done[k];
+            const bool act = t0 + k + 1 <= active;
+            dd[k] = act ? dg[k + 1] : 0;
+            lo0[k] = max(dd[k] - cbs, 0);
+            hi[k] = min(dd[k], pbeam);
+            pos[k] = lo0[k];
         }
-        if (!any_lane(live)) break;
+#pragma unroll
+        for (int st = 32; st >= 1; st >>= 1) {
+#pragma unroll
+            for (int k = 0; k < SPL; ++k) {
+                const int c = min(pos[k] + st, hi[k]);
+                pos[k] = bk[2 * c - 2] <= mk[2 * (dd[k] - c)] ? c : pos[k];
+            }
+        }
+        bool tie = false;
+#pragma unroll
+        for (int k = 0; k < SPL; ++k) {
+            const int r = pos[k];
+            const bool below = r > lo0[k];  // then beam[r-1] and cand[d-r] both exist
+            const float a = bk[2 * (below ? r : 1) - 2], b = mk[2 * (below ? dd[k] - r : 0)];
+            tie |= below && a == b && a != FLT_MAX;
+            res[k + 1] = r;
+        }
+        replay = any_lane(tie);
+    }
+    if (replay) {
+        int lo[SPL], hi[SPL];
+        bool done[SPL];
+#pragma unroll
+        for (int k = 0; k < SPL; ++k) {
+            lo[k] = max(dg[k + 1] - cbs, 0);
+            hi[k] = min(dg[k + 1], pbeam);
+            done[k] = t0 + k + 1 > active;
+            res[k + 1] = 0;
+        }
+        for (;;) {
+            bool live = false;
+#pragma unroll
+            for (int k = 0; k < SPL; ++k) {
+                // branch-free round: all four values are read (one LDS round
+                // trip, two ds_read2), then the reference's if / else-if / else
+                // picks the update
+                const bool exit_low = !done[k] && lo[k] > hi[k];  // loop exit: return low
+                res[k + 1] = exit_low ? lo[k] : res[k + 1];
+                done[k] = done[k] || exit_low;
+                const int ai = done[k] ? 0 : (lo[k] + hi[k]) >> 1;
+                const int bj = done[k] ? 0 : dg[k + 1] - ai;
+                const float al = bk[2 * ai - 2], ar = bk[2 * ai];
+                const float bl = mk[2 * bj - 2], br = mk[2 * bj];
+                const bool go_left = al > br, go_right = !go_left && bl > ar;
+                const bool found = !done[k] && !go_left && !go_right;
+                hi[k] = (!done[k] && go_left) ? ai - 1 : hi[k];
+                lo[k] = (!done[k] && go_right) ? ai + 1 : lo[k];
+                res[k + 1] = found ? ai : res[k + 1];
+                done[k] = done[k] || found;
+                live |= !done[k];
+            }
+            if (!any_lane(live)) break;
+        }
     }
     res[0] = __builtin_amdgcn_update_dpp(0, res[SPL], 0x138, 0xF, 0xF, false);  // DPP wave_shr:1; lane 0 reads 0
     if (lane == 0) res[0] = 0;
@@ -867,14 +914,18 @@ __device__ __forceinline__ void merge_path(const SearchParams &P, uint2 *bp, con
 // candidates are sorted (warp_sort<1>), staged in `ms`, and merged into the
 // beam in place.  `span`: slots at or past it hold (FLT_MAX, MAX_INDEX), so a
 // candidate buffer filled only in its first 8 or 16 slots is sorted with the
-// stages that reach that block size (sort32<TOP>).
+// stages that reach that block size (sort32<TOP>).  `fast_ok` stays true while
+// every pair merged into this beam has a key in (-FLT_MAX, FLT_MAX) or is the
+// empty (FLT_MAX, MAX_INDEX) pair (merge_path's condition for its split
+// search).
 __device__ __forceinline__ void merge_beam(const SearchParams &P, uint2 *bp, uint2 *ms, const float *cd,
-                                           const uint32_t *ci, int span) {
+                                           const uint32_t *ci, int span, bool &fast_ok) {
     const int lane = lane_id_opaque();
     const int nl = lane & 31, h = lane >> 5;
     const int cbs = P.cbs, pbeam = P.pbeam;
     float ck = nl < cbs ? cd[nl] : FLT_MAX;
     uint32_t cv = nl < cbs ? ci[nl] : kMaxIndex;
+    fast_ok = fast_ok && !any_lane(!((ck > -FLT_MAX && ck < FLT_MAX) || (ck == FLT_MAX && cv == kMaxIndex)));
     // every key of the span at most FLT_MAX (never inf or NaN)
     const bool short_ok = !any_lane(nl < span && !(ck <= FLT_MAX));
     if (short_ok && span <= 8) sort32<8>(ck, cv);
@@ -890,9 +941,9 @@ __device__ __forceinline__ void merge_beam(const SearchParams &P, uint2 *bp, uin
         small_merge<1, true>(pbeam, bp, ms, nl, h == 0);
     } else {
         const int spl = (P.seg_active + 63) / 64;
-        if (spl == 1) merge_path<1>(P, bp, ms);
-        else if (spl == 2) merge_path<2>(P, bp, ms);
-        else merge_path<4>(P, bp, ms);
+        if (spl == 1) merge_path<1>(P, bp, ms, fast_ok);
+        else if (spl == 2) merge_path<2>(P, bp, ms, fast_ok);
+        else merge_path<4>(P, bp, ms, fast_ok);
     }
     __syncthreads();
 }
@@ -1449,6 +1500,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
     // candidate slots the next merge may find filled (the rest hold the
     // reset pair): the entry point's slot 0 first, then what each stage fills
     int cand_span = 1;
+    bool split_fast = true;  // merge_path may search its splits directly
     const float *data = P.data;
 
     FG_PHASE(0);
@@ -1468,7 +1520,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
         // adaptive_search.cuh:447-451).  A search that stops because no beam entry is left to
         // expand has merged them already: its final merge sees an empty
         // candidate buffer and leaves the beam as it is.
-        merge_beam(P, bp, ms, cd, ci, cand_span);
+        merge_beam(P, bp, ms, cd, ci, cand_span, split_fast);
         FG_PHASE(2);
         if (iter >= P.max_iter) break;
         for (int i = beam_sz + lane; i < pbeam; i += 64) bp[i] = kEmpty;

@@ -300,3 +300,80 @@ def test_short_candidate_sort_equals_full_network(top):
     O.lib().fgo_bitonic_sort(O.ptr(k1, C.c_float), O.ptr(v1, C.c_uint32), 32)
     O.lib().fgo_bitonic_sort(O.ptr(k2, C.c_float), O.ptr(v2, C.c_uint32), top)
     assert not (np.array_equal(k1, k2) and np.array_equal(v1, v2))
+
+
+def _direct_split(a, b, d):
+    """The kernel's direct split search (fg_search.hip merge_path): the last
+    i in [max(d - nb, 0), min(d, na)] with a[i-1] <= b[d-i], by steps of
+    32 .. 1 that test min(pos + step, hi), and whether the boundary pair
+    a[r-1], b[d-r] ties below FLT_MAX."""
+    na, nb = len(a), len(b)
+    fa = lambda i: -FLT_MAX if i < 0 else (FLT_MAX if i >= na else a[i])
+    fb = lambda j: -FLT_MAX if j < 0 else (FLT_MAX if j >= nb else b[j])
+    lo0, hi = max(d - nb, 0), min(d, na)
+    pos = lo0
+    for step in (32, 16, 8, 4, 2, 1):
+        c = min(pos + step, hi)
+        assert -1 <= c - 1 < na and 0 <= d - c <= nb  # reads stay in range
+        if fa(c - 1) <= fb(d - c):
+            pos = c
+    tie = pos > lo0 and fa(pos - 1) == fb(d - pos) and fa(pos - 1) != FLT_MAX
+    return pos, tie
+
+
+def _segmented_merge(ak, av, bk, bv, split):
+    """topk_candidate_sort_and_merge's output loop (utils.cuh:618-680) with the
+    reference block's segmentation, the split of each boundary from `split`."""
+    pbeam = len(ak)
+    active = min(256, ((pbeam + 3) // 4 + 31) // 32 * 32)
+    ok, ov = [], []
+    for t in range(active):
+        ob, oe = min(pbeam, t * pbeam // active), min(pbeam, (t + 1) * pbeam // active)
+        tb, te = split(ob), split(oe)
+        ti, ci, ce = tb, ob - tb, oe - te
+        for _ in range(ob, oe):
+            if ci >= ce or (ti < te and ak[ti] <= bk[ci]):
+                ok.append(ak[ti]); ov.append(av[ti]); ti += 1
+            else:
+                ok.append(bk[ci]); ov.append(bv[ci]); ci += 1
+    return ok, ov
+
+
+@pytest.mark.parametrize("pbeam", [256, 512, 1024])
+def test_direct_split_search_equals_bisection(pbeam):
+    """The kernel finds merge-path splits by a direct binary search and replays
+    the reference's bisection only when a boundary pair ties below FLT_MAX.
+    Without such a tie the merged beam must equal the reference's
+    (fgo_merge_path_partition, the bisection of utils.cuh:588-616) -- also when
+    empty (FLT_MAX, MAX_INDEX) entries tie, where the split index may differ.
+    With ties the split can differ, so the guard is not vacuous."""
+    rng = np.random.default_rng(pbeam)
+    L = O.lib()
+    fmax = float(FLT_MAX)
+    clean = differ_when_tied = 0
+    for case in range(120):
+        span = [3, 40, 5000, 100000][case % 4]  # key range: heavy, some, few ties
+        nfill = int(rng.integers(0, pbeam + 1))
+        ak = np.full(pbeam, fmax, np.float32)
+        av = np.full(pbeam, MAXI, np.uint32)
+        ak[:nfill] = np.sort(rng.integers(0, span, nfill)).astype(np.float32)
+        av[:nfill] = rng.permutation(1 << 20)[:nfill]
+        nc = int(rng.integers(0, 33))
+        bk = np.full(32, fmax, np.float32)
+        bv = np.full(32, MAXI, np.uint32)
+        bk[:nc] = np.sort(rng.integers(0, span, nc)).astype(np.float32)
+        bv[:nc] = (1 << 21) + rng.permutation(1 << 20)[:nc]
+        ref = lambda d: L.fgo_merge_path_partition(O.ptr(ak, C.c_float), pbeam, O.ptr(bk, C.c_float), 32, d)
+        active = min(256, ((pbeam + 3) // 4 + 31) // 32 * 32)
+        bounds = [min(pbeam, t * pbeam // active) for t in range(1, active + 1)]
+        fast = {d: _direct_split(list(ak), list(bk), d) for d in bounds}
+        tied = any(t for _, t in fast.values())
+        got = _segmented_merge(list(ak), list(av), list(bk), list(bv),
+                               lambda d: 0 if d == 0 else fast[d][0])
+        want = _segmented_merge(list(ak), list(av), list(bk), list(bv), ref)
+        if not tied:
+            clean += 1
+            assert got == want, (case, pbeam)
+        elif got != want:
+            differ_when_tied += 1
+    assert clean > 30 and differ_when_tied > 0, (clean, differ_when_tied)
