@@ -393,6 +393,15 @@ __device__ __forceinline__ float uni(float v) {
 
 __device__ __forceinline__ bool finite_below_max(float x) { return isfinite(x) && x < FLT_MAX; }
 
+// An exact distance as a beam key: NaN and values beyond +-FLT_MAX (from an
+// overflowing or NaN vector) become +-FLT_MAX (NaN: FLT_MAX).  The merge-path
+// partition stands -FLT_MAX / FLT_MAX in for positions before / past the
+// arrays (utils.cuh:600-603); a key outside that range, or unordered, sends
+// the partition past the arrays, so keys are kept within it.
+__device__ __forceinline__ float beam_key(float d) {
+    return d != d ? FLT_MAX : (d > FLT_MAX ? FLT_MAX : (d < -FLT_MAX ? -FLT_MAX : d));
+}
+
 // ------------------------------------------------------------ query preparation
 
 // utils.cuh:790-939 for one wave: rotate (x*signs, pad, FWHT len = 1..B/2 with
@@ -651,7 +660,7 @@ __device__ __forceinline__ void exact_generic_pass(const SearchParams &P, uint64
         const int e = e0 + 2 * j + h;
         if (e < n && nl == 0) {
             const int slot = static_cast<int>(slot_list ? slot_list[e] : static_cast<uint32_t>(e));
-            cd[slot] = ip ? -r : r;
+            cd[slot] = beam_key(ip ? -r : r);
         }
     }
 }
@@ -882,8 +891,14 @@ __device__ __forceinline__ void merge_path(const SearchParams &P, uint2 *bp, con
         const bool act = t0 + k < active;
         const int tb = act ? res[k] : 0;
         const int cb = act ? dg[k] - res[k] : 0;
-        const int na = act ? res[k + 1] - res[k] : 0;
         nsl[k] = act ? dg[k + 1] - dg[k] : 0;
+        // The bisection resolves equal keys at each boundary on its own, so
+        // two boundaries can disagree (seen at the first merge, where every
+        // entry is the empty pair): more than nsl beam entries, or fewer
+        // than none.  The reference's output loop then takes only beam
+        // entries, or only candidates from cb on (utils.cuh:660-671), which is
+        // what the count clamped to [0, nsl] gives.
+        const int na = act ? min(max(res[k + 1] - res[k], 0), nsl[k]) : 0;
         bool ina[4];
 #pragma unroll
         for (int s2 = 0; s2 < 4; ++s2) {
@@ -1277,7 +1292,7 @@ __device__ __forceinline__ void exact_pass(const SearchParams &P, const G &g, in
     const int e = e0 + 2 * c + h;
     if (e < n && (nl & (kGroup - 1)) == 0) {
         const int sl = slot_list ? static_cast<int>(slot_list[e] & 31u) : e;
-        cd[sl] = ip ? -r4 : r4;
+        cd[sl] = beam_key(ip ? -r4 : r4);
     }
 }
 
@@ -1469,8 +1484,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
         qr[k] = (DPL > 0 && i < g.dim) ? qv[i] : 0.0f;
     }
 
-    const float entry_d = uni(half_distance(P.data + static_cast<uint64_t>(P.entry) * g.row, qsrc, g.dim, nl,
-                                            P.use_ip != 0, true));
+    const float entry_d = uni(beam_key(half_distance(P.data + static_cast<uint64_t>(P.entry) * g.row, qsrc, g.dim,
+                                                     nl, P.use_ip != 0, true)));
     // the query's LDS copy may share the candidate and staging area: every
     // lane is done reading it before that area is initialised
     __syncthreads();

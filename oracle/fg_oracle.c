@@ -292,10 +292,20 @@ float fgo_scalar_ip(int dim, const float *a, const float *b) {
     return -sum;
 }
 
+/* An exact distance as a beam key.  The reference's merge-path partition
+ * stands -FLT_MAX / FLT_MAX in for positions before / past the arrays
+ * (utils.cuh:600-603): a key beyond that range (an overflowing vector) or
+ * unordered (NaN) sends the partition past the arrays there, which reads
+ * out of bounds.  Both implementations here clamp instead (NaN to FLT_MAX):
+ * parity unpinned for such inputs, identical to the reference otherwise. */
+static inline float beam_key(float d) {
+    return d != d ? FLT_MAX : (d > FLT_MAX ? FLT_MAX : (d < -FLT_MAX ? -FLT_MAX : d));
+}
+
 static inline float index_distance(const fgo_index *ix, const float *query, uint32_t node) {
     const float *row = ix->data + (uint64_t)node * ix->lay.row_offset;
-    return ix->use_ip ? fgo_warp_ip((int)ix->lay.dim, query, row)
-                      : fgo_warp_l2((int)ix->lay.dim, query, row);
+    return beam_key(ix->use_ip ? fgo_warp_ip((int)ix->lay.dim, query, row)
+                               : fgo_warp_l2((int)ix->lay.dim, query, row));
 }
 
 /* ---------------------------------------------------------------- networks */
@@ -308,17 +318,36 @@ static inline void cex(float *k, uint32_t *v, uint32_t lo, uint32_t hi, int asc)
     }
 }
 
+/* Cross-lane compare-exchange, utils.cuh:309-316: each of the two lanes
+ * decides for itself whether to take its partner's pair, the lower one with
+ * p = asc, the upper one with p = !asc.  For ordered keys that is one swap;
+ * with a NaN key both tests are false on one side only, so one pair is
+ * duplicated and the other dropped, as on the device. */
+static inline void cex_lanes(float *k, uint32_t *v, uint32_t lo, uint32_t hi, int asc) {
+    const float a = k[lo], b = k[hi];
+    const uint32_t va = v[lo], vb = v[hi];
+    const int take_lo = a != b && ((a < b) != (asc != 0));
+    const int take_hi = b != a && ((b < a) != (asc == 0));
+    if (take_lo) { k[lo] = b; v[lo] = vb; }
+    if (take_hi) { k[hi] = a; v[hi] = va; }
+}
+
 /* One stage (block size kk) of the bitonic network.  utils.cuh:330-414 with N
  * items per lane in the blocked layout (position = N*lane + i): warp_merge at
  * range r is exactly this stage with kk = N*r (kk = 2..N for range 1), all
  * compare-exchanges at distance j = kk/2 .. 1, ascending iff (pos & kk) == 0
  * at the lower position. */
 void fgo_bitonic_stage(float *keys, uint32_t *vals, uint32_t n, uint32_t kk) {
+    /* n positions over 32 lanes, n / 32 per lane (one for n <= 32): a
+     * distance below that stays inside a lane (utils.cuh:319-328, one
+     * symmetric swap), a larger one crosses lanes */
+    const uint32_t per_lane = n > 32 ? n / 32 : 1;
     for (uint32_t j = kk >> 1; j >= 1; j >>= 1)
         for (uint32_t lo = 0; lo < n; ++lo) {
             const uint32_t hi = lo ^ j;
             if (hi <= lo || hi >= n) continue;
-            cex(keys, vals, lo, hi, (lo & kk) == 0);
+            if (j < per_lane) cex(keys, vals, lo, hi, (lo & kk) == 0);
+            else cex_lanes(keys, vals, lo, hi, (lo & kk) == 0);
         }
 }
 

@@ -72,6 +72,27 @@ def test_search_dim1536(gpu_available):
     _assert_equal(ids, cnt, rids, rcnt, "aniso1536 beam 32")
 
 
+@pytest.mark.parametrize("bad", ["inf", "nan"])
+def test_search_non_finite_distances(gpu_available, bad):
+    """One row in twenty gets a vector that overflows (1e30: exact distances
+    are inf) or is NaN, after the graph and codes were built from the real
+    data, so estimates stay finite while such children's exact distances
+    enter the candidate buffer and the beam as non-finite keys.  The merges
+    then take the reference's bisection and full candidate network, and ids
+    and counters must still equal the oracle's."""
+    import dataclasses
+    cb, q, _ = small_index()
+    rows = cb.rows.copy()
+    rng = np.random.default_rng(7)
+    pick = rng.choice(cb.npoints, cb.npoints // 20, replace=False)
+    pick = pick[pick != cb.entry]
+    rows[pick, :cb.layout.dim] = np.float32(1e30) if bad == "inf" else np.float32(np.nan)
+    cb2 = dataclasses.replace(cb, rows=rows)
+    for beam in (64, 256, 512):
+        ids, cnt, rids, rcnt = _run(cb2, q, 100, beam)
+        _assert_equal(ids, cnt, rids, rcnt, f"{bad} beam {beam}")
+
+
 def test_empty_batch(gpu_available):
     """nq = 0 is a no-op through both entry points (no launch, outputs untouched)."""
     import torch
