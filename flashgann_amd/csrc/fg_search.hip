@@ -1407,8 +1407,9 @@ __device__ __forceinline__ void hash_contains_n(const uint32_t *t, uint32_t nb, 
     } while (0)
 
 // One wave per workgroup; the register budget targets 5 waves per SIMD
-// (<= 96 VGPRs), which LDS also allows for beams up to 256 (21 workgroups per
-// CU at 6,960 bytes).  The generic-geometry instantiation (padded dimension
+// (<= 96 VGPRs; the fixed-geometry kernels use 77-79, which leaves room for
+// a sixth), which LDS also allows for beams up to 256 (6,400 bytes a
+// workgroup at beam 256).  The generic-geometry instantiation (padded dimension
 // >= 256) gets 4 (<= 128 VGPRs) for its wider load batches: at padded
 // dimension 1024 and up its LDS (raw query, planes, rotation scratch) holds
 // it to fewer waves than that anyway.
