@@ -274,13 +274,26 @@ def build_codebook(base: np.ndarray, degree: int, signs: np.ndarray, use_ip: boo
                    alpha: float = 1.0, candidates: int | None = None, fill_random: bool = True,
                    store_entry: bool = True, verbose: bool = False) -> Codebook:
     """Builds a complete codebook in the reference layout."""
+    x = torch.as_tensor(np.ascontiguousarray(base, dtype=np.float32), device=device)
+    nbrs = build_graph(x, degree, random_links=random_links, alpha=alpha, candidates=candidates,
+                       fill_random=fill_random, verbose=verbose)
+    return codebook_from_graph(base, nbrs, signs, use_ip=use_ip, device=device, store_entry=store_entry)
+
+
+def codebook_from_graph(base: np.ndarray, nbrs, signs: np.ndarray, use_ip: bool = False,
+                        device: str | torch.device = "cpu", store_entry: bool = True,
+                        entry: int | None = None) -> Codebook:
+    """Encodes a given graph ((n, degree) neighbour ids, -1 = padding) into a
+    codebook in the reference layout.  `entry` overrides the stored entry
+    point (default: the node nearest the mean)."""
     n, dim = base.shape
+    nbrs = torch.as_tensor(np.asarray(nbrs) if not isinstance(nbrs, torch.Tensor) else nbrs,
+                           dtype=torch.int64, device=device)
+    degree = int(nbrs.shape[1])
     lay = Layout.make(dim, degree)
     if signs.shape[0] != lay.padded_dim:
         raise ValueError("signs must have padded_dim entries")
     x = torch.as_tensor(np.ascontiguousarray(base, dtype=np.float32), device=device)
-    nbrs = build_graph(x, degree, random_links=random_links, alpha=alpha, candidates=candidates,
-                       fill_random=fill_random, verbose=verbose)
     codes, factors = encode(x, nbrs, signs, use_ip=use_ip,
                             chunk_edges=(1 << 22) if x.device.type == "cuda" else (1 << 20))
     rows = np.zeros((n, lay.row_offset), dtype=np.float32)
@@ -291,8 +304,9 @@ def build_codebook(base: np.ndarray, degree: int, signs: np.ndarray, use_ip: boo
     ids = nbrs.cpu().numpy()
     ids = np.where(ids < 0, MAX_INDEX, ids).astype(np.uint32)
     rows[:, lay.neighbor_offset : lay.row_offset].view(np.uint32)[:] = ids
-    entry = entry_point(x) if store_entry else MAX_INDEX
-    return Codebook(rows, np.asarray(signs, dtype=np.float32), entry, lay)
+    if entry is None:
+        entry = entry_point(x) if store_entry else MAX_INDEX
+    return Codebook(rows, np.asarray(signs, dtype=np.float32), int(entry), lay)
 
 
 def ground_truth(base: np.ndarray, queries: np.ndarray, k: int,

@@ -1520,7 +1520,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
     const float *data = P.data;
 
     FG_PHASE(0);
-    for (int iter = 0; iter < kMaxIterations; ++iter) {
+    int iter = 0;
+    for (; iter < kMaxIterations; ++iter) {
         // lane-derived values are recomputed in each iteration, not held
         const int lane = lane_id_opaque();
         const int h = lane >> 5, nl = lane & 31;
@@ -1532,10 +1533,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
         }
         FG_PHASE(1);
         // The merge runs before the iteration-limit test, so a search stopped
-        // by the limit merges its last candidates here (the final merge,
-        // adaptive_search.cuh:447-451).  A search that stops because no beam entry is left to
-        // expand has merged them already: its final merge sees an empty
-        // candidate buffer and leaves the beam as it is.
+        // by max_iter merges its last candidates here (the reference's final
+        // merge, adaptive_search.cuh:447-451).  A search that stops because no
+        // beam entry is left to expand has merged them already: its final
+        // merge sees an empty candidate buffer and leaves the beam as it is.
+        // A search that runs all kMaxIterations iterations (max_iter > 1024,
+        // i.e. beam >= 931) leaves the loop without passing here again and
+        // merges after it.
         merge_beam(P, bp, ms, cd, ci, cand_span, split_fast);
         FG_PHASE(2);
         if (iter >= P.max_iter) break;
@@ -1881,6 +1885,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
         else FG_PHASE(8);
         __syncthreads();
     }
+    // the loop ran out at kMaxIterations: the last iteration's exact-scored
+    // candidates are still in the buffer (adaptive_search.cuh:449-451)
+    if (iter == kMaxIterations) merge_beam(P, bp, ms, cd, ci, cand_span, split_fast);
 
     FG_PHASE(3);
     // result writer (adaptive_search.cuh:455-464)

@@ -553,23 +553,24 @@ int fgo_warp_keep_topk(const float *values, const int *valid, int keep_k, int *k
 
 /* -------------------------------------------------------------- controller */
 
-/* adaptive_search_utils.cuh:8-18 */
-typedef struct {
-    int spec_degree;
-    float rho;
-    int policy_iters;
-    uint32_t top1_node;
-    int top1_stall_iters;
-    int warmup_done;
-    float entry_distance;
-    float last_expander_distance;
-    float current_expander_distance;
-} ctl_state;
+/* adaptive_search_utils.cuh:8-18 is fgo_ctl_state (fg_oracle.h); the search
+ * starts it as adaptive_search.cuh:75-85 and :115 do. */
+void fgo_ctl_init(fgo_ctl_state *st, float entry_distance) {
+    st->spec_degree = 1;
+    st->rho = 0.25f;
+    st->policy_iters = 0;
+    st->top1_node = FGO_MAX_INDEX;
+    st->top1_stall_iters = 0;
+    st->warmup_done = 0;
+    st->entry_distance = entry_distance;
+    st->last_expander_distance = FLT_MAX;
+    st->current_expander_distance = FLT_MAX;
+}
 
 static inline int finite_below_max(float x) { return isfinite(x) && x < FLT_MAX; }
 
 /* adaptive_search_utils.cuh:51-72 */
-static float expander_progress(const ctl_state *prev, float *last, float *cur) {
+static float expander_progress(const fgo_ctl_state *prev, float *last, float *cur) {
     const float entry = prev->entry_distance;
     *last = finite_below_max(prev->last_expander_distance) ? prev->last_expander_distance : entry;
     *cur = finite_below_max(prev->current_expander_distance) ? prev->current_expander_distance : *last;
@@ -582,7 +583,7 @@ static float expander_progress(const ctl_state *prev, float *last, float *cur) {
 
 /* adaptive_search.cuh:166-190 with adaptive_search_utils.cuh:32-39, 74-119
  * (CHECK_INTERVAL = 1, so every non-stage-II iteration re-tunes rho). */
-static void controller_step(ctl_state *st, uint32_t beam0, float phase2_rho) {
+void fgo_controller_step(fgo_ctl_state *st, uint32_t beam0, float phase2_rho) {
     const uint32_t cur_top1 = beam0 & 0x7fffffffu;
     const int stall = (st->policy_iters > 0 && cur_top1 == st->top1_node) ? st->top1_stall_iters + 1 : 0;
     const int phase_changed = st->warmup_done || stall >= 4;
@@ -605,6 +606,21 @@ static void controller_step(ctl_state *st, uint32_t beam0, float phase2_rho) {
         st->rho = clamp_float(fmaf(span, rate, base), 0.0f, cap);
     }
     st->policy_iters += 1;
+}
+
+/* adaptive_search_utils.cuh:41-49 (record_selected_expander_dist): the LAST
+ * selected expander's distance becomes the current one. */
+void fgo_record_expander(fgo_ctl_state *st, const float *parent_dist, uint32_t n_parents) {
+    st->last_expander_distance = finite_below_max(st->current_expander_distance)
+                                     ? st->current_expander_distance : st->entry_distance;
+    st->current_expander_distance = parent_dist[n_parents - 1];
+}
+
+/* adaptive_search_utils.cuh:25-30: valid only once the beam's last slot is
+ * filled; then the distance at position min(K, beam) - 1. */
+float fgo_kth_cutoff(int K, int beam, const uint32_t *beam_idx, const float *beam_dist) {
+    if (beam_idx[beam - 1] == FGO_MAX_INDEX) return FLT_MAX;
+    return beam_dist[(K < beam ? K : beam) - 1];
 }
 
 /* ------------------------------------------------------------------ search */
@@ -659,7 +675,7 @@ static int search_one_ws(const fgo_index *ix, const float *query, int K, int bea
     uint32_t plist[FGO_SEARCH_WIDTH], pnode[FGO_SEARCH_WIDTH];
     float pdist[FGO_SEARCH_WIDTH];
 
-    ctl_state st = {1, 0.25f, 0, FGO_MAX_INDEX, 0, 0, FLT_MAX, FLT_MAX, FLT_MAX};
+    fgo_ctl_state st;
     hash_reset(hash, bitlen);
     for (uint32_t i = 0; i < pbeam; ++i) { bd[i] = FLT_MAX; bi[i] = FGO_MAX_INDEX; }
     for (uint32_t i = 0; i < cbs; ++i) { cd[i] = FLT_MAX; ci[i] = FGO_MAX_INDEX; }
@@ -669,14 +685,15 @@ static int search_one_ws(const fgo_index *ix, const float *query, int K, int bea
     c.exact++;
     ci[0] = ix->entry;
     cd[0] = entry_dist;
-    st.entry_distance = entry_dist;
+    fgo_ctl_init(&st, entry_dist);
     fgo_hash_insert(hash, bitlen, ix->entry);
 
     fgo_query_prepare(query, ix->signs, dim, B, &ws->qf);          /* :121-123 */
     const fgo_query_factors *qf = &ws->qf;
 
     for (int iter = 0; iter < FGO_MAX_ITERATIONS; ++iter) {
-        if ((iter + 1) % FGO_HASH_RESET == 0) {                       /* :128-134 */
+        const int restored = (iter + 1) % FGO_HASH_RESET == 0;
+        if (restored) {                                               /* :128-134 */
             hash_reset(hash, bitlen);
             for (int i = 0; i < beam_sz; ++i) fgo_hash_insert(hash, bitlen, bi[i] & ~FGO_MSB);
         }
@@ -687,12 +704,8 @@ static int search_one_ws(const fgo_index *ix, const float *query, int K, int bea
         for (uint32_t i = 0; i < cbs; ++i) { cd[i] = FLT_MAX; ci[i] = FGO_MAX_INDEX; }
         for (int i = 0; i < FGO_SEARCH_WIDTH; ++i) { pnode[i] = FGO_MAX_INDEX; pdist[i] = FLT_MAX; }
         uint32_t compact_count = 0;
-        /* adaptive_search_utils.cuh:25-30 */
-        float kth_cutoff = FLT_MAX;
-        if (bi[beam_sz - 1] != FGO_MAX_INDEX)
-            kth_cutoff = bd[(K < beam_sz ? K : beam_sz) - 1];
-
-        controller_step(&st, bi[0], phase2_rho);                     /* :166-191 */
+        const float kth_cutoff = fgo_kth_cutoff(K, beam_sz, bi, bd);   /* :160-163 */
+        fgo_controller_step(&st, bi[0], phase2_rho);                  /* :166-191 */
 
         const uint32_t nexp = fgo_pick_expanders(st.spec_degree, plist, beam_sz, bi);  /* :193-197 */
         if (!nexp) break;
@@ -702,10 +715,7 @@ static int search_one_ws(const fgo_index *ix, const float *query, int K, int bea
             pnode[p] = bi[plist[p]] & 0x7fffffffu;
             pdist[p] = bd[plist[p]];
         }
-        /* adaptive_search_utils.cuh:41-49 */
-        st.last_expander_distance = finite_below_max(st.current_expander_distance)
-                                        ? st.current_expander_distance : st.entry_distance;
-        st.current_expander_distance = pdist[nexp - 1];
+        fgo_record_expander(&st, pdist, nexp);                         /* :213-215 */
 
         fgo_trace_rec *tr = (trace && tl < trace_cap) ? &trace[tl] : NULL;
         if (tr) {
@@ -718,6 +728,10 @@ static int search_one_ws(const fgo_index *ix, const float *query, int K, int bea
             tr->top1 = bi[0];
             tr->top1_dist = bd[0];
             tr->kth_cutoff = kth_cutoff;
+            tr->stall = st.top1_stall_iters;
+            tr->last_expander_distance = st.last_expander_distance;
+            tr->current_expander_distance = st.current_expander_distance;
+            tr->restored = (uint32_t)restored;
         }
 
         const int kth_valid = finite_below_max(kth_cutoff);

@@ -93,7 +93,25 @@ typedef struct {
     uint32_t n_cand;
     uint32_t cand_idx[FGO_BUFFER_BOUND];
     float cand_dist[FGO_BUFFER_BOUND];
+    /* controller state after this iteration's update and expander record */
+    int32_t stall;               /* top1_stall_iters */
+    float last_expander_distance;
+    float current_expander_distance;
+    uint32_t restored;           /* 1 if the visited set was rebuilt this iteration */
 } fgo_trace_rec;
+
+/* Adaptive controller state (adaptive_search_utils.cuh:8-18). */
+typedef struct {
+    int spec_degree;
+    float rho;
+    int policy_iters;
+    uint32_t top1_node;
+    int top1_stall_iters;
+    int warmup_done;
+    float entry_distance;
+    float last_expander_distance;
+    float current_expander_distance;
+} fgo_ctl_state;
 
 /* ---- sizing helpers ---- */
 int fgo_compute_layout(uint32_t dim, uint32_t degree, fgo_layout *out);
@@ -132,6 +150,12 @@ uint32_t fgo_hash_insert(uint32_t *table, unsigned bitlen, uint32_t key);
 uint32_t fgo_hash_contains(const uint32_t *table, unsigned bitlen, uint32_t key);
 uint32_t fgo_pick_expanders(int n, uint32_t *out, int m, uint32_t *beam_idx);
 int fgo_warp_keep_topk(const float *values, const int *valid, int keep_k, int *keep_out);
+
+/* ---- controller ---- */
+void fgo_ctl_init(fgo_ctl_state *st, float entry_distance);
+void fgo_controller_step(fgo_ctl_state *st, uint32_t beam0, float phase2_rho);
+void fgo_record_expander(fgo_ctl_state *st, const float *parent_dist, uint32_t n_parents);
+float fgo_kth_cutoff(int K, int beam, const uint32_t *beam_idx, const float *beam_dist);
 
 /* ---- search ---- */
 int fgo_search_one(const fgo_index *ix, const float *query, int K, int beam, uint32_t *out,

@@ -47,7 +47,16 @@ class TraceRec(C.Structure):
     _fields_ = [("iter", C.c_uint32), ("theta", C.c_uint32), ("rho", C.c_float),
                 ("n_parents", C.c_uint32), ("parents", C.c_uint32 * 8), ("top1", C.c_uint32),
                 ("top1_dist", C.c_float), ("kth_cutoff", C.c_float), ("n_cand", C.c_uint32),
-                ("cand_idx", C.c_uint32 * 32), ("cand_dist", C.c_float * 32)]
+                ("cand_idx", C.c_uint32 * 32), ("cand_dist", C.c_float * 32),
+                ("stall", C.c_int32), ("last_expander_distance", C.c_float),
+                ("current_expander_distance", C.c_float), ("restored", C.c_uint32)]
+
+
+class CtlState(C.Structure):
+    _fields_ = [("spec_degree", C.c_int), ("rho", C.c_float), ("policy_iters", C.c_int),
+                ("top1_node", C.c_uint32), ("top1_stall_iters", C.c_int), ("warmup_done", C.c_int),
+                ("entry_distance", C.c_float), ("last_expander_distance", C.c_float),
+                ("current_expander_distance", C.c_float)]
 
 
 COUNTER_DTYPE = np.dtype([(n, np.uint32) for n, _ in Counters._fields_])
@@ -107,6 +116,11 @@ def lib():
         L.fgo_pick_expanders.restype = C.c_uint32
         L.fgo_warp_keep_topk.argtypes = [f32p, C.POINTER(C.c_int), C.c_int, C.POINTER(C.c_int)]
         L.fgo_warp_keep_topk.restype = C.c_int
+        L.fgo_ctl_init.argtypes = [C.POINTER(CtlState), C.c_float]
+        L.fgo_controller_step.argtypes = [C.POINTER(CtlState), C.c_uint32, C.c_float]
+        L.fgo_record_expander.argtypes = [C.POINTER(CtlState), f32p, C.c_uint32]
+        L.fgo_kth_cutoff.argtypes = [C.c_int, C.c_int, u32p, f32p]
+        L.fgo_kth_cutoff.restype = C.c_float
         L.fgo_search_one.argtypes = [C.POINTER(Index), f32p, C.c_int, C.c_int, u32p, C.POINTER(Counters),
                                      C.POINTER(TraceRec), C.c_uint32, u32p]
         L.fgo_search_one.restype = C.c_int

@@ -1,0 +1,170 @@
+"""Hand-built codebooks whose searches can be traced by hand.
+
+Every edge u -> v carries factor_dq = factor_vq = 0 and an all-zero code, so
+the search's RaBitQ estimate (include/utils.cuh:989-993)
+
+    est = triple_x + d(q, u) + factor_dq * width * (2 raw - sum_q) + factor_vq * low
+
+is exactly triple_x + d(q, u).  Setting triple_x = est(u -> v) - d(q, u)
+gives each edge the estimate the scenario wants, independent of the query's
+quantization.  Node vectors are integer points q + o with |o|^2 = the wanted
+squared distance (four-square decompositions), so exact distances are exact
+integers too.  Used by the CPU trace tests and, unchanged, by the GPU parity
+tests.
+"""
+from __future__ import annotations
+
+import functools
+import math
+
+import numpy as np
+
+from flashgann_amd.codebook import MAX_INDEX, Codebook, Layout
+
+DIM = 40  # padded dimension 64: the smallest layout with a code region
+
+
+@functools.lru_cache(maxsize=None)
+def four_squares(n: int) -> tuple[int, int, int, int]:
+    """a^2 + b^2 + c^2 + d^2 == n with a >= b >= c >= d >= 0 (brute force)."""
+    a = math.isqrt(n)
+    while a >= 0:
+        r1 = n - a * a
+        b = min(a, math.isqrt(r1))
+        while b >= 0:
+            r2 = r1 - b * b
+            c = min(b, math.isqrt(r2))
+            while c >= 0:
+                r3 = r2 - c * c
+                d = math.isqrt(r3)
+                if d * d == r3 and d <= c:
+                    return a, b, c, d
+                c -= 1
+            b -= 1
+        a -= 1
+    raise ValueError(n)
+
+
+def query(dim: int = DIM) -> np.ndarray:
+    """(10, 3, 0, ...): its rotation is not constant, so the quantizer's width
+    is nonzero (a constant rotated query is undefined in the reference)."""
+    q = np.zeros(dim, np.float32)
+    q[0], q[1] = 10, 3
+    return q
+
+
+def make(dist: dict[int, int], adj: dict[int, list[int]], est: dict[tuple[int, int], int],
+         degree: int, entry: int = 0, dim: int = DIM) -> tuple[Codebook, np.ndarray]:
+    """Codebook over nodes 0..max(dist) at the given squared distances from
+    query(); adj[u] lists u's neighbours (padded with 0xFFFFFFFF to degree);
+    est[(u, v)] is the estimate of edge u -> v (default: the exact distance)."""
+    n = max(dist) + 1
+    q = query(dim)
+    lay = Layout.make(dim, degree)
+    rows = np.zeros((n, lay.row_offset), np.float32)
+    for v in range(n):
+        o = np.zeros(dim, np.float32)
+        o[2:6] = four_squares(dist[v])
+        rows[v, :dim] = q + o
+    f = rows[:, lay.factor_offset:lay.neighbor_offset].reshape(n, 3, degree)
+    ids = rows[:, lay.neighbor_offset:lay.row_offset].view(np.uint32)
+    ids[:] = MAX_INDEX
+    f[:, 0, :] = np.float32(np.finfo(np.float32).max)  # padding edges
+    for u, lst in adj.items():
+        assert len(lst) <= degree
+        for j, v in enumerate(lst):
+            if v is None:
+                continue
+            ids[u, j] = v
+            e = est.get((u, v), dist[v])
+            f[u, 0, j] = e - dist[u]
+    signs = np.ones(lay.padded_dim, np.float32)
+    return Codebook(rows, signs, entry, lay), q[None, :]
+
+
+def scenario_cutoff():
+    """Degree 4, beam 3, K 2: the K-th cutoff at beam[min(K, beam) - 1] and
+    the near count's `<=` (an estimate equal to the cutoff), the keep-all
+    shortcut, and the rho trajectory of stage I."""
+    dist = {0: 100, 1: 36, 2: 49, 3: 64, 4: 81, 5: 25, 6: 40, 7: 50, 8: 80, 9: 30, 10: 45}
+    adj = {0: [1, 2, 3, 4], 1: [5, 6, 7, 8], 2: [0, 1], 3: [0], 4: [0], 5: [1, 6, 0, 2],
+           6: [9, 10, 1, 5], 7: [1], 8: [1], 9: [5, 6, 10, 1], 10: [6]}
+    est = {(1, 6): 49}  # node 6 is at 40 but estimated at 49, the cutoff
+    return make(dist, adj, est, degree=4)
+
+
+def scenario_stage2():
+    """Degree 8, beam 64, K 10: three dead-end stage-I expansions under a
+    fixed top-1 (the entry), the switch to stage II on the fourth stall, and a
+    stage-II round over three parents that keeps 4 children each (selected by
+    estimate, compacted in (task, lane) order)."""
+    dist = {0: 1}
+    adj = {0: [1, 2, 3, 4, 5, 6, 7, 8]}
+    for i in range(1, 9):
+        dist[i] = 10 * i
+        adj[i] = [0]
+    pattern = [8, 1, 7, 2, 6, 3, 5, 4]  # estimate rank of each neighbour slot
+    nxt = 9
+    for p, base in ((4, 100), (5, 200), (6, 300)):
+        kids = list(range(nxt, nxt + 8))
+        nxt += 8
+        adj[p] = kids
+        for k, r in zip(kids, pattern):
+            dist[k] = base + 10 * r
+            adj[k] = [p]
+    return make(dist, adj, {}, degree=8)
+
+
+def scenario_reset(n: int = 40):
+    """Degree 3 path: node i links to i+1, i+2, i-1 and lies at squared
+    distance 10000 - 10 i, so stage I expands node 2k at iteration k.  The
+    visited set is rebuilt from the beam at iteration 15, before that
+    iteration's merge: node 29, scored at iteration 14, is then admitted a
+    second time by its sibling 30 (the reference's quirk at
+    adaptive_search.cuh:128-145)."""
+    dist = {i: 10000 - 10 * i for i in range(n)}
+    adj = {}
+    for i in range(n):
+        adj[i] = [i + 1 if i + 1 < n else None, i + 2 if i + 2 < n else None, i - 1 if i >= 1 else None]
+    return make(dist, adj, {}, degree=3)
+
+
+def complete_graph(n: int = 33, dim: int = 128, nq: int = 8, seed: int = 11):
+    """n integer points, each linked to all others (degree n - 1) in
+    (distance, id) order, with real RaBitQ codes; queries from the same
+    distribution."""
+    from flashgann_amd import builder, datasets
+    rng = np.random.default_rng(seed)
+    base = rng.integers(0, 40, size=(n, dim)).astype(np.float32)
+    q = rng.integers(0, 40, size=(nq, dim)).astype(np.float32)
+    d = ((base[:, None, :].astype(np.float64) - base[None, :, :]) ** 2).sum(-1)
+    np.fill_diagonal(d, np.inf)
+    order = np.lexsort((np.broadcast_to(np.arange(n), (n, n)), d), axis=1)[:, : n - 1]
+    cb = builder.codebook_from_graph(base, order, datasets.signs_for(128, 1), entry=0)
+    return cb, q, base
+
+
+@functools.lru_cache(maxsize=None)
+def line_index(n: int = 20000, dim: int = 64, degree: int = 32):
+    """Points i e_0 (i = 0..n-1) on a line, each linked to its `degree`
+    nearest by (distance, id), with real RaBitQ codes; entry point 0 and four
+    queries past the far end.  Stage I walks ~16 nodes per iteration, so a
+    search never runs out of unexpanded entries: it stops at max_iter =
+    min((11 beam + 9) / 10, 1024) (gpu_search_adaptive.cu:96,
+    adaptive_search_config.cuh:12) with candidates still arriving."""
+    from flashgann_amd import builder, datasets
+    base = np.zeros((n, dim), np.float32)
+    base[:, 0] = np.arange(n)
+    # the degree nearest of r are the window of degree + 1 points around r
+    # (shifted inwards at the ends) without r, ordered by (distance, id)
+    lo = np.clip(np.arange(n) - degree // 2, 0, n - 1 - degree)
+    win = lo[:, None] + np.arange(degree + 1)[None, :]
+    r = np.arange(n)[:, None]
+    nbrs = win[win != r].reshape(n, degree)
+    order = np.lexsort((nbrs, np.abs(nbrs - r)), axis=1)
+    nbrs = np.take_along_axis(nbrs, order, axis=1)
+    cb = builder.codebook_from_graph(base, nbrs, datasets.signs_for(64, 1), entry=0)
+    q = np.zeros((4, dim), np.float32)
+    q[:, 0] = [n + 10, n + 500, n + 3000, 2 * n]
+    q[:, 1] = [0, 1, 2, 3]
+    return cb, q, base

@@ -1,0 +1,252 @@
+"""Pins for the oracle's controller and search-loop sequencing.
+
+The expected values below are worked out by hand from the reference's rules
+(the derivation is in each docstring), not recomputed with the oracle's
+formulas: the controller (src/adaptive_search_utils.cuh:32-135), the K-th
+cutoff (:25-30), the loop order of src/adaptive_search.cuh:126-215 (reset and
+restore, then the merge, then cutoff, controller, pick), the near count and
+keep rules (:281-302, :397-404), max_iter (gpu_search_adaptive.cu:96) and the
+final merge (adaptive_search.cuh:449-451).  The hand-built codebooks are in
+tests/crafted.py.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import crafted
+from oracle import oracle as O
+
+FLT_MAX = float(np.finfo(np.float32).max)
+MSB = 0x80000000
+
+
+def _ctl(entry):
+    st = O.CtlState()
+    O.lib().fgo_ctl_init(O.C.byref(st), entry)
+    return st
+
+
+def _step(st, beam0, rho2):
+    O.lib().fgo_controller_step(O.C.byref(st), beam0, rho2)
+    return st.spec_degree, st.rho, st.top1_stall_iters
+
+
+def _record(st, dists):
+    a = np.asarray(dists, np.float32)
+    O.lib().fgo_record_expander(O.C.byref(st), O.ptr(a, O.C.c_float), len(a))
+    return st.last_expander_distance, st.current_expander_distance
+
+
+def test_controller_trajectory_degree32():
+    """Degree 32: phase-2 rate 1 - 4/32 = 0.875, stage-I span 0.875 - 0.25 =
+    0.625.  Entry distance 1000.
+      step 0 (top-1 5): first update, rate 0.25, stall 0; expander at 900
+      step 1 (top-1 7): progress (1000 - 900)/1000 = 0.1 -> 0.25 + 0.0625 = 0.3125
+      step 2 (top-1 7, stall 1): expander 850 recorded after step 1, progress
+             (900 - 850)/1000 = 0.05 -> 0.34375
+      step 3 (stall 2): expander 850 again, progress 0 -> 0.34375
+      step 4 (stall 3): expander 800, progress 0.05 -> 0.375
+      step 5 (stall 4): stage II, theta 8, rate 0.875
+      then the three expanders 100, 200, 300: the LAST one (300) is recorded
+      step 6 (top-1 9): stall back to 0 but stage II sticks."""
+    st = _ctl(1000.0)
+    assert _step(st, 5, 0.875) == (1, 0.25, 0)
+    assert _record(st, [900]) == (1000.0, 900.0)
+    th, rho, stall = _step(st, 7, 0.875)
+    assert (th, stall) == (1, 0) and rho == pytest.approx(0.3125, abs=1e-6)
+    assert _record(st, [850]) == (900.0, 850.0)
+    th, rho, stall = _step(st, 7, 0.875)
+    assert (th, stall) == (1, 1) and rho == pytest.approx(0.34375, abs=1e-6)
+    _record(st, [850])
+    th, rho, stall = _step(st, 7 | MSB, 0.875)  # the expanded flag is masked off
+    assert (th, stall) == (1, 2) and rho == pytest.approx(0.34375, abs=1e-6)
+    _record(st, [800])
+    th, rho, stall = _step(st, 7, 0.875)
+    assert (th, stall) == (1, 3) and rho == pytest.approx(0.375, abs=1e-6)
+    _record(st, [2000])
+    assert _step(st, 7, 0.875) == (8, 0.875, 4)
+    assert st.warmup_done == 1
+    assert _record(st, [100, 200, 300]) == (2000.0, 300.0)
+    assert _step(st, 9, 0.875) == (8, 0.875, 0)
+    assert st.policy_iters == 7
+
+
+def test_controller_small_degree_span_and_cap():
+    """Degree <= 4: phase-2 rate 0 (RHO_MIN), so the span and the cap are
+    RHO_MAX - RHO_MIN = 0.99.  Entry 100, expanders 100 then 40: progress
+    0.6 -> 0.25 + 0.594 = 0.844; then 40 -> 0 (progress 0.4): 0.844 + 0.396
+    is clamped to 0.99."""
+    st = _ctl(100.0)
+    _step(st, 1, 0.0)
+    _record(st, [100])
+    _step(st, 2, 0.0)
+    _record(st, [40])
+    assert _step(st, 3, 0.0)[1] == pytest.approx(0.844, abs=1e-6)
+    _record(st, [0])
+    assert _step(st, 4, 0.0)[1] == pytest.approx(0.99, abs=1e-7)
+
+
+def test_controller_progress_guards():
+    """Progress is 0 when it would be negative, and when the entry distance
+    is 0 (|entry| <= 1e-20) or not finite: the rate then stays where it is.
+    Entry 100, expanders 50 then 80: step 2 moves the rate by 0.625 * 0.5 to
+    0.5625, step 3 (progress -0.3) keeps it.  Entries 0 and inf never move it
+    from 0.25."""
+    for entry, exps, r2 in ((100.0, [50, 80], 0.5625), (0.0, [0, -5], 0.25), (float("inf"), [3, 1], 0.25)):
+        st = _ctl(entry)
+        _step(st, 1, 0.875)
+        _record(st, [exps[0]])
+        assert _step(st, 2, 0.875)[1] == r2, entry
+        _record(st, [exps[1]])
+        assert _step(st, 3, 0.875)[1] == r2, entry
+
+
+def test_kth_cutoff_position():
+    """Valid only once the beam's last slot holds an id; then the distance at
+    position min(K, beam) - 1."""
+    L = O.lib()
+    idx = np.array([3, 4, 5, 6, 0xFFFFFFFF], np.uint32)
+    d = np.array([1, 2, 3, 4, FLT_MAX], np.float32)
+    u32, f32 = O.C.c_uint32, O.C.c_float
+    assert L.fgo_kth_cutoff(2, 5, O.ptr(idx, u32), O.ptr(d, f32)) == FLT_MAX
+    assert L.fgo_kth_cutoff(2, 4, O.ptr(idx, u32), O.ptr(d, f32)) == 2.0
+    assert L.fgo_kth_cutoff(3, 4, O.ptr(idx, u32), O.ptr(d, f32)) == 3.0
+    assert L.fgo_kth_cutoff(10, 4, O.ptr(idx, u32), O.ptr(d, f32)) == 4.0
+    idx[1] |= MSB  # expanded entries count as filled
+    assert L.fgo_kth_cutoff(1, 2, O.ptr(idx, u32), O.ptr(d, f32)) == 1.0
+
+
+def _trace(cb, q, K, beam):
+    out, cnt, tr = O.OracleIndex.from_codebook(cb).search_one(q[0], K, beam, trace_cap=1100)
+    c = tuple(getattr(cnt, f) for f, _ in O.Counters._fields_)
+    recs = []
+    for t in tr:
+        ids = [t.cand_idx[i] for i in range(32) if t.cand_idx[i] != 0xFFFFFFFF]
+        ds = [t.cand_dist[i] for i in range(32) if t.cand_idx[i] != 0xFFFFFFFF]
+        recs.append(dict(theta=t.theta, rho=t.rho, parents=list(t.parents)[: t.n_parents],
+                         top1=t.top1 & ~MSB, kth=t.kth_cutoff, cand=ids, cdist=ds, stall=t.stall,
+                         last=t.last_expander_distance, cur=t.current_expander_distance,
+                         restored=t.restored))
+    return out.tolist(), c, recs
+
+
+def test_trace_cutoff_and_near_count():
+    """Degree 4 (span and cap 0.99), beam 3 (max_iter (33 + 9)/10 = 4), K 2.
+      it 0: expand 0 (d 100); keep ceil(4 * 0.75) = 3 of 4 valid, so all four
+            are estimated (36, 49, 64, 81) and 1, 2, 3 scored in estimate
+            order.  The beam was not full: no cutoff.
+      it 1: beam [1:36, 2:49, 3:64] is full, cutoff = beam[K-1] = 49.  Expand
+            1; its children are estimated at 25, 49 (node 6, truly at 40), 50,
+            80.  Near count (estimate <= 49) = 2, so 2 are kept: 5 and 6.
+      it 2: beam [5:25, 1:36, 6:40], cutoff 36; progress (100 - 36)/100 = 0.64,
+            rate 0.25 + 0.99 * 0.64 = 0.8836.  Expand 5: all its children
+            are visited (the keep-all shortcut: no estimates).
+      it 3: progress (36 - 25)/100 = 0.11: 0.8836 + 0.1089 is capped at 0.99;
+            keep ceil(4 * 0.01) = 1.  Expand 6 (top-1 5 again: stall 1);
+            children 9 (est 30) and 10 (est 45) are estimated, one kept: 9.
+      it 4: the iteration limit; the final merge puts 9 at rank 2.
+    Counters: 4 iterations, 4 expansions, 16 ids, 4 + 4 + 2 estimates,
+    1 + 3 + 2 + 1 exact distances."""
+    cb, q = crafted.scenario_cutoff()
+    out, cnt, tr = _trace(cb, q, 2, 3)
+    assert out == [5, 9]
+    assert cnt == (4, 4, 16, 10, 7, 0xFFFFFFFF)
+    assert [t["parents"] for t in tr] == [[0], [1], [5], [6]]
+    assert [t["kth"] for t in tr] == [FLT_MAX, 49.0, 36.0, 36.0]
+    assert [t["cand"] for t in tr] == [[1, 2, 3], [5, 6], [], [9]]
+    assert [t["cdist"] for t in tr] == [[36, 49, 64], [25, 40], [], [30]]
+    assert [t["top1"] for t in tr] == [0, 1, 5, 5]
+    assert [t["stall"] for t in tr] == [0, 0, 0, 1]
+    assert np.allclose([t["rho"] for t in tr], [0.25, 0.25, 0.8836, 0.99], atol=1e-6)
+    assert [(t["last"], t["cur"]) for t in tr] == [(100, 100), (100, 36), (36, 25), (25, 40)]
+    assert all(t["theta"] == 1 for t in tr)
+
+
+def test_trace_stage2_switch_and_keep():
+    """Degree 8 (phase-2 rate 0.5), beam 64 (never full: no cutoff), K 10.
+      it 0: expand the entry 0 (d 1, top-1 for good); keep ceil(8 * 0.75) = 6
+            of its 8 children (10 .. 80): 1 .. 6 are scored.
+      it 1-3: expand 1, 2, 3 (dead ends); the top-1 stalls 1, 2, 3 times and
+            progress is negative (expanders get farther), so the rate stays 0.25.
+      it 4: fourth stall: theta 8, rate 0.5.  The unexpanded entries are 4, 5,
+            6: three tasks.  Keep min(ceil(8 * 0.5), 32 / 8) = 4 per parent.
+            Each parent's slots hold estimate ranks 8 1 7 2 6 3 5 4, so the
+            kept lanes are 1, 3, 5, 7 and the list, in (task, lane) order,
+            is 10 12 14 16 | 18 20 22 24 | 26 28 30 32 (distances base + 10,
+            + 20, + 30, + 40 for bases 100, 200, 300).
+      it 5: the first 8 of those 12 in beam order; it 6: the other 4; it 7
+            finds nothing to expand.
+    Counters: 7 iterations, 1+1+1+1+3+8+4 = 19 expansions, 4 * 8 + 24 + 64 +
+    32 = 152 ids, 8 + 24 estimates, 1 + 6 + 12 exact distances, stage II
+    from iteration 4."""
+    cb, q = crafted.scenario_stage2()
+    out, cnt, tr = _trace(cb, q, 10, 64)
+    assert out == [0, 1, 2, 3, 4, 5, 6, 10, 12, 14]
+    assert cnt == (7, 19, 152, 32, 19, 4)
+    assert [t["theta"] for t in tr] == [1, 1, 1, 1, 8, 8, 8]
+    assert [t["stall"] for t in tr] == [0, 1, 2, 3, 4, 5, 6]
+    assert np.allclose([t["rho"] for t in tr], [0.25] * 4 + [0.5] * 3)
+    assert [t["parents"] for t in tr] == [[0], [1], [2], [3], [4, 5, 6],
+                                         [10, 12, 14, 16, 18, 20, 22, 24], [26, 28, 30, 32]]
+    assert tr[0]["cand"] == [1, 2, 3, 4, 5, 6]
+    assert tr[4]["cand"] == [10, 12, 14, 16, 18, 20, 22, 24, 26, 28, 30, 32]
+    assert tr[4]["cdist"] == [110, 120, 130, 140, 210, 220, 230, 240, 310, 320, 330, 340]
+    assert all(t["kth"] == FLT_MAX for t in tr)
+    # the last selected expander's distance is the one recorded
+    assert (tr[4]["cur"], tr[5]["cur"], tr[6]["cur"]) == (60.0, 240.0, 340.0)
+
+
+def test_trace_reset_readmits_pending_sibling():
+    """Degree-3 path (i -> i+1, i+2, i-1; distance 10000 - 10 i), beam 16,
+    K 16: iteration k expands node 2k and scores 2k+1, 2k+2 (2k-1 is
+    visited).  max_iter = (176 + 9)/10 = 18.  At iteration 15 the visited set
+    is rebuilt from the beam before the merge, so 29 and 30 (scored at
+    iteration 14) are not in it: expanding 30 admits 29 a second time.  The
+    final beam holds 29 twice.  No estimates (keep ceil(3 (1 - rate)) = 3
+    while the rate stays below 1/3), 1 + 2 * 18 + 1 exact distances."""
+    cb, q = crafted.scenario_reset()
+    out, cnt, tr = _trace(cb, q, 16, 16)
+    assert out == [36, 35, 34, 33, 32, 31, 30, 29, 29, 28, 27, 26, 25, 24, 23, 22]
+    assert cnt == (18, 18, 54, 0, 38, 0xFFFFFFFF)
+    assert [t["parents"] for t in tr] == [[2 * k] for k in range(18)]
+    assert [t["restored"] for t in tr] == [1 if k == 15 else 0 for k in range(18)]
+    for k, t in enumerate(tr):
+        want = [31, 32, 29] if k == 15 else [2 * k + 1, 2 * k + 2]
+        assert t["cand"] == want, k
+
+
+def test_complete_graph_beam_covers_all_is_brute_force():
+    """On a complete graph with beam >= n every node is scored exactly and
+    never evicted, so the result is the brute-force top-K (distinct integer
+    distances).  The searches end before the first visited-set rebuild
+    (iteration 15), so no node is admitted twice."""
+    cb, q, base = crafted.complete_graph()
+    d = ((q[:, None, :].astype(np.float64) - base[None]) ** 2).sum(-1)
+    gt = np.lexsort((np.broadcast_to(np.arange(base.shape[0]), d.shape), d), axis=1)[:, :10]
+    ids, cnt = O.OracleIndex.from_codebook(cb).search(q, 10, 64)
+    assert (cnt["iterations"] < 15).all()
+    for i in range(q.shape[0]):
+        ds = np.sort(d[i])
+        assert ds[9] < ds[10], "ties at the K-th place"
+    assert np.array_equal(ids, gt)
+
+
+@pytest.mark.parametrize("beam", [1, 16, 64, 100, 128, 256, 930, 931, 1000, 1024])
+def test_line_iterations_and_final_merge(beam):
+    """A search on the line never runs out of unexpanded entries, so it runs
+    exactly min((11 beam + 9)/10, 1024) iterations.  Whatever stops it, the
+    last iteration's candidates are merged: the result's distances are the K
+    smallest of all exact distances the search computed (the beam keeps the
+    best `beam` of everything merged, and K <= beam)."""
+    cb, q, base = crafted.line_index()
+    oix = O.OracleIndex.from_codebook(cb)
+    K = min(10, beam)
+    for qi in range(2):
+        out, cnt, tr = oix.search_one(q[qi], K, beam, trace_cap=1100)
+        assert cnt.iterations == min((11 * beam + 9) // 10, 1024)
+        seen = [float(((base[0] - q[qi]) ** 2).sum())]
+        for t in tr:
+            seen += [t.cand_dist[i] for i in range(32) if t.cand_idx[i] != 0xFFFFFFFF]
+        got = np.sort(((base[out.astype(np.int64)] - q[qi]) ** 2).sum(-1))
+        assert np.array_equal(got, np.sort(np.asarray(seen, np.float32))[:K]), (beam, qi)
