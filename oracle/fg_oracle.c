@@ -26,12 +26,25 @@
  *                                of compare-exchange on tiny inputs
  *   merges                       vs heapq.merge / sorted() on distinct keys
  *   hash                         set semantics vs a Python set
- *   pick / keep / controller     hand-computed cases
+ *   pick / keep counts           hand-computed cases
+ *   controller, K-th cutoff      hand-computed trajectories of the exported
+ *                                fgo_controller_step / fgo_record_expander /
+ *                                fgo_kth_cutoff (test_oracle_traces.py)
+ *   loop order                   hand-traced searches over hand-built
+ *                                codebooks (tests/crafted.py): cutoff and
+ *                                `<=` near count in both stages, the switch
+ *                                to stage II and its keep rule, the visited
+ *                                set's rebuild at iteration 15 (a pending
+ *                                sibling admitted twice), max_iter and the
+ *                                final merge (a line graph whose searches run
+ *                                to the iteration limit)
  *   entry point / recall / I/O   the reference's own host headers compiled
  *                                from /root/reference (oracle/_ref)
- *   whole search                 recall vs brute-force ground truth, plus
- *                                internal invariants (sorted beam, unique
- *                                expansions, counters)
+ *   whole search                 recall vs brute-force ground truth; a
+ *                                complete graph with beam >= n returns the
+ *                                brute-force top-K exactly; internal
+ *                                invariants (sorted beam, unique expansions,
+ *                                counters)
  * Parity unpinned -- these cannot be pinned without running the reference
  * (no CUDA toolchain here), so they are the oracle's stated choices:
  *   - the fp-contraction sites (fmaf exactly where nvcc's default --fmad=true

@@ -97,7 +97,9 @@ def scenario_stage2():
     """Degree 8, beam 64, K 10: three dead-end stage-I expansions under a
     fixed top-1 (the entry), the switch to stage II on the fourth stall, and a
     stage-II round over three parents that keeps 4 children each (selected by
-    estimate, compacted in (task, lane) order)."""
+    estimate, compacted in (task, lane) order).  Parents 4 and 5 have 8 fresh
+    children; parent 6 has 5 (its other slots point at visited nodes), one
+    more than it keeps, so the keep-all shortcut must not apply."""
     dist = {0: 1}
     adj = {0: [1, 2, 3, 4, 5, 6, 7, 8]}
     for i in range(1, 9):
@@ -105,14 +107,47 @@ def scenario_stage2():
         adj[i] = [0]
     pattern = [8, 1, 7, 2, 6, 3, 5, 4]  # estimate rank of each neighbour slot
     nxt = 9
-    for p, base in ((4, 100), (5, 200), (6, 300)):
+    for p, base in ((4, 100), (5, 200)):
         kids = list(range(nxt, nxt + 8))
         nxt += 8
         adj[p] = kids
         for k, r in zip(kids, pattern):
             dist[k] = base + 10 * r
             adj[k] = [p]
+    # parent 6: fresh 25..29 at ranks 5, 1, 4, 2, 3 between visited 0, 1, 2
+    adj[6] = [25, 0, 26, 1, 27, 2, 28, 29]
+    for k, r in zip((25, 26, 27, 28, 29), (5, 1, 4, 2, 3)):
+        dist[k] = 300 + 10 * r
+        adj[k] = [6]
     return make(dist, adj, {}, degree=8)
+
+
+def scenario_stage2_cutoff():
+    """Degree 8, beam 8, K 8: stage II with a valid cutoff (beam[7]) and an
+    estimate equal to it.  Node 1's two far children (500, 510) fill the beam;
+    2 and 3 are dead ends; the fourth stall switches to stage II over parents
+    4, 5, 6, 9, of which only 4 has fresh children, estimated at 400, 500 (node
+    31, truly at 450), 600 .. 1100 against the cutoff 500."""
+    dist = {0: 1}
+    adj = {0: [1, 2, 3, 4, 5, 6, 7, 8]}
+    for i in range(1, 9):
+        dist[i] = 10 * i
+        adj[i] = [0]
+    adj[1] = [9, 10, 0]
+    dist[9], dist[10] = 500, 510
+    adj[9], adj[10] = [1], [1]
+    kids = list(range(30, 38))
+    adj[4] = kids
+    est = {}
+    for k, e in zip(kids, (400, 500, 600, 700, 800, 900, 1000, 1100)):
+        dist[k] = e
+        adj[k] = [4]
+    dist[31] = 450
+    est[(4, 31)] = 500
+    for i in range(11, 30):  # unused ids, so that 30.. exist
+        dist[i] = 5000
+        adj[i] = [0]
+    return make(dist, adj, est, degree=8)
 
 
 def scenario_reset(n: int = 40):

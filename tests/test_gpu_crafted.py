@@ -46,6 +46,7 @@ def test_line_search_at_max_iter(gpu_available, beam):
 @pytest.mark.parametrize("name,K,beam,want", [
     ("scenario_cutoff", 2, 3, [5, 9]),
     ("scenario_stage2", 10, 64, [0, 1, 2, 3, 4, 5, 6, 10, 12, 14]),
+    ("scenario_stage2_cutoff", 8, 8, [0, 1, 2, 3, 4, 5, 6, 30]),
     ("scenario_reset", 16, 16, [36, 35, 34, 33, 32, 31, 30, 29, 29, 28, 27, 26, 25, 24, 23, 22]),
 ])
 def test_hand_traced_scenarios(gpu_available, name, K, beam, want):

@@ -171,30 +171,57 @@ def test_trace_stage2_switch_and_keep():
             progress is negative (expanders get farther), so the rate stays 0.25.
       it 4: fourth stall: theta 8, rate 0.5.  The unexpanded entries are 4, 5,
             6: three tasks.  Keep min(ceil(8 * 0.5), 32 / 8) = 4 per parent.
-            Each parent's slots hold estimate ranks 8 1 7 2 6 3 5 4, so the
-            kept lanes are 1, 3, 5, 7 and the list, in (task, lane) order,
-            is 10 12 14 16 | 18 20 22 24 | 26 28 30 32 (distances base + 10,
-            + 20, + 30, + 40 for bases 100, 200, 300).
-      it 5: the first 8 of those 12 in beam order; it 6: the other 4; it 7
-            finds nothing to expand.
+            The slots of 4 and 5 hold estimate ranks 8 1 7 2 6 3 5 4, so their
+            kept lanes are 1, 3, 5, 7: 10 12 14 16 | 18 20 22 24 (distances
+            base + 10 .. + 40 for bases 100, 200).  Parent 6 has 5 fresh
+            children (ranks 5 1 4 2 3 in slots 0 2 4 6 7): 5 > 4, so all 5 are
+            estimated and the four best kept, listed in lane order 26 27 28 29
+            (310, 340, 320, 330).
+      it 5: the first 8 of those 12 in beam order; it 6: the other 4 in beam
+            order (26, 28, 29, 27); it 7 finds nothing to expand.
     Counters: 7 iterations, 1+1+1+1+3+8+4 = 19 expansions, 4 * 8 + 24 + 64 +
-    32 = 152 ids, 8 + 24 estimates, 1 + 6 + 12 exact distances, stage II
-    from iteration 4."""
+    32 = 152 ids, 8 + 8 + 8 + 5 estimates, 1 + 6 + 12 exact distances, stage
+    II from iteration 4."""
     cb, q = crafted.scenario_stage2()
     out, cnt, tr = _trace(cb, q, 10, 64)
     assert out == [0, 1, 2, 3, 4, 5, 6, 10, 12, 14]
-    assert cnt == (7, 19, 152, 32, 19, 4)
+    assert cnt == (7, 19, 152, 29, 19, 4)
     assert [t["theta"] for t in tr] == [1, 1, 1, 1, 8, 8, 8]
     assert [t["stall"] for t in tr] == [0, 1, 2, 3, 4, 5, 6]
     assert np.allclose([t["rho"] for t in tr], [0.25] * 4 + [0.5] * 3)
     assert [t["parents"] for t in tr] == [[0], [1], [2], [3], [4, 5, 6],
-                                         [10, 12, 14, 16, 18, 20, 22, 24], [26, 28, 30, 32]]
+                                         [10, 12, 14, 16, 18, 20, 22, 24], [26, 28, 29, 27]]
     assert tr[0]["cand"] == [1, 2, 3, 4, 5, 6]
-    assert tr[4]["cand"] == [10, 12, 14, 16, 18, 20, 22, 24, 26, 28, 30, 32]
-    assert tr[4]["cdist"] == [110, 120, 130, 140, 210, 220, 230, 240, 310, 320, 330, 340]
+    assert tr[4]["cand"] == [10, 12, 14, 16, 18, 20, 22, 24, 26, 27, 28, 29]
+    assert tr[4]["cdist"] == [110, 120, 130, 140, 210, 220, 230, 240, 310, 340, 320, 330]
     assert all(t["kth"] == FLT_MAX for t in tr)
     # the last selected expander's distance is the one recorded
     assert (tr[4]["cur"], tr[5]["cur"], tr[6]["cur"]) == (60.0, 240.0, 340.0)
+
+
+def test_trace_stage2_cutoff_near_count():
+    """Degree 8, beam 8 (max_iter 9), K 8: the cutoff is beam[7].
+      it 0: expand 0 (top-1 for good): 1 .. 6 scored (keep 6 of 8).
+      it 1: beam [0 .. 6] is not full.  Expand 1: its two children 9 (500)
+            and 10 (510) are both kept (2 <= 6).
+      it 2: beam [0 .. 6, 9] is full: cutoff 500.  2 and 3 (it 3) are dead ends.
+      it 4: fourth stall, stage II over the unexpanded 4, 5, 6, 9.  Only 4 has
+            fresh children, estimated 400, 500, 600 .. 1100: near count
+            (estimate <= 500) 2, so min(2, 4) = 2 are kept: 30 (400) and 31
+            (estimated 500, truly 450).
+      it 5: beam [0 .. 6, 30] (31 and 9 fall out), cutoff 400; expand 30, a
+            dead end; it 6 finds nothing to expand.
+    Counters: 6 iterations, 1+1+1+1+4+1 = 9 expansions, 4 * 8 + 4 * 8 + 8 = 72
+    ids, 8 + 8 estimates, 1 + 6 + 2 + 2 exact distances."""
+    cb, q = crafted.scenario_stage2_cutoff()
+    out, cnt, tr = _trace(cb, q, 8, 8)
+    assert out == [0, 1, 2, 3, 4, 5, 6, 30]
+    assert cnt == (6, 9, 72, 16, 11, 4)
+    assert [t["parents"] for t in tr] == [[0], [1], [2], [3], [4, 5, 6, 9], [30]]
+    assert [t["kth"] for t in tr] == [FLT_MAX, FLT_MAX, 500.0, 500.0, 500.0, 400.0]
+    assert [t["cand"] for t in tr] == [[1, 2, 3, 4, 5, 6], [9, 10], [], [], [30, 31], []]
+    assert tr[4]["cdist"] == [400.0, 450.0]
+    assert [t["theta"] for t in tr] == [1, 1, 1, 1, 8, 8]
 
 
 def test_trace_reset_readmits_pending_sibling():
