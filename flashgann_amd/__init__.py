@@ -97,9 +97,18 @@ class Index:
     def entry(self) -> int:
         return int(self.info.entry)
 
+    def _host_queries(self, queries) -> np.ndarray:
+        """(nq, dim) float32 C-contiguous; a single 1-D query becomes (1, dim)."""
+        q = np.ascontiguousarray(queries, dtype=np.float32)
+        if q.ndim == 1:
+            q = q.reshape(1, -1)
+        if q.ndim != 2 or q.shape[1] != int(self.info.dim):
+            raise ValueError(f"queries must have shape (nq, {int(self.info.dim)}), got {tuple(np.shape(queries))}")
+        return q
+
     def search(self, queries: np.ndarray, K: int, beam: int, counters: bool = False):
         """Host queries in, host ids out.  Returns (ids, Stats, counters|None)."""
-        q = np.ascontiguousarray(queries, dtype=np.float32)
+        q = self._host_queries(queries)
         nq = q.shape[0]
         out = np.zeros((nq, K), dtype=np.uint32)
         cnt = np.zeros((nq, FG_COUNTERS_PER_QUERY), dtype=np.uint32) if counters else None
@@ -133,7 +142,7 @@ class Index:
                                       C.c_void_p(stream or None)))
 
     def query_prepare(self, queries: np.ndarray):
-        q = np.ascontiguousarray(queries, dtype=np.float32)
+        q = self._host_queries(queries)
         nq, b = q.shape[0], int(self.info.padded_dim)
         rot = np.zeros((nq, b), dtype=np.float32)
         qt = np.zeros((nq, b), dtype=np.uint8)
@@ -145,7 +154,7 @@ class Index:
         return rot, qt, lhw, sq
 
     def score_edges(self, queries: np.ndarray, query_ix, parents, slots):
-        q = np.ascontiguousarray(queries, dtype=np.float32)
+        q = self._host_queries(queries)
         qi = np.ascontiguousarray(query_ix, dtype=np.uint32)
         pa = np.ascontiguousarray(parents, dtype=np.uint32)
         sl = np.ascontiguousarray(slots, dtype=np.uint32)

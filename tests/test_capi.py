@@ -62,3 +62,20 @@ def test_search_stream_rejects_null_index():
     L = _lib.lib()
     rc = L.fg_search_stream(None, None, 0, 10, 64, None, 16, 2, None)
     assert rc == _lib.FG_EINVAL and b"NULL" in L.fg_last_error()
+
+
+def test_index_query_shape_checks():
+    """Host queries must be (nq, dim); one 1-D query becomes (1, dim).  The
+    check runs before any library call (a wrong shape would otherwise make
+    fg_search read past the host buffer)."""
+    import pytest
+    from flashgann_amd import Index
+    from flashgann_amd._lib import IndexInfo
+    ix = Index.__new__(Index)
+    ix._h = None
+    ix.info = IndexInfo(dim=128)
+    assert ix._host_queries(np.zeros(128, np.float32)).shape == (1, 128)
+    assert ix._host_queries(np.zeros((3, 128), np.float64)).dtype == np.float32
+    for bad in (np.zeros(96, np.float32), np.zeros((3, 64), np.float32), np.zeros((2, 3, 128), np.float32)):
+        with pytest.raises(ValueError):
+            ix._host_queries(bad)
