@@ -106,15 +106,19 @@ class Index:
             raise ValueError(f"queries must have shape (nq, {int(self.info.dim)}), got {tuple(np.shape(queries))}")
         return q
 
-    def search(self, queries: np.ndarray, K: int, beam: int, counters: bool = False):
-        """Host queries in, host ids out.  Returns (ids, Stats, counters|None)."""
+    def search(self, queries: np.ndarray, K: int, beam: int, counters: bool = False, noalloc: bool = False):
+        """Host queries in, host ids out.  Returns (ids, Stats, counters|None).
+        noalloc=True calls fg_search_noalloc (staging in the library's fixed
+        per-device area, no device allocation; at most
+        FG_NOALLOC_STAGING_BYTES of staging per call)."""
         q = self._host_queries(queries)
         nq = q.shape[0]
         out = np.zeros((nq, K), dtype=np.uint32)
         cnt = np.zeros((nq, FG_COUNTERS_PER_QUERY), dtype=np.uint32) if counters else None
         st = Stats()
-        check(lib().fg_search(self._h, _fptr(q), nq, K, beam, _uptr(out),
-                              _uptr(cnt) if cnt is not None else None, C.byref(st)))
+        fn = lib().fg_search_noalloc if noalloc else lib().fg_search
+        check(fn(self._h, _fptr(q), nq, K, beam, _uptr(out), _uptr(cnt) if cnt is not None else None,
+                 C.byref(st)))
         return out, st, cnt
 
     def search_device(self, queries_ptr: int, nq: int, K: int, beam: int, results_ptr: int,

@@ -20,9 +20,10 @@ FG_METRIC_IP = 1
 FG_ENTRY_AUTO = 0xFFFFFFFF
 FG_COUNTERS_PER_QUERY = 6
 FG_PROFILE_SLOTS = 12
+FG_NOALLOC_STAGING_BYTES = 16 << 20
 
 EXPORTED = (
-    "fg_index_create", "fg_index_load", "fg_index_destroy", "fg_index_get_info", "fg_search",
+    "fg_index_create", "fg_index_load", "fg_index_destroy", "fg_index_get_info", "fg_search", "fg_search_noalloc",
     "fg_search_device", "fg_search_stream", "fg_search_profile", "fg_lds_bytes", "fg_query_prepare", "fg_score_edges", "fg_last_error",
     "fg_version",
 )
@@ -69,6 +70,7 @@ def lib():
         L.fg_index_get_info.argtypes = [vp, C.POINTER(IndexInfo)]
         L.fg_search.argtypes = [vp, f32p, C.c_uint32, C.c_uint32, C.c_uint32, u32p, u32p,
                                 C.POINTER(Stats)]
+        L.fg_search_noalloc.argtypes = L.fg_search.argtypes
         L.fg_search_device.argtypes = [vp, vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp, vp]
         L.fg_search_profile.argtypes = [vp, vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp, vp]
         L.fg_search_stream.argtypes = [vp, vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, C.c_uint32, C.c_uint32, vp]

@@ -28,6 +28,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <fstream>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -1995,6 +1996,14 @@ __global__ __launch_bounds__(64) void fg_score_kernel(ScoreParams S) {
 
 // ================================================================== host side
 
+// Staging area of fg_search_noalloc: the device copies of one call's queries,
+// result ids and counters, at 256-byte aligned offsets.  Each device holds
+// its own copy until the process ends.  In host code `scratch` names a
+// host-side stand-in, not device memory: its device address comes from
+// hipGetSymbolAddress (noalloc_staging), and only that address is passed to
+// kernels and copies.
+static __device__ __align__(256) unsigned char scratch[FG_NOALLOC_STAGING_BYTES];
+
 struct fg_index {
     int device = 0;
     float *d_rows = nullptr;
@@ -2012,6 +2021,8 @@ struct fg_index {
     uint32_t *d_cnt = nullptr;
     size_t cnt_cap = 0;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    // this device's staging area of fg_search_noalloc (device address)
+    unsigned char *noalloc = nullptr;
     // serving streams of fg_search_stream (created on first use, default priority)
     static constexpr int kMaxServeStreams = 8;
     hipStream_t serve[kMaxServeStreams] = {};
@@ -2086,6 +2097,27 @@ uint32_t host_entry_point(const float *rows, uint64_t n, uint32_t dim, uint64_t 
     }
     return best;
 }
+
+// Device address of `scratch` on `device` (which must be current), resolved
+// once per device and kept for the life of the process.
+constexpr int kMaxDevices = 64;
+std::mutex g_staging_mu;
+unsigned char *g_staging[kMaxDevices] = {};
+
+int noalloc_staging(int device, unsigned char **out) {
+    std::lock_guard<std::mutex> lock(g_staging_mu);
+    if (device < 0 || device >= kMaxDevices) return fail(FG_EDEVICE, "device ordinal out of range");
+    if (!g_staging[device]) {
+        void *p = nullptr;
+        FG_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "address of the fg_search_noalloc staging area");
+        if (!p) return fail(FG_EDEVICE, "address of the fg_search_noalloc staging area is NULL");
+        g_staging[device] = static_cast<unsigned char *>(p);
+    }
+    *out = g_staging[device];
+    return FG_OK;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
 int ensure(void **p, size_t *cap, size_t need) {
     if (*cap >= need) return FG_OK;
@@ -2252,6 +2284,11 @@ int fg_index_create(const float *rows, uint64_t npoints, uint32_t dim, uint32_t 
         delete ix;
         return fail(FG_ENOMEM, "QG upload exceeds currently available GPU memory");
     }
+    // set-up of fg_search_noalloc on this device (current here)
+    if (int rc = noalloc_staging(ix->device, &ix->noalloc)) {
+        delete ix;
+        return rc;
+    }
     if (hipMalloc(&ix->d_rows, bytes) != hipSuccess || hipMalloc(&ix->d_signs, ix->padded_dim * sizeof(float)) != hipSuccess) {
         fg_index_destroy(ix);
         return fail(FG_ENOMEM, "hipMalloc of the codebook failed");
@@ -2396,31 +2433,23 @@ int fg_search_profile(fg_index *ix, const float *d_queries, uint32_t nq, uint32_
     return launch_t<true>(P, reinterpret_cast<hipStream_t>(stream));
 }
 
-int fg_search(fg_index *ix, const float *queries, uint32_t nq, uint32_t K, uint32_t beam, uint32_t *result_ids,
-              uint32_t *counters, fg_stats *stats) {
-    if (!ix) return fail(FG_EINVAL, "index is NULL");
-    if (nq && (!queries || !result_ids)) return fail(FG_EINVAL, "NULL host buffer");
-    SearchParams P;
-    if (int rc = make_params(ix, nq, K, beam, P)) return rc;
-    if (stats) {
-        stats->elapsed_s = 0.0;
-        stats->kernel_ms = 0.0f;
-        stats->lds_bytes = P.lds.total;
-        stats->visited_slots = 4u * static_cast<uint32_t>(P.buckets);
-    }
-    if (nq == 0) return FG_OK;
+}  // extern "C"
+
+namespace {
+
+// Host-buffer search of fg_search / fg_search_noalloc: the queries are copied
+// into `dq`, the kernel runs on the null stream, and the ids (and counters)
+// are copied back from `dres` (`dcnt`).
+int search_host(fg_index *ix, SearchParams &P, const float *queries, uint32_t nq, uint32_t K, uint32_t *result_ids,
+                uint32_t *counters, fg_stats *stats, float *dq, uint32_t *dres, uint32_t *dcnt) {
     const size_t qb = static_cast<size_t>(nq) * ix->dim * sizeof(float);
     const size_t rb = static_cast<size_t>(nq) * K * sizeof(uint32_t);
     const size_t cb = static_cast<size_t>(nq) * FG_COUNTERS_PER_QUERY * sizeof(uint32_t);
-    if (int rc = ensure(reinterpret_cast<void **>(&ix->d_q), &ix->q_cap, qb)) return rc;
-    if (int rc = ensure(reinterpret_cast<void **>(&ix->d_res), &ix->res_cap, rb)) return rc;
-    if (counters)
-        if (int rc = ensure(reinterpret_cast<void **>(&ix->d_cnt), &ix->cnt_cap, cb)) return rc;
-    FG_HIP(hipMemcpy(ix->d_q, queries, qb, hipMemcpyHostToDevice), "query upload");
+    FG_HIP(hipMemcpy(dq, queries, qb, hipMemcpyHostToDevice), "query upload");
     FG_HIP(hipDeviceSynchronize(), "sync before search");
-    P.queries = ix->d_q;
-    P.results = ix->d_res;
-    P.counters = counters ? ix->d_cnt : nullptr;
+    P.queries = dq;
+    P.results = dres;
+    P.counters = counters ? dcnt : nullptr;
     P.phase = nullptr;
     const auto t0 = std::chrono::high_resolution_clock::now();
     FG_HIP(hipEventRecord(ix->ev0, nullptr), "event record");
@@ -2433,9 +2462,61 @@ int fg_search(fg_index *ix, const float *queries, uint32_t nq, uint32_t K, uint3
         float ms = 0.0f;
         if (hipEventElapsedTime(&ms, ix->ev0, ix->ev1) == hipSuccess) stats->kernel_ms = ms;
     }
-    FG_HIP(hipMemcpy(result_ids, ix->d_res, rb, hipMemcpyDeviceToHost), "result download");
-    if (counters) FG_HIP(hipMemcpy(counters, ix->d_cnt, cb, hipMemcpyDeviceToHost), "counter download");
+    FG_HIP(hipMemcpy(result_ids, dres, rb, hipMemcpyDeviceToHost), "result download");
+    if (counters) FG_HIP(hipMemcpy(counters, dcnt, cb, hipMemcpyDeviceToHost), "counter download");
     return FG_OK;
+}
+
+int search_prologue(fg_index *ix, const float *queries, uint32_t nq, uint32_t K, uint32_t beam, uint32_t *result_ids,
+                    fg_stats *stats, SearchParams &P) {
+    if (!ix) return fail(FG_EINVAL, "index is NULL");
+    if (nq && (!queries || !result_ids)) return fail(FG_EINVAL, "NULL host buffer");
+    if (int rc = make_params(ix, nq, K, beam, P)) return rc;
+    if (stats) {
+        stats->elapsed_s = 0.0;
+        stats->kernel_ms = 0.0f;
+        stats->lds_bytes = P.lds.total;
+        stats->visited_slots = 4u * static_cast<uint32_t>(P.buckets);
+    }
+    return FG_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fg_search(fg_index *ix, const float *queries, uint32_t nq, uint32_t K, uint32_t beam, uint32_t *result_ids,
+              uint32_t *counters, fg_stats *stats) {
+    SearchParams P;
+    if (int rc = search_prologue(ix, queries, nq, K, beam, result_ids, stats, P)) return rc;
+    if (nq == 0) return FG_OK;
+    const size_t qb = static_cast<size_t>(nq) * ix->dim * sizeof(float);
+    const size_t rb = static_cast<size_t>(nq) * K * sizeof(uint32_t);
+    const size_t cb = static_cast<size_t>(nq) * FG_COUNTERS_PER_QUERY * sizeof(uint32_t);
+    if (int rc = ensure(reinterpret_cast<void **>(&ix->d_q), &ix->q_cap, qb)) return rc;
+    if (int rc = ensure(reinterpret_cast<void **>(&ix->d_res), &ix->res_cap, rb)) return rc;
+    if (counters)
+        if (int rc = ensure(reinterpret_cast<void **>(&ix->d_cnt), &ix->cnt_cap, cb)) return rc;
+    return search_host(ix, P, queries, nq, K, result_ids, counters, stats, ix->d_q, ix->d_res, ix->d_cnt);
+}
+
+int fg_search_noalloc(fg_index *ix, const float *queries, uint32_t nq, uint32_t K, uint32_t beam,
+                      uint32_t *result_ids, uint32_t *counters, fg_stats *stats) {
+    SearchParams P;
+    if (int rc = search_prologue(ix, queries, nq, K, beam, result_ids, stats, P)) return rc;
+    if (nq == 0) return FG_OK;
+    // staging: queries, then result ids, then counters, each 256-byte aligned
+    const size_t qb = align256(static_cast<size_t>(nq) * ix->dim * sizeof(float));
+    const size_t rb = align256(static_cast<size_t>(nq) * K * sizeof(uint32_t));
+    const size_t cb = counters ? align256(static_cast<size_t>(nq) * FG_COUNTERS_PER_QUERY * sizeof(uint32_t)) : 0;
+    if (qb + rb + cb > FG_NOALLOC_STAGING_BYTES)
+        return fail(FG_EINVAL, "fg_search_noalloc: " + std::to_string(nq) + " queries need " +
+                                   std::to_string(qb + rb + cb) + " bytes of staging, above its maximum of " +
+                                   std::to_string(FG_NOALLOC_STAGING_BYTES) + " (use fewer queries per call)");
+    if (!ix->noalloc) return fail(FG_EDEVICE, "fg_search_noalloc: staging area not set up");
+    unsigned char *base = ix->noalloc;
+    return search_host(ix, P, queries, nq, K, result_ids, counters, stats, reinterpret_cast<float *>(base),
+                       reinterpret_cast<uint32_t *>(base + qb), reinterpret_cast<uint32_t *>(base + qb + rb));
 }
 
 int fg_query_prepare(fg_index *ix, const float *queries, uint32_t nq, float *rotated, uint8_t *quantized,

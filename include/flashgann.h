@@ -102,6 +102,23 @@ int fg_index_get_info(const fg_index *index, fg_index_info *info);
 int fg_search(fg_index *index, const float *queries, uint32_t nq, uint32_t K, uint32_t beam,
               uint32_t *result_ids, uint32_t *counters, fg_stats *stats);
 
+/* Allocation-free variant of fg_search.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory while they search (tight
+ * serving loops, harnesses that forbid hipMalloc).  Same arguments, results,
+ * counters and statistics as fg_search, but the device copies of the queries,
+ * result ids and counters are staged in a fixed area of
+ * FG_NOALLOC_STAGING_BYTES that the library holds on each device until the
+ * process ends (set up by fg_index_create), instead of buffers it allocates;
+ * the call itself allocates nothing.  A call needs
+ * align256(nq*dim*4) + align256(nq*K*4) [+ align256(nq*24) with counters]
+ * bytes of it and is rejected with FG_EINVAL above the maximum (about 17,900
+ * queries at dim 128, K 100, with counters).  Every call on one device
+ * shares that area: calls that overlap on one device race, so issue them from
+ * one host thread at a time per device. */
+#define FG_NOALLOC_STAGING_BYTES (16u << 20)
+int fg_search_noalloc(fg_index *index, const float *queries, uint32_t nq, uint32_t K, uint32_t beam,
+                      uint32_t *result_ids, uint32_t *counters, fg_stats *stats);
+
 /* Device-resident variant: d_queries, d_results (and d_counters, may be NULL)
  * are device pointers; the kernel is enqueued on `stream` (a hipStream_t, NULL
  * = default stream) and the call returns without synchronising.  This is the
