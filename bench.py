@@ -71,8 +71,18 @@ def main() -> int:
     ap.add_argument("--beam", type=int, default=0, help="skip the sweep and use this beam")
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="CPU-oracle work budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle (baseline and id checks)")
-    ap.add_argument("--full-sweep", action="store_true",
-                    help="time every beam of --beams instead of stopping at the first that reaches the target")
+    ap.add_argument("--stop-at-target", action="store_true",
+                    help="end the beam sweep at the first beam that reaches the target recall (default: sweep every "
+                         "beam of --beams for recall, QPS and oracle parity; the headline is the first beam that "
+                         "reaches the target either way)")
+    ap.add_argument("--full-sweep", action="store_true", help="(the default; kept for old command lines)")
+    ap.add_argument("--graph", type=str, default="mixed", choices=("mixed", "rng"),
+                    help="mixed: RNG-pruned k-NN edges plus degree/4 seeded random long links, empty slots to "
+                         "random targets (the default); rng: RNG-pruned k-NN edges only, empty slots backfilled "
+                         "from the k-NN candidates")
+    ap.add_argument("--no-rng-graph", action="store_true",
+                    help="skip the side measurement on the RNG-only graph (default: C2 with the mixed graph also "
+                         "sweeps the RNG-only graph and reports it in config.rng_graph)")
     ap.add_argument("--parity-sample", type=int, default=500,
                     help="queries per swept beam whose GPU ids are compared with the CPU oracle's")
     ap.add_argument("--traffic", type=str, default=os.path.join(ROOT, "profiles", "search_c2_traffic.json"))
@@ -115,7 +125,9 @@ def main() -> int:
     signs = datasets.signs_for(B, conf["cfg"])
     log(f"data {args.n}x{dim} + {args.nq} queries in {time.time() - t0:.1f}s")
     use_ip = args.metric == "ip"
-    tag = f"{args.config}_{args.n}_{args.nq}_{args.components}_{args.degree}_{args.K}" + ("_ip" if use_ip else "")
+    tag = (f"{args.config}_{args.n}_{args.nq}_{args.components}_{args.degree}_{args.K}" + ("_ip" if use_ip else "")
+           + ("_rng" if args.graph == "rng" else ""))
+    graph_kw = dict(random_links=0, fill_random=False) if args.graph == "rng" else {}
     cb_path = os.path.join(args.cache, tag + ".index") if args.cache else ""
     gt_path = os.path.join(args.cache, tag + ".gt.npy") if args.cache else ""
     if cb_path and os.path.exists(cb_path) and os.path.exists(gt_path):
@@ -124,7 +136,7 @@ def main() -> int:
         log(f"codebook and ground truth loaded from {args.cache}")
     else:
         t0 = time.time()
-        cb = builder.build_codebook(base, args.degree, signs, use_ip=use_ip, device=dev)
+        cb = builder.build_codebook(base, args.degree, signs, use_ip=use_ip, device=dev, **graph_kw)
         log(f"codebook built on GPU in {time.time() - t0:.1f}s (entry {cb.entry})")
         t0 = time.time()
         gt = builder.ground_truth(base, queries, args.K, device=dev, use_ip=use_ip)
@@ -162,8 +174,19 @@ def main() -> int:
     # Oracle handle for the per-beam id checks (bounded samples) and the CPU
     # baseline; built once.
     oix = None
-    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    threads = max(1, min(threads or 1, 16))
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    # the host's CPU share for this GPU: the affinity set, bounded by the
+    # thread count the host configures for its jobs (OMP_NUM_THREADS)
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    threads = max(1, min(affinity, share) if share > 0 else affinity)
+    cpu_model = ""
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                cpu_model = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
     if not args.no_cpu:
         from oracle import oracle as O
         oix = O.OracleIndex.from_codebook(cb, use_ip=use_ip)
@@ -202,7 +225,7 @@ def main() -> int:
                if "oracle_sample" in row else ""))
         if chosen is None and r >= args.target_recall:
             chosen = beam
-            if not args.full_sweep:
+            if args.stop_at_target:
                 break
     if chosen is None:
         chosen = beams[-1]
@@ -316,14 +339,58 @@ def main() -> int:
         oix.search(queries[:one], args.K, chosen, threads=1)
         one_qps = one / (time.perf_counter() - t1)
         cpu = {"value": round(sample / cpu_s, 1), "unit": "queries/s", "cores": threads, "kind": "port",
-               "sample": f"first {sample} of the {args.nq} C2 queries at beam {chosen}, "
+               "sample": f"first {sample} of the {args.nq} {args.config.upper()} queries at beam {chosen}, "
                          f"{threads} host threads, {cpu_s:.1f} s wall",
-               "ids_identical_to_gpu": same, "single_thread_value": round(one_qps, 1)}
+               "ids_identical_to_gpu": same, "single_thread_value": round(one_qps, 1),
+               "cpu_model": cpu_model, "affinity_cpus": affinity, "os_cpu_count": os.cpu_count(),
+               "omp_num_threads": share or None}
         log(f"cpu oracle: {sample / cpu_s:.0f} QPS on {threads} threads; ids identical on {same * 100:.2f}% "
             f"of the sample")
 
+    # Side measurement (never `value`): the same data on an RNG-only graph
+    # (RNG-pruned k-NN edges, no random long links), swept over the same beams.
+    rng_graph = None
+    if args.config == "c2" and args.graph == "mixed" and not args.no_rng_graph and not use_ip:
+        t0 = time.time()
+        cb_r = builder.build_codebook(base, args.degree, signs, device=dev, random_links=0, fill_random=False)
+        log(f"RNG-only graph built in {time.time() - t0:.1f}s")
+        ix_r = fg.Index.from_codebook(cb_r)
+        oix_r = O.OracleIndex.from_codebook(cb_r) if oix is not None else None
+        rows = []
+        for beam in beams:
+            ix_r.search_device(dq.data_ptr(), args.nq, args.K, beam, dres.data_ptr(), 0, stream.cuda_stream)
+            torch.cuda.synchronize()
+            ms = []
+            for _ in range(3):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                ix_r.search_device(dq.data_ptr(), args.nq, args.K, beam, dres.data_ptr(), 0, stream.cuda_stream)
+                e1.record(stream)
+                torch.cuda.synchronize()
+                ms.append(e0.elapsed_time(e1))
+            rids = dres.cpu().numpy().view(np.uint32)
+            row = {"beam": beam, "recall": round(float(recall_of(rids)), 5),
+                   "qps": round(args.nq / (min(ms) / 1e3), 1), "kernel_ms": round(min(ms), 4)}
+            if oix_r is not None and args.parity_sample > 0:
+                m = min(args.nq, args.parity_sample)
+                pids, _ = oix_r.search(queries[:m], args.K, beam, threads=threads)
+                row["oracle_ids_identical"] = float((pids == rids[:m]).all(1).mean())
+                row["oracle_sample"] = m
+            rows.append(row)
+            log(f"RNG-only graph, beam {beam}: recall@{args.K} {row['recall']:.4f}, {row['qps']:.0f} QPS"
+                + (f", ids identical to the oracle on {row['oracle_ids_identical'] * 100:.2f}% of "
+                   f"{row['oracle_sample']}" if "oracle_sample" in row else ""))
+        first = next((r["beam"] for r in rows if r["recall"] >= args.target_recall), None)
+        rng_graph = {"graph": "RNG-pruned k-NN edges only (random_links=0, empty slots backfilled from the "
+                              "k-NN candidates)", "beam_sweep": rows, "first_beam_reaching_target": first}
+        ix_r.close()
+        del cb_r, oix_r
+
+    graph_desc = ("RNG-pruned k-NN edges only, empty slots backfilled from the k-NN candidates" if args.graph == "rng"
+                  else f"RNG-pruned exact k-NN edges (2*degree candidates) plus {args.degree // 4} seeded random "
+                       "long links per node, empty slots to random targets")
     line = {
-        "metric": ("queries/sec at recall@100>=0.95 (1M x 128 fp32, deg 32)" if args.config == "c2" and not use_ip
+        "metric":("queries/sec at recall@100>=0.95 (1M x 128 fp32, deg 32)" if args.config == "c2" and not use_ip
                    else f"queries/sec at recall@{args.K}>={args.target_recall} ({args.n} x {dim} fp32, deg {args.degree}"
                         f"{', inner product' if use_ip else ''})"),
         "value": round(qps, 1),
@@ -342,7 +409,8 @@ def main() -> int:
                                f"beam={chosen}" + (", inner product" if use_ip else ""),
                    "beam": chosen, "recall": round(float(recall), 5), "beam_sweep": sweep,
                    "host_buffers_qps": round(host_qps, 1), "work_per_query": work, "serving": serving,
-                   "lds_bytes": fg.lds_bytes(dim, chosen, args.degree)},
+                   "lds_bytes": fg.lds_bytes(dim, chosen, args.degree), "graph": graph_desc,
+                   "rng_graph": rng_graph},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "fg_search_kernel", "kernel_ms": round(kernel_ms, 4),

@@ -3,6 +3,8 @@ work counters must be identical: integer data makes every distance exact,
 and the oracle fixes the same tie and race resolution)."""
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 
@@ -48,6 +50,17 @@ def test_search_float_unit_vectors(gpu_available):
     cb, q, _ = small_index(n=3000, dim=96, comps=32, kind="unit")
     ids, cnt, rids, rcnt = _run(cb, q, 10, 64)
     _assert_equal(ids, cnt, rids, rcnt, "unit96")
+
+
+@pytest.mark.parametrize("degree,K,beam", [(16, 10, 64), (16, 100, 256), (16, 100, 512), (32, 100, 256),
+                                           (32, 100, 512)])
+def test_search_c3_shapes(gpu_available, degree, K, beam):
+    """C3's shapes on float data against the oracle: 96-d unit vectors
+    (padded 128) with degree-16 and degree-32 graphs, each through its
+    fixed-geometry kernel, at K = 10 and K = 100 and merge-path beams."""
+    cb, q, _ = small_index(n=4000, nq=32, dim=96, comps=32, degree=degree, kind="unit")
+    ids, cnt, rids, rcnt = _run(cb, q, K, beam)
+    _assert_equal(ids, cnt, rids, rcnt, f"unit96 degree {degree} K={K} beam={beam}")
 
 
 def test_search_inner_product(gpu_available):
@@ -179,11 +192,22 @@ def test_search_inner_product_generic(gpu_available):
     _assert_equal(ids, cnt, rids, rcnt, "ip300")
 
 
-def test_cli_end_to_end(gpu_available, tmp_path):
-    """The gpu_flashgann CLI (main.cu's interface) on files written in the
-    reference's formats: printed recall equals the oracle's recall of the
-    same search, and the CSV row has the reference's columns."""
-    import os
+_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+_CLIS = {
+    # this build's CLI (main.cu's interface on qg_host.hpp)
+    "gpu_flashgann": os.path.join(_ROOT, "flashgann_amd", "bin", "gpu_flashgann"),
+    # the reference's own main.cu, unchanged, linked with this build's
+    # replacement of gpu_search_adaptive.cu (built by `make -C oracle ref`
+    # where the reference tree exists; the binary travels with the tree)
+    "reference_main": os.path.join(_ROOT, "oracle", "_ref", "gpu_flashgann_ref"),
+}
+
+
+@pytest.mark.parametrize("cli_name", sorted(_CLIS))
+def test_cli_end_to_end(gpu_available, tmp_path, cli_name):
+    """A CLI with main.cu's interface on files written in the reference's
+    formats: printed recall equals the oracle's recall of the same search,
+    and the CSV row has the reference's columns."""
     import re
     import subprocess
     from flashgann_amd import builder
@@ -197,8 +221,9 @@ def test_cli_end_to_end(gpu_available, tmp_path):
     write_fvecs(paths["query.fvecs"], q)
     write_ivecs(paths["gt.ivecs"], gt)
     cb.save(paths["cb.index"])
-    cli = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "flashgann_amd", "bin",
-                       "gpu_flashgann")
+    cli = _CLIS[cli_name]
+    if not os.path.exists(cli):
+        pytest.skip(f"{cli} not built (the reference tree was absent at build time)")
     r = subprocess.run([cli, paths["base.fvecs"], paths["query.fvecs"], paths["gt.ivecs"], paths["cb.index"],
                         "10", "64", "32", "-csv", paths["out.csv"]], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stderr
@@ -229,6 +254,9 @@ def test_search_stream_matches_single_launch(gpu_available, batch, nstreams):
     got = out.cpu()  # ordered after the batches on the caller's stream
     assert torch.equal(got, ref.cpu())
     ix.close()
+    from oracle import oracle as O
+    oids, _ = O.OracleIndex.from_codebook(cb).search(q, 100, 128)
+    assert np.array_equal(got.numpy().view(np.uint32), oids)
 
 
 @pytest.mark.parametrize("dim,degree,kind", [(128, 32, "int"), (96, 32, "unit"), (96, 16, "unit")])
