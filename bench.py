@@ -80,6 +80,12 @@ def main() -> int:
                     help="mixed: RNG-pruned k-NN edges plus degree/4 seeded random long links, empty slots to "
                          "random targets (the default); rng: RNG-pruned k-NN edges only, empty slots backfilled "
                          "from the k-NN candidates")
+    ap.add_argument("--alpha", type=float, default=1.0,
+                    help="RNG prune slack: drop a candidate v when a kept w has alpha^2 d(w,v) < d(u,v)")
+    ap.add_argument("--random-links", type=int, default=-1,
+                    help="seeded random long links per node (default: degree/4; the rng graph has none)")
+    ap.add_argument("--candidates", type=int, default=0, help="k-NN candidates per node before the prune "
+                    "(default: 2*degree)")
     ap.add_argument("--no-rng-graph", action="store_true",
                     help="skip the side measurement on the RNG-only graph (default: C2 with the mixed graph also "
                          "sweeps the RNG-only graph and reports it in config.rng_graph)")
@@ -89,8 +95,12 @@ def main() -> int:
     ap.add_argument("--cache", type=str, default="", help="directory to reuse the built index and ground truth")
     ap.add_argument("--serve-batches", type=int, default=8,
                     help="batches of nq queries in the serving measurement (0 = skip)")
+    ap.add_argument("--large", type=str, default="auto", choices=("auto", "on", "off"),
+                    help="draw the data on the GPU and build the graph from a partitioned k-NN search "
+                         "(auto: when n x dim exceeds 2^31 floats, i.e. C5 at 10M)")
     ap.add_argument("--copy-probe", action="store_true",
-                    help="also run one plain 1 GiB device copy (counter calibration for profiling)")
+                    help="also run a 1 GiB device copy, a 1 GiB elementwise kernel and a 512 MiB random-row "
+                         "gather, each of known traffic (counter calibration for profiling)")
     args = ap.parse_args()
     conf = CONFIGS[args.config]
     for key in ("n", "nq", "components", "degree", "K", "beams"):
@@ -120,14 +130,40 @@ def main() -> int:
 
     from flashgann_amd.codebook import read_codebook
 
+    # Sets too large to draw and hold on the host (C5: 10M x 1536 = 61 GB)
+    # are drawn on the GPU and get the partitioned k-NN graph; the codebook
+    # rows still land in host memory, where the CPU oracle reads them.
+    large = args.n * dim > (1 << 31) if args.large == "auto" else args.large == "on"
     t0 = time.time()
-    base, queries = getattr(datasets, conf["gen"])(args.n, args.nq, dim, args.components, config=conf["cfg"])
+    if large:
+        gen_dev = getattr(datasets, conf["gen"] + "_device", None)
+        if gen_dev is None:
+            print(f"bench.py: {args.config} has no device-side generator for a set of {args.n} x {dim}",
+                  file=sys.stderr)
+            return 2
+        base, queries_t = gen_dev(args.n, args.nq, dim, args.components, config=conf["cfg"], device=dev)
+        queries = queries_t.cpu().numpy()
+        del queries_t
+    else:
+        base, queries = getattr(datasets, conf["gen"])(args.n, args.nq, dim, args.components, config=conf["cfg"])
     signs = datasets.signs_for(B, conf["cfg"])
-    log(f"data {args.n}x{dim} + {args.nq} queries in {time.time() - t0:.1f}s")
+    log(f"data {args.n}x{dim} + {args.nq} queries in {time.time() - t0:.1f}s"
+        + (" (drawn on the GPU)" if large else ""))
+    if large:
+        graph_kw_large = dict(knn_method="partitioned", verbose=True)
+    else:
+        graph_kw_large = {}
     use_ip = args.metric == "ip"
     tag = (f"{args.config}_{args.n}_{args.nq}_{args.components}_{args.degree}_{args.K}" + ("_ip" if use_ip else "")
            + ("_rng" if args.graph == "rng" else ""))
     graph_kw = dict(random_links=0, fill_random=False) if args.graph == "rng" else {}
+    if args.random_links >= 0 and args.graph == "mixed":
+        graph_kw["random_links"] = args.random_links
+    graph_kw["alpha"] = args.alpha
+    if args.candidates:
+        graph_kw["candidates"] = args.candidates
+    if args.alpha != 1.0 or args.random_links >= 0 or args.candidates:
+        tag += f"_a{args.alpha}_r{args.random_links}_c{args.candidates}"
     cb_path = os.path.join(args.cache, tag + ".index") if args.cache else ""
     gt_path = os.path.join(args.cache, tag + ".gt.npy") if args.cache else ""
     if cb_path and os.path.exists(cb_path) and os.path.exists(gt_path):
@@ -136,11 +172,18 @@ def main() -> int:
         log(f"codebook and ground truth loaded from {args.cache}")
     else:
         t0 = time.time()
-        cb = builder.build_codebook(base, args.degree, signs, use_ip=use_ip, device=dev, **graph_kw)
+        cb = builder.build_codebook(base, args.degree, signs, use_ip=use_ip, device=dev, **graph_kw,
+                                    **graph_kw_large)
         log(f"codebook built on GPU in {time.time() - t0:.1f}s (entry {cb.entry})")
         t0 = time.time()
         gt = builder.ground_truth(base, queries, args.K, device=dev, use_ip=use_ip)
-        log(f"ground truth in {time.time() - t0:.1f}s")
+        bad = builder.check_ground_truth(base, queries, gt, sample=32, use_ip=use_ip, device=dev)
+        log(f"ground truth in {time.time() - t0:.1f}s (32 sampled queries rechecked one at a time: {bad} wrong)")
+        if bad:
+            print(f"bench.py: the ground truth failed its recheck on {bad} of 32 sampled queries", file=sys.stderr)
+            return 3
+        if large:
+            base = None  # the device copy; the codebook rows hold the vectors
         if cb_path:
             os.makedirs(args.cache, exist_ok=True)
             cb.save(cb_path)
@@ -153,7 +196,18 @@ def main() -> int:
         dst.copy_(src)
         torch.cuda.synchronize()
         log("copy probe: 1 GiB read + 1 GiB written by one device copy")
-        del src, dst
+        torch.mul(src, 2.0, out=dst)
+        torch.cuda.synchronize()
+        log("copy probe: 1 GiB read + 1 GiB written by one elementwise kernel")
+        # random 512-byte rows, the search's exact-distance access pattern:
+        # 2^20 of the 2^21 rows gathered (512 MiB read, 512 MiB written, plus
+        # the 8 MiB index)
+        perm = torch.randperm(1 << 21, device=dev)[: 1 << 20]
+        torch.cuda.synchronize()
+        g = src.view(-1, 128).index_select(0, perm)
+        torch.cuda.synchronize()
+        log("copy probe: 512 MiB of random 512-byte rows gathered by one index_select")
+        del src, dst, perm, g
 
     index = fg.Index.from_codebook(cb, metric=fg.METRIC_IP if use_ip else fg.METRIC_L2)
     dq = torch.as_tensor(queries, device=dev)
@@ -386,9 +440,14 @@ def main() -> int:
         ix_r.close()
         del cb_r, oix_r
 
-    graph_desc = ("RNG-pruned k-NN edges only, empty slots backfilled from the k-NN candidates" if args.graph == "rng"
-                  else f"RNG-pruned exact k-NN edges (2*degree candidates) plus {args.degree // 4} seeded random "
-                       "long links per node, empty slots to random targets")
+    knn_desc = ("k-NN candidates searched in the 2 nearest of ~n/2500 k-means cells" if large
+                else "exact k-NN candidates")
+    graph_desc = (f"RNG-pruned k-NN edges only ({knn_desc}), empty slots backfilled from the candidates"
+                  if args.graph == "rng"
+                  else f"RNG-pruned k-NN edges ({knn_desc}, {args.candidates or 2 * args.degree} per node"
+                       + (f", alpha {args.alpha}" if args.alpha != 1.0 else "")
+                       + f") plus {args.random_links if args.random_links >= 0 else args.degree // 4} seeded "
+                       "random long links per node, empty slots to random targets")
     line = {
         "metric":("queries/sec at recall@100>=0.95 (1M x 128 fp32, deg 32)" if args.config == "c2" and not use_ip
                    else f"queries/sec at recall@{args.K}>={args.target_recall} ({args.n} x {dim} fp32, deg {args.degree}"
@@ -403,8 +462,8 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": f"synthetic: seeded {conf['gen'].replace('_', ' ')} ({args.components} components), "
-                "graph and codes built in-run",
+        "data": f"synthetic: seeded {conf['gen'].replace('_', ' ')} ({args.components} components"
+                + (", drawn on the GPU" if large else "") + "), graph and codes built in-run",
         "config": {"workload": f"{args.config.upper()} {args.n}x{dim} deg {args.degree}, K={args.K}, nq={args.nq}, "
                                f"beam={chosen}" + (", inner product" if use_ip else ""),
                    "beam": chosen, "recall": round(float(recall), 5), "beam_sweep": sweep,

@@ -37,6 +37,8 @@ gets f = 0 and triple_x = 0.  Edges to padding get triple_x = FLT_MAX.
 """
 from __future__ import annotations
 
+import time
+
 import numpy as np
 import torch
 
@@ -55,7 +57,10 @@ def knn(base: torch.Tensor, k: int, queries: torch.Tensor | None = None,
 
     Returns (ids int64 [m,k], sqdist float32 [m,k]) ordered by (dist, id).
     Squared distances are |x|^2 + |y|^2 - 2 x.y in float32, exact for
-    integer-valued data with |.|^2 < 2^24."""
+    integer-valued data with |.|^2 < 2^24.  The distance block of one step
+    stays at `chunk_elems` floats: on this ROCm build a float32 product whose
+    output spans more than 2^31 bytes has returned wrong rows (measured: rows
+    56-63 of a 107 x 10M product), so no product here is that large."""
     q = base if queries is None else queries
     n = base.shape[0]
     m = q.shape[0]
@@ -82,6 +87,107 @@ def knn(base: torch.Tensor, k: int, queries: torch.Tensor | None = None,
         o = torch.argsort(dv, dim=1, stable=True)
         ids_out[s:e] = torch.gather(di, 1, o)[:, :kk]
         d_out[s:e] = torch.gather(dv, 1, o)[:, :kk]
+    return ids_out, d_out
+
+
+def kmeans(x: torch.Tensor, cells: int, sample: int = 1 << 18, iters: int = 8, seed: int = 0x5EED,
+           chunk: int = 1 << 16) -> torch.Tensor:
+    """Lloyd's k-means on a seeded sample of x (float32 on x's device):
+    returns (cells, dim) centroids.  Initial centroids are distinct sample
+    points; a cell left empty keeps its centroid."""
+    n, dim = x.shape
+    g = torch.Generator().manual_seed(seed)
+    m = min(n, max(sample, cells))
+    pick = torch.randperm(n, generator=g)[:m].to(x.device)
+    xs = x[pick]
+    c = xs[torch.randperm(m, generator=g)[:cells].to(x.device)].clone()
+    for _ in range(iters):
+        a = _nearest_cells(xs, c, 1, chunk)[:, 0]
+        sums = torch.zeros_like(c).index_add_(0, a, xs)
+        cnt = torch.bincount(a, minlength=cells).to(x.dtype)
+        nz = cnt > 0
+        c[nz] = sums[nz] / cnt[nz, None]
+    return c
+
+
+def _nearest_cells(x: torch.Tensor, c: torch.Tensor, probes: int, chunk: int = 1 << 16) -> torch.Tensor:
+    """(n, probes) int64: the `probes` nearest centroids of each row of x."""
+    cn = _sqnorm(c)
+    out = torch.empty((x.shape[0], probes), dtype=torch.int64, device=x.device)
+    for s in range(0, x.shape[0], chunk):
+        d = cn[None, :] - 2.0 * (x[s:s + chunk] @ c.T)
+        out[s:s + chunk] = torch.topk(d, probes, dim=1, largest=False).indices
+    return out
+
+
+def knn_partitioned(x: torch.Tensor, k: int, cells: int | None = None, probes: int = 2, seed: int = 0x5EED,
+                    verbose: bool = False, block_elems: int = 1 << 28):
+    """Approximate k nearest neighbours of every row of x (excluding itself)
+    for sets too large for knn(): k-means cells (about 2,500 points each),
+    every point in the cell of its nearest centroid, and each point's
+    neighbours searched exactly among the points of its `probes` nearest
+    cells.  Returns (ids int64 [n,k], sqdist float32 [n,k]) ordered by
+    (dist, id), -1 / inf where fewer than k points were searched."""
+    n, dim = x.shape
+    dev = x.device
+    cells = cells or max(1, min(n // 2500, 1 << 16))
+    t0 = time.time()
+    cen = kmeans(x, cells, seed=seed)
+    near = _nearest_cells(x, cen, probes)
+    del cen
+    home = near[:, 0]
+    order = torch.argsort(home)
+    bounds = torch.zeros(cells + 1, dtype=torch.int64, device=dev)
+    bounds[1:] = torch.cumsum(torch.bincount(home, minlength=cells), 0)
+    qorder = torch.argsort(near.reshape(-1))
+    qbounds = torch.zeros(cells + 1, dtype=torch.int64, device=dev)
+    qbounds[1:] = torch.cumsum(torch.bincount(near.reshape(-1), minlength=cells), 0)
+    del near
+    if verbose:
+        print(f"[builder] {cells} cells in {time.time() - t0:.1f}s", flush=True)
+    xn = _sqnorm(x)
+    # per cell up to 16 more than k, so that ties at a cell's k-th distance
+    # still resolve by id after the merge (as in knn())
+    kx = k + 16
+    cid = torch.full((n * probes, kx), -1, dtype=torch.int32, device=dev)
+    cdist = torch.full((n * probes, kx), float("inf"), dtype=torch.float32, device=dev)
+    bh, qh = bounds.cpu().tolist(), qbounds.cpu().tolist()
+    for c in range(cells):
+        mem = order[bh[c]:bh[c + 1]]
+        qry = qorder[qh[c]:qh[c + 1]]  # (point, probe) pairs as point * probes + probe
+        if mem.numel() == 0 or qry.numel() == 0:
+            continue
+        xm, mn = x[mem], xn[mem]
+        kk = min(kx, mem.numel())
+        step = max(1, block_elems // mem.numel())
+        for s in range(0, qry.numel(), step):
+            qs = qry[s:s + step]
+            qp = qs // probes
+            d = xn[qp][:, None] + mn[None, :] - 2.0 * (x[qp] @ xm.T)
+            d.clamp_(min=0.0)
+            d.masked_fill_(qp[:, None] == mem[None, :], float("inf"))
+            dv, di = torch.topk(d, kk, dim=1, largest=False, sorted=False)
+            cid[qs, :kk] = mem[di].to(torch.int32)
+            cdist[qs, :kk] = dv
+        if verbose and (c + 1) % 1000 == 0:
+            print(f"[builder] cell {c + 1}/{cells} searched ({time.time() - t0:.1f}s)", flush=True)
+    del order, qorder, xn
+    if verbose:
+        print(f"[builder] per-cell neighbours in {time.time() - t0:.1f}s", flush=True)
+    cid = cid.view(n, probes * kx)
+    cdist = cdist.view(n, probes * kx)
+    ids_out = torch.empty((n, k), dtype=torch.int64, device=dev)
+    d_out = torch.empty((n, k), dtype=torch.float32, device=dev)
+    big = torch.iinfo(torch.int64).max
+    for s in range(0, n, 1 << 20):
+        ci = cid[s:s + (1 << 20)].to(torch.int64)
+        cd = cdist[s:s + (1 << 20)]
+        cd = torch.where(ci < 0, torch.full_like(cd, float("inf")), cd)
+        o = torch.argsort(torch.where(ci < 0, torch.full_like(ci, big), ci), dim=1)
+        ci, cd = torch.gather(ci, 1, o), torch.gather(cd, 1, o)
+        o = torch.argsort(cd, dim=1, stable=True)[:, :k]
+        ids_out[s:s + (1 << 20)] = torch.gather(ci, 1, o)
+        d_out[s:s + (1 << 20)] = torch.gather(cd, 1, o)
     return ids_out, d_out
 
 
@@ -161,21 +267,31 @@ def hadamard_rotation(signs: np.ndarray, device) -> torch.Tensor:
 
 def build_graph(x: torch.Tensor, degree: int, random_links: int | None = None,
                 seed: int = 0x5EED, alpha: float = 1.0, candidates: int | None = None,
-                fill_random: bool = True, verbose: bool = False, dist_block_elems: int = 1 << 32) -> torch.Tensor:
+                fill_random: bool = True, verbose: bool = False, dist_block_elems: int = 1 << 30,
+                knn_method: str = "exact") -> torch.Tensor:
     """Returns (n, degree) int64 neighbour ids (-1 = padding).  The final
     neighbour distances are gathered in row blocks of at most
-    `dist_block_elems` floats."""
+    `dist_block_elems` floats.  knn_method "exact" takes the candidates from
+    knn(), "partitioned" from knn_partitioned() (sets of millions of
+    high-dimensional points, where the exact search is out of reach)."""
     n = x.shape[0]
     dev = x.device
     kc = min(candidates or 2 * degree, n - 1)
     on_gpu = x.device.type == "cuda"
-    cand, cd = knn(x, kc, chunk_elems=(1 << 30) if on_gpu else (1 << 28))
+    if knn_method == "partitioned":
+        cand, cd = knn_partitioned(x, kc, verbose=verbose)
+    elif knn_method == "exact":
+        cand, cd = knn(x, kc)
+    else:
+        raise ValueError(f"unknown knn_method {knn_method!r}")
     if verbose:
         print(f"[builder] knn done k={kc}", flush=True)
     nr = degree // 4 if random_links is None else random_links
     nr = min(nr, max(0, n - 1 - degree)) if n > 2 * degree else 0
     local_cap = degree - nr
     local_keep = _prune(cand, cd, x, local_cap, alpha2=alpha * alpha, chunk=32768 if on_gpu else 4096)
+    if verbose:
+        print("[builder] RNG prune done", flush=True)
     ar = torch.arange(kc, device=dev)[None, :]
     o = torch.argsort(torch.where(local_keep, ar, kc + ar), dim=1)
     local = torch.where(torch.gather(local_keep, 1, o), torch.gather(cand, 1, o),
@@ -211,116 +327,162 @@ def build_graph(x: torch.Tensor, degree: int, random_links: int | None = None,
     return torch.gather(merged, 1, o)
 
 
-def encode(x: torch.Tensor, nbrs: torch.Tensor, signs: np.ndarray, use_ip: bool = False,
-           chunk_edges: int = 1 << 20):
-    """Per-edge codes (n, deg, B/8) uint8 and factors (n, 3, deg) float32."""
-    n, dim = x.shape
-    deg = nbrs.shape[1]
-    b = signs.shape[0]
+def _encode_chunk(x: torch.Tensor, nb: torch.Tensor, c0: torch.Tensor, p: torch.Tensor, pos: torch.Tensor,
+                  weights: torch.Tensor, b: int, use_ip: bool):
+    """Codes (m, deg, B/8) uint8 and factors (m, 3, deg) float32 of the
+    edges of m nodes: nb (m, deg) neighbour ids, c0 (m, dim) their vectors."""
+    m, deg = nb.shape
+    dim = x.shape[1]
     dev = x.device
-    p = hadamard_rotation(signs, dev)
-    pos = torch.as_tensor(code_bit_positions(b), device=dev)
-    weights = (2 ** torch.arange(8, device=dev, dtype=torch.int64))
-    codes = torch.zeros((n, deg, b // 8), dtype=torch.uint8, device=dev)
-    factors = torch.zeros((n, 3, deg), dtype=torch.float32, device=dev)
-    rows = max(1, chunk_edges // max(1, deg * b // 128))
-    for s in range(0, n, rows):
-        e = min(n, s + rows)
-        c = torch.zeros((e - s, b), dtype=torch.float64, device=dev)
-        c[:, :dim] = x[s:e].to(torch.float64)
-        nb = nbrs[s:e]
-        valid = nb >= 0
-        v = torch.zeros((e - s, deg, b), dtype=torch.float64, device=dev)
-        v[:, :, :dim] = x[nb.clamp(min=0)].to(torch.float64)
-        r = v - c[:, None, :]
-        y = r @ p.T
-        bits = (y > 0)
-        sgn = bits.to(torch.float64) * 2.0 - 1.0
-        nr = (r * r).sum(-1)
-        sabs = y.abs().sum(-1)
-        ssum = sgn.sum(-1)
-        zero = sabs <= 0
-        if use_ip:
-            f = torch.where(zero, torch.zeros_like(nr), -nr / torch.where(zero, torch.ones_like(sabs), sabs))
-            tx = torch.zeros_like(f)
-        else:
-            f = torch.where(zero, torch.zeros_like(nr), -2.0 * nr / torch.where(zero, torch.ones_like(sabs), sabs))
-            pc = c @ p.T
-            spc = (sgn * pc[:, None, :]).sum(-1)
-            tx = torch.where(zero, torch.zeros_like(nr), nr - f * spc)
-        fvq = f * ssum
-        tx = torch.where(valid, tx, torch.full_like(tx, FLT_MAX))
-        f = torch.where(valid, f, torch.zeros_like(f))
-        fvq = torch.where(valid, fvq, torch.zeros_like(fvq))
-        factors[s:e, 0] = tx.to(torch.float32)
-        factors[s:e, 1] = f.to(torch.float32)
-        factors[s:e, 2] = fvq.to(torch.float32)
-        ordered = torch.zeros((e - s, deg, b), dtype=torch.int64, device=dev)
-        ordered[:, :, pos] = (bits & valid[:, :, None]).to(torch.int64)
-        packed = (ordered.view(e - s, deg, b // 8, 8) * weights).sum(-1)
-        codes[s:e] = packed.to(torch.uint8)
+    c = torch.zeros((m, b), dtype=torch.float64, device=dev)
+    c[:, :dim] = c0.to(torch.float64)
+    valid = nb >= 0
+    v = torch.zeros((m, deg, b), dtype=torch.float64, device=dev)
+    v[:, :, :dim] = x[nb.clamp(min=0)].to(torch.float64)
+    r = v - c[:, None, :]
+    del v
+    y = r @ p.T
+    bits = (y > 0)
+    sgn = bits.to(torch.float64) * 2.0 - 1.0
+    nr = (r * r).sum(-1)
+    del r
+    sabs = y.abs().sum(-1)
+    del y
+    ssum = sgn.sum(-1)
+    zero = sabs <= 0
+    if use_ip:
+        f = torch.where(zero, torch.zeros_like(nr), -nr / torch.where(zero, torch.ones_like(sabs), sabs))
+        tx = torch.zeros_like(f)
+    else:
+        f = torch.where(zero, torch.zeros_like(nr), -2.0 * nr / torch.where(zero, torch.ones_like(sabs), sabs))
+        pc = c @ p.T
+        spc = (sgn * pc[:, None, :]).sum(-1)
+        tx = torch.where(zero, torch.zeros_like(nr), nr - f * spc)
+    del sgn
+    fvq = f * ssum
+    tx = torch.where(valid, tx, torch.full_like(tx, FLT_MAX))
+    f = torch.where(valid, f, torch.zeros_like(f))
+    fvq = torch.where(valid, fvq, torch.zeros_like(fvq))
+    factors = torch.stack([tx, f, fvq], 1).to(torch.float32)
+    ordered = torch.zeros((m, deg, b), dtype=torch.int64, device=dev)
+    ordered[:, :, pos] = (bits & valid[:, :, None]).to(torch.int64)
+    del bits
+    codes = (ordered.view(m, deg, b // 8, 8) * weights).sum(-1).to(torch.uint8)
     return codes, factors
 
 
-def entry_point(x: torch.Tensor) -> int:
-    """The node nearest the mean vector (float64)."""
-    xd = x.to(torch.float64)
-    mu = xd.mean(0, keepdim=True)
-    return int(torch.argmin(_sqnorm(xd - mu)).item())
+def _encode_setup(signs: np.ndarray, dev):
+    b = signs.shape[0]
+    return (hadamard_rotation(signs, dev), torch.as_tensor(code_bit_positions(b), device=dev),
+            2 ** torch.arange(8, device=dev, dtype=torch.int64))
 
 
-def build_codebook(base: np.ndarray, degree: int, signs: np.ndarray, use_ip: bool = False,
+def _encode_rows_per_chunk(deg: int, b: int, chunk_edges: int) -> int:
+    return max(1, chunk_edges // max(1, deg * b // 128))
+
+
+def encode(x: torch.Tensor, nbrs: torch.Tensor, signs: np.ndarray, use_ip: bool = False,
+           chunk_edges: int = 1 << 20):
+    """Per-edge codes (n, deg, B/8) uint8 and factors (n, 3, deg) float32."""
+    n = x.shape[0]
+    deg = nbrs.shape[1]
+    b = signs.shape[0]
+    p, pos, weights = _encode_setup(signs, x.device)
+    codes = torch.zeros((n, deg, b // 8), dtype=torch.uint8, device=x.device)
+    factors = torch.zeros((n, 3, deg), dtype=torch.float32, device=x.device)
+    rows = _encode_rows_per_chunk(deg, b, chunk_edges)
+    for s in range(0, n, rows):
+        e = min(n, s + rows)
+        codes[s:e], factors[s:e] = _encode_chunk(x, nbrs[s:e], x[s:e], p, pos, weights, b, use_ip)
+    return codes, factors
+
+
+def entry_point(x: torch.Tensor, chunk: int = 1 << 20) -> int:
+    """The node nearest the mean vector (float64), in row chunks."""
+    n = x.shape[0]
+    mu = torch.zeros(x.shape[1], dtype=torch.float64, device=x.device)
+    for s in range(0, n, chunk):
+        mu += x[s:s + chunk].to(torch.float64).sum(0)
+    mu /= n
+    best, best_d = 0, float("inf")
+    for s in range(0, n, chunk):
+        d = _sqnorm(x[s:s + chunk].to(torch.float64) - mu[None, :])
+        i = int(torch.argmin(d).item())
+        if float(d[i]) < best_d:
+            best, best_d = s + i, float(d[i])
+    return best
+
+
+def build_codebook(base, degree: int, signs: np.ndarray, use_ip: bool = False,
                    device: str | torch.device = "cpu", random_links: int | None = None,
                    alpha: float = 1.0, candidates: int | None = None, fill_random: bool = True,
-                   store_entry: bool = True, verbose: bool = False) -> Codebook:
-    """Builds a complete codebook in the reference layout."""
-    x = torch.as_tensor(np.ascontiguousarray(base, dtype=np.float32), device=device)
+                   store_entry: bool = True, verbose: bool = False, knn_method: str = "exact") -> Codebook:
+    """Builds a complete codebook in the reference layout.  `base` is a numpy
+    array or a float32 tensor (already on `device` for sets too large to
+    hold twice)."""
+    x = _as_device(base, device)
     nbrs = build_graph(x, degree, random_links=random_links, alpha=alpha, candidates=candidates,
-                       fill_random=fill_random, verbose=verbose)
-    return codebook_from_graph(base, nbrs, signs, use_ip=use_ip, device=device, store_entry=store_entry)
+                       fill_random=fill_random, verbose=verbose, knn_method=knn_method)
+    return codebook_from_graph(x, nbrs, signs, use_ip=use_ip, device=device, store_entry=store_entry,
+                               verbose=verbose)
 
 
-def codebook_from_graph(base: np.ndarray, nbrs, signs: np.ndarray, use_ip: bool = False,
+def _as_device(base, device) -> torch.Tensor:
+    if isinstance(base, torch.Tensor):
+        return base.to(device=device, dtype=torch.float32)
+    return torch.as_tensor(np.ascontiguousarray(base, dtype=np.float32), device=device)
+
+
+def codebook_from_graph(base, nbrs, signs: np.ndarray, use_ip: bool = False,
                         device: str | torch.device = "cpu", store_entry: bool = True,
-                        entry: int | None = None) -> Codebook:
+                        entry: int | None = None, verbose: bool = False) -> Codebook:
     """Encodes a given graph ((n, degree) neighbour ids, -1 = padding) into a
     codebook in the reference layout.  `entry` overrides the stored entry
-    point (default: the node nearest the mean)."""
-    n, dim = base.shape
+    point (default: the node nearest the mean).  The host rows are filled one
+    chunk of nodes at a time, so the device never holds more than a chunk's
+    codes."""
+    x = _as_device(base, device)
+    n, dim = x.shape
     nbrs = torch.as_tensor(np.asarray(nbrs) if not isinstance(nbrs, torch.Tensor) else nbrs,
                            dtype=torch.int64, device=device)
     degree = int(nbrs.shape[1])
     lay = Layout.make(dim, degree)
     if signs.shape[0] != lay.padded_dim:
         raise ValueError("signs must have padded_dim entries")
-    x = torch.as_tensor(np.ascontiguousarray(base, dtype=np.float32), device=device)
-    codes, factors = encode(x, nbrs, signs, use_ip=use_ip,
-                            chunk_edges=(1 << 22) if x.device.type == "cuda" else (1 << 20))
+    b = lay.padded_dim
+    p, pos, weights = _encode_setup(signs, x.device)
     rows = np.zeros((n, lay.row_offset), dtype=np.float32)
-    rows[:, :dim] = base
     code_bytes = rows[:, lay.code_offset : lay.factor_offset].view(np.uint8)
-    code_bytes[:] = codes.cpu().numpy().reshape(n, -1)
-    rows[:, lay.factor_offset : lay.neighbor_offset] = factors.cpu().numpy().reshape(n, -1)
-    ids = nbrs.cpu().numpy()
-    ids = np.where(ids < 0, MAX_INDEX, ids).astype(np.uint32)
-    rows[:, lay.neighbor_offset : lay.row_offset].view(np.uint32)[:] = ids
+    ids = rows[:, lay.neighbor_offset : lay.row_offset].view(np.uint32)
+    step = _encode_rows_per_chunk(degree, b, 1 << 20)
+    for s in range(0, n, step):
+        e = min(n, s + step)
+        nb = nbrs[s:e]
+        codes, factors = _encode_chunk(x, nb, x[s:e], p, pos, weights, b, use_ip)
+        rows[s:e, :dim] = x[s:e].cpu().numpy()
+        code_bytes[s:e] = codes.cpu().numpy().reshape(e - s, -1)
+        rows[s:e, lay.factor_offset : lay.neighbor_offset] = factors.cpu().numpy().reshape(e - s, -1)
+        nbh = nb.cpu().numpy()
+        ids[s:e] = np.where(nbh < 0, MAX_INDEX, nbh).astype(np.uint32)
+        if verbose and (s // step) % 100 == 99:
+            print(f"[builder] encoded {e}/{n} nodes", flush=True)
     if entry is None:
         entry = entry_point(x) if store_entry else MAX_INDEX
     return Codebook(rows, np.asarray(signs, dtype=np.float32), int(entry), lay)
 
 
-def ground_truth(base: np.ndarray, queries: np.ndarray, k: int,
-                 device: str | torch.device = "cpu", use_ip: bool = False) -> np.ndarray:
+def ground_truth(base, queries, k: int, device: str | torch.device = "cpu", use_ip: bool = False,
+                 chunk_elems: int = 1 << 28) -> np.ndarray:
     """Exact top-k ids (int32) by L2 (or by -<q,x> for IP), ties by id."""
-    b = torch.as_tensor(np.ascontiguousarray(base, dtype=np.float32), device=device)
-    q = torch.as_tensor(np.ascontiguousarray(queries, dtype=np.float32), device=device)
+    b = _as_device(base, device)
+    q = _as_device(queries, device)
     if not use_ip:
-        ids, _ = knn(b, k, queries=q, exclude_self=False,
-                     chunk_elems=(1 << 30) if b.device.type == "cuda" else (1 << 28))
+        ids, _ = knn(b, k, queries=q, exclude_self=False, chunk_elems=chunk_elems)
         return ids.cpu().numpy().astype(np.int32)
     out = []
-    for s in range(0, q.shape[0], 1024):
-        d = -(q[s : s + 1024] @ b.T)
+    rows = max(1, chunk_elems // max(1, b.shape[0]))
+    for s in range(0, q.shape[0], rows):
+        d = -(q[s : s + rows] @ b.T)
         dv, di = torch.topk(d, min(b.shape[0], k + 16), dim=1, largest=False)
         o = torch.argsort(di, dim=1)
         di, dv = torch.gather(di, 1, o), torch.gather(dv, 1, o)
@@ -329,10 +491,32 @@ def ground_truth(base: np.ndarray, queries: np.ndarray, k: int,
     return np.concatenate(out).astype(np.int32)
 
 
+def check_ground_truth(base, queries, gt: np.ndarray, sample: int = 32, use_ip: bool = False,
+                       device: str | torch.device = "cpu") -> int:
+    """Recomputes `sample` evenly spaced queries' distances to every base
+    point one query at a time (a matrix-vector product, independent of the
+    blocked products ground_truth uses) and returns how many of them have a
+    ground-truth set whose largest distance exceeds that query's true k-th
+    distance (0 for a correct ground truth, ties included)."""
+    b = _as_device(base, device)
+    q = _as_device(queries, device)
+    k = gt.shape[1]
+    bn = _sqnorm(b)
+    bad = 0
+    for i in np.linspace(0, q.shape[0] - 1, min(sample, q.shape[0])).astype(np.int64):
+        d = -(b @ q[int(i)]) if use_ip else bn - 2.0 * (b @ q[int(i)])
+        kth = torch.topk(d, k, largest=False).values.max()
+        got = d[torch.as_tensor(gt[int(i)], device=b.device, dtype=torch.int64)].max()
+        if float(got) > float(kth) + 1e-4 * max(1.0, abs(float(kth))):
+            bad += 1
+    return bad
+
+
 def graph_stats(nbrs: np.ndarray) -> dict:
     valid = nbrs != MAX_INDEX
     return {"mean_degree": float(valid.sum(1).mean()), "min_degree": int(valid.sum(1).min())}
 
 
-__all__ = ["knn", "build_graph", "encode", "build_codebook", "ground_truth", "entry_point",
+__all__ = ["knn", "knn_partitioned", "kmeans", "build_graph", "encode", "build_codebook", "ground_truth",
+           "check_ground_truth", "entry_point",
            "hadamard_rotation", "graph_stats"]

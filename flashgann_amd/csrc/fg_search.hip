@@ -1976,9 +1976,28 @@ __global__ __launch_bounds__(64) void fg_score_kernel(ScoreParams S) {
     const int hw = W >> 1;
     const int32_t part = raw_partial(code, h * hw, (h + 1) * hw, planes, W);
     const int32_t raw_split = add32i(part);
-    // the search kernel's own routine for the generic geometry (W >= 8)
+    // the search kernel's own routines: raw_batch for padded dimensions 64 and
+    // 128 (W = 2, 4; the fixed geometries), raw_words for W >= 8
     const bool vec_ok = S.row_offset % 4 == 0 && S.code_offset % 4 == 0;
-    const int32_t raw_full = W >= 8 ? raw_words(code, planes, W, vec_ok, true) : raw_partial(code, 0, W, planes, W);
+    uint32_t wor = 0;
+    for (int w = 0; w < W; ++w) wor |= planes[kPlanes * W + w];
+    const bool any_wrap = uni(wor) != 0u;
+    int32_t raw_full;
+    if (W == 4 || W == 2) {
+        int32_t r[1];
+        if (W == 4) {
+            uint32_t c[1][4];
+            load_code<4>(code, vec_ok, c[0]);
+            raw_batch<1, 4>(c, planes, any_wrap, r);
+        } else {
+            uint32_t c[1][2];
+            load_code<2>(code, vec_ok, c[0]);
+            raw_batch<1, 2>(c, planes, any_wrap, r);
+        }
+        raw_full = r[0];
+    } else {
+        raw_full = raw_words(code, planes, W, vec_ok, any_wrap);
+    }
     const float el = tx == FLT_MAX ? 0.0f : estimate_formula(raw_split, sq, w, lo, tx, fdq, fvq, pd);
     const float es = tx == FLT_MAX ? FLT_MAX : estimate_formula(raw_full, sq, w, lo, tx, fdq, fvq, pd);
     const uint32_t child = reinterpret_cast<const uint32_t *>(prow + (S.factor_offset + 3 * S.deg))[slot];

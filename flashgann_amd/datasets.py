@@ -93,6 +93,38 @@ def anisotropic_unit_mixture(n: int, nq: int, dim: int = 1536, components: int =
     return draw(n, 1), draw(nq, 2)
 
 
+def anisotropic_unit_mixture_device(n: int, nq: int, dim: int = 1536, components: int = 4096, config: int = 5,
+                                    device="cuda", chunk: int = 1 << 19):
+    """The C5 mixture drawn on a torch device, for sets too large to draw on
+    the host (10M x 1536 is 61 GB): the same means and per-component scales
+    as anisotropic_unit_mixture (numpy, stream 0), with the component choices
+    and the normal draws from torch generators on `device` seeded with the
+    same per-stream seeds.  Returns float32 tensors (base, queries) on
+    `device`; deterministic for a given device type and torch version (the
+    host generator's values differ)."""
+    import torch
+    r0 = _rng(config, 0)
+    means = torch.as_tensor(r0.standard_normal(size=(components, dim)).astype(np.float32), device=device)
+    scales = torch.as_tensor((0.05 + 0.45 * r0.uniform(0.0, 1.0, size=(components, dim))).astype(np.float32),
+                             device=device)
+
+    def draw(count: int, stream: int):
+        g = torch.Generator(device=device)
+        g.manual_seed(SEED_BASE + 16 * config + stream)
+        comp = torch.randint(0, components, (count,), generator=g, device=device)
+        out = torch.empty((count, dim), dtype=torch.float32, device=device)
+        for s in range(0, count, chunk):
+            e = min(count, s + chunk)
+            z = torch.randn((e - s, dim), generator=g, device=device, dtype=torch.float32)
+            c = comp[s:e]
+            x = torch.addcmul(means[c], scales[c], z)
+            out[s:e] = x / torch.linalg.vector_norm(x, dim=1, keepdim=True)
+            del z, x
+        return out
+
+    return draw(n, 1), draw(nq, 2)
+
+
 def signs_for(padded_dim: int, config: int = 1) -> np.ndarray:
     """The +-1 diagonal of the rotation P = H_B * diag(signs)."""
     r = _rng(config, 3)

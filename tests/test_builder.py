@@ -142,3 +142,61 @@ def test_build_index_cli_round_trip(tmp_path):
     assert gt.shape == (16, 10)
     out, _ = O.OracleIndex.from_codebook(cb).search(q, 10, 64)
     assert compute_recall(out, gt, 10) >= 0.9
+
+
+def test_partitioned_knn_reduces_to_exact_knn():
+    """Searching every cell (probes == cells) is the exact k-NN search:
+    identical ids and distances to knn() on integer data, where every
+    distance is exact."""
+    import torch
+    from flashgann_amd import builder, datasets
+    base, _ = datasets.integer_mixture(4000, 1, 64, 8, config=1)
+    x = torch.as_tensor(base)
+    a_ids, a_d = builder.knn(x, 24)
+    b_ids, b_d = builder.knn_partitioned(x, 24, cells=6, probes=6)
+    assert torch.equal(a_ids, b_ids) and torch.equal(a_d, b_d)
+
+
+def test_partitioned_knn_overlap_on_c5_mixture():
+    """Two probed cells of eight find nearly all exact neighbours of the C5
+    generator's well-separated anisotropic components."""
+    import torch
+    from flashgann_amd import builder, datasets
+    base, _ = datasets.anisotropic_unit_mixture(12000, 1, 128, 12)
+    x = torch.as_tensor(base)
+    a, _ = builder.knn(x, 64)
+    b, _ = builder.knn_partitioned(x, 64, probes=2)
+    a, b = a.numpy(), b.numpy()
+    overlap = np.mean([len(np.intersect1d(a[i], b[i])) / 64 for i in range(0, 12000, 7)])
+    assert overlap > 0.99, overlap
+    g = builder.build_graph(x, 32, knn_method="partitioned")
+    assert g.shape == (12000, 32) and (g >= 0).all()
+
+
+def test_device_generator_shapes_and_determinism():
+    """The device form of the C5 generator (here on the CPU device): unit
+    rows, the requested shapes, the same draws for the same seed."""
+    from flashgann_amd import datasets
+    a, qa = datasets.anisotropic_unit_mixture_device(3000, 40, 96, 16, device="cpu", chunk=1000)
+    b, qb = datasets.anisotropic_unit_mixture_device(3000, 40, 96, 16, device="cpu", chunk=700)
+    assert a.shape == (3000, 96) and qa.shape == (40, 96)
+    assert np.allclose(a.norm(dim=1).numpy(), 1.0, atol=1e-5)
+    assert (a == b).all() and (qa == qb).all()
+
+
+def test_ground_truth_recheck():
+    """check_ground_truth accepts the exact ground truth (ties included) and
+    flags rows whose sets hold points beyond the true k-th distance."""
+    from flashgann_amd import builder, datasets
+    base, q = datasets.integer_mixture(3000, 40, 64, 8, config=2)
+    for ip in (False, True):
+        gt = builder.ground_truth(base, q, 20, use_ip=ip)
+        assert builder.check_ground_truth(base, q, gt, sample=40, use_ip=ip) == 0
+        bad = gt.copy()
+        bad[::5] = gt[::5][:, ::-1] + 0  # same sets: still fine
+        assert builder.check_ground_truth(base, q, bad, sample=40, use_ip=ip) == 0
+        # the 20 worst points: largest distance, or smallest inner product
+        score = ((base[None] - q[:, None]) ** 2).sum(-1) if not ip else -(q @ base.T)
+        far = np.argsort(score, axis=1)[:, -20:]
+        bad[::4] = far[::4]
+        assert builder.check_ground_truth(base, q, bad, sample=40, use_ip=ip) == 10
