@@ -13,7 +13,9 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "liboracle.so")
+# FG_ORACLE_LIB names another build of fg_oracle.c (the mutation tests load
+# deliberately broken copies through it)
+LIB_PATH = os.environ.get("FG_ORACLE_LIB") or os.path.join(HERE, "liboracle.so")
 REF_LIB_PATH = os.path.join(HERE, "_ref", "libfg_ref_host.so")
 
 MAX_INDEX = 0xFFFFFFFF
