@@ -783,7 +783,9 @@ __device__ __forceinline__ void small_merge(int pbeam, uint2 *bp, const uint2 *m
 // It searches its right boundaries; the left one is its neighbour's.  The
 // searches read the sentinel-padded arrays, so no bound needs a branch:
 // bp[-1], ms[-1] = -FLT_MAX and bp[pbeam], ms[32] = FLT_MAX stand for the
-// reference's out-of-range values.
+// reference's out-of-range values.  Segments before `tbase` are not touched
+// (the caller has shown that they output the beam unchanged); lane l owns
+// segments tbase + l*SPL ...
 //
 // The splits valid at a diagonal d (i beam entries and d - i candidates,
 // with beam[i-1] <= cand[d-i] and cand[d-i-1] <= beam[i]) form an interval
@@ -797,10 +799,11 @@ __device__ __forceinline__ void small_merge(int pbeam, uint2 *bp, const uint2 *m
 // split of such a tie gives the same output.  Any other equal pair sends the
 // whole wave through the reference's bisection, replayed step by step.
 template <int SPL>
-__device__ __forceinline__ void merge_path(const SearchParams &P, uint2 *bp, const uint2 *ms, bool fast_ok) {
+__device__ __forceinline__ void merge_path(const SearchParams &P, uint2 *bp, const uint2 *ms, bool fast_ok,
+                                           int tbase) {
     const int lane = lane_id_opaque();
     const int cbs = P.cbs, pbeam = P.pbeam, active = P.seg_active;
-    const int t0 = lane * SPL;
+    const int t0 = tbase + lane * SPL;
     const float *bk = reinterpret_cast<const float *>(bp);  // key of entry i at bk[2 i]
     const float *mk = reinterpret_cast<const float *>(ms);
     int dg[SPL + 1], res[SPL + 1];
@@ -878,7 +881,7 @@ __device__ __forceinline__ void merge_path(const SearchParams &P, uint2 *bp, con
         }
     }
     res[0] = __builtin_amdgcn_update_dpp(0, res[SPL], 0x138, 0xF, 0xF, false);  // DPP wave_shr:1; lane 0 reads 0
-    if (lane == 0) res[0] = 0;
+    if (lane == 0) res[0] = dg[0];  // segment tbase starts with beam entries only (d(0) = 0)
     // Each segment's na beam entries and nb candidates (na + nb <= 4) are
     // read into 4 slots: slot s is beam entry tb + s for s < na, candidate
     // cb + s - na after.  Output position of a slot = d(t) + the number of
@@ -955,11 +958,34 @@ __device__ __forceinline__ void merge_beam(const SearchParams &P, uint2 *bp, uin
         small_merge<1, false>(pbeam, bp, ms, lane, true);
     } else if (pbeam == 32) {
         small_merge<1, true>(pbeam, bp, ms, nl, h == 0);
+    } else if (P.seg_active <= 64) {
+        merge_path<1>(P, bp, ms, fast_ok, 0);  // one segment per lane: nothing to save
     } else {
-        const int spl = (P.seg_active + 63) / 64;
-        if (spl == 1) merge_path<1>(P, bp, ms, fast_ok);
-        else if (spl == 2) merge_path<2>(P, bp, ms, fast_ok);
-        else merge_path<4>(P, bp, ms, fast_ok);
+        // Segments whose outputs lie wholly at or before position lb, the
+        // number of beam entries with a key below the smallest candidate's,
+        // output the beam unchanged: at a diagonal d <= lb the only valid split
+        // takes d beam entries (beam[d-1] < cand[0], and any split with fewer
+        // would need cand[j] <= beam[i] for some i < d), so the reference's
+        // bisection returns it.  lb in two steps of 64 probes; then the first
+        // segment t with d(t+1) > lb.
+        const int active = P.seg_active;
+        const float c0 = pair_key(ms[0]);
+        const float *bk = reinterpret_cast<const float *>(bp);
+        const int st = (pbeam + 63) / 64;  // <= 16
+        const int p1 = min((lane + 1) * st, pbeam) - 1;
+        const int c1 = __popcll(ballot(bk[2 * p1] < c0));
+        const int q2 = c1 * st + lane;
+        const int c2 = __popcll(ballot(lane < st && q2 < pbeam && bk[2 * min(q2, pbeam)] < c0));
+        const int lb = uni(min(c1 * st + c2, pbeam));
+        int tf = static_cast<int>(static_cast<uint32_t>(lb) * static_cast<uint32_t>(active) / static_cast<uint32_t>(pbeam));
+        const auto seg_end = [&](int t) {
+            return static_cast<int>(__umulhi(static_cast<uint32_t>(t * pbeam), P.seg_magic));
+        };
+        if (tf < active && seg_end(tf + 1) <= lb) ++tf;
+        const int spl = (active - tf + 63) / 64;
+        if (spl == 1) merge_path<1>(P, bp, ms, fast_ok, tf);
+        else if (spl == 2) merge_path<2>(P, bp, ms, fast_ok, tf);
+        else if (spl > 2) merge_path<4>(P, bp, ms, fast_ok, tf);
     }
     __syncthreads();
 }
@@ -1557,21 +1583,59 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
         // pick_expanders (utils.cuh:752-787): first theta unexpanded entries
         // the picked entries' ids and distances go straight to the parent
         // lists (an unexpanded entry's id has the top bit clear)
+        // Beams up to 256: lane l reads entry base + l (64 per step).  Larger
+        // beams, where the first unexpanded entry sits about halfway down:
+        // lane l scans entries base + 4 l .. base + 4 l + 3 (256 per step, in
+        // index order across lanes); a lane's rank offset is the exclusive
+        // prefix of the per-lane counts, summed from the ballots of their bits.
         uint32_t nexp = 0;
-        for (int base = 0; base < beam_sz; base += 64) {
-            const int j = base + lane;
-            const uint2 e = bp[j < pbeam ? j : pbeam];  // unconditional read; bp[pbeam] is a sentinel
-            const bool fresh = j < beam_sz && (e.y & kMsb) == 0;
-            const uint64_t m = ballot(fresh);
-            if (fresh) {
-                const uint32_t r = static_cast<uint32_t>(__popcll(m & ((1ull << lane) - 1ull))) + nexp;
-                if (r < static_cast<uint32_t>(theta)) {
-                    pnode[r] = e.y;
-                    pdist[r] = __uint_as_float(e.x);
-                    bp[j].y = e.y | kMsb;
+        if (beam_sz <= 256) {
+            for (int base = 0; base < beam_sz; base += 64) {
+                const int j = base + lane;
+                const uint2 e = bp[j < pbeam ? j : pbeam];  // unconditional read; bp[pbeam] is a sentinel
+                const bool fresh = j < beam_sz && (e.y & kMsb) == 0;
+                const uint64_t m = ballot(fresh);
+                if (fresh) {
+                    const uint32_t r = static_cast<uint32_t>(__popcll(m & ((1ull << lane) - 1ull))) + nexp;
+                    if (r < static_cast<uint32_t>(theta)) {
+                        pnode[r] = e.y;
+                        pdist[r] = __uint_as_float(e.x);
+                        bp[j].y = e.y | kMsb;
+                    }
+                }
+                nexp += static_cast<uint32_t>(__popcll(m));
+                if (nexp >= static_cast<uint32_t>(theta)) {
+                    nexp = static_cast<uint32_t>(theta);
+                    break;
                 }
             }
-            nexp += static_cast<uint32_t>(__popcll(m));
+        } else for (int base = 0; base < beam_sz; base += 256) {
+            const int j0 = base + 4 * lane;
+            uint2 e[4];
+            bool fresh[4];
+            uint32_t cnt = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int j = j0 + k;
+                e[k] = bp[j < pbeam ? j : pbeam];  // unconditional read; bp[pbeam] is a sentinel
+                fresh[k] = j < beam_sz && (e[k].y & kMsb) == 0;
+                cnt += fresh[k] ? 1u : 0u;
+            }
+            const uint64_t b0 = ballot(cnt & 1u), b1 = ballot(cnt & 2u), b2 = ballot(cnt & 4u);
+            const uint64_t lt = (1ull << lane) - 1ull;
+            uint32_t r = nexp + static_cast<uint32_t>(__popcll(b0 & lt) + 2 * __popcll(b1 & lt) + 4 * __popcll(b2 & lt));
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if (fresh[k]) {
+                    if (r < static_cast<uint32_t>(theta)) {
+                        pnode[r] = e[k].y;
+                        pdist[r] = __uint_as_float(e[k].x);
+                        bp[j0 + k].y = e[k].y | kMsb;
+                    }
+                    ++r;
+                }
+            }
+            nexp += static_cast<uint32_t>(__popcll(b0) + 2 * __popcll(b1) + 4 * __popcll(b2));
             if (nexp >= static_cast<uint32_t>(theta)) {
                 nexp = static_cast<uint32_t>(theta);
                 break;
