@@ -938,8 +938,9 @@ __device__ __forceinline__ void merge_path(const SearchParams &P, uint2 *bp, con
 // empty (FLT_MAX, MAX_INDEX) pair (merge_path's condition for its split
 // search).
 __device__ __forceinline__ void merge_beam(const SearchParams &P, uint2 *bp, uint2 *ms, const float *cd,
-                                           const uint32_t *ci, int span, bool &fast_ok) {
+                                           const uint32_t *ci, int span, bool &fast_ok, int &lb_out) {
     const int lane = lane_id_opaque();
+    lb_out = 0;
     const int nl = lane & 31, h = lane >> 5;
     const int cbs = P.cbs, pbeam = P.pbeam;
     float ck = nl < cbs ? cd[nl] : FLT_MAX;
@@ -977,6 +978,7 @@ __device__ __forceinline__ void merge_beam(const SearchParams &P, uint2 *bp, uin
         const int q2 = c1 * st + lane;
         const int c2 = __popcll(ballot(lane < st && q2 < pbeam && bk[2 * min(q2, pbeam)] < c0));
         const int lb = uni(min(c1 * st + c2, pbeam));
+        lb_out = lb;
         int tf = static_cast<int>(static_cast<uint32_t>(lb) * static_cast<uint32_t>(active) / static_cast<uint32_t>(pbeam));
         const auto seg_end = [&](int t) {
             return static_cast<int>(__umulhi(static_cast<uint32_t>(t * pbeam), P.seg_magic));
@@ -1544,6 +1546,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
     // reset pair): the entry point's slot 0 first, then what each stage fills
     int cand_span = 1;
     bool split_fast = true;  // merge_path may search its splits directly
+    // beams over 256: every beam entry before scan_from is expanded (the pick
+    // starts there); a merge leaves entries before its lb in place
+    int scan_from = 0, lb_merge = 0;
     const float *data = P.data;
 
     FG_PHASE(0);
@@ -1567,7 +1572,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
         // A search that runs all kMaxIterations iterations (max_iter > 1024,
         // i.e. beam >= 931) leaves the loop without passing here again and
         // merges after it.
-        merge_beam(P, bp, ms, cd, ci, cand_span, split_fast);
+        merge_beam(P, bp, ms, cd, ci, cand_span, split_fast, lb_merge);
+        scan_from = min(scan_from, lb_merge);
         FG_PHASE(2);
         if (iter >= P.max_iter) break;
         for (int i = beam_sz + lane; i < pbeam; i += 64) bp[i] = kEmpty;
@@ -1609,7 +1615,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
                     break;
                 }
             }
-        } else for (int base = 0; base < beam_sz; base += 256) {
+        } else {
+          int lastj = -1;  // the entry that took rank theta - 1
+          for (int base = scan_from; base < beam_sz; base += 256) {
             const int j0 = base + 4 * lane;
             uint2 e[4];
             bool fresh[4];
@@ -1631,6 +1639,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
                         pnode[r] = e[k].y;
                         pdist[r] = __uint_as_float(e[k].x);
                         bp[j0 + k].y = e[k].y | kMsb;
+                        if (r + 1 == static_cast<uint32_t>(theta)) lastj = j0 + k;
                     }
                     ++r;
                 }
@@ -1640,6 +1649,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
                 nexp = static_cast<uint32_t>(theta);
                 break;
             }
+          }
+          // entries up to the last one picked are now all expanded
+          const uint64_t bl = ballot(lastj >= 0);
+          scan_from = bl ? __builtin_amdgcn_readlane(lastj, __builtin_ctzll(bl)) + 1 : beam_sz;
         }
         __syncthreads();
         if (nexp == 0) break;
@@ -1952,7 +1965,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
     }
     // the loop ran out at kMaxIterations: the last iteration's exact-scored
     // candidates are still in the buffer (adaptive_search.cuh:449-451)
-    if (iter == kMaxIterations) merge_beam(P, bp, ms, cd, ci, cand_span, split_fast);
+    if (iter == kMaxIterations) merge_beam(P, bp, ms, cd, ci, cand_span, split_fast, lb_merge);
 
     FG_PHASE(3);
     // result writer (adaptive_search.cuh:455-464)
