@@ -288,6 +288,22 @@ __device__ __forceinline__ uint32_t half_popc(uint64_t m) {
     return lane_in(0xFFFFFFFF00000000ull) ? hi : lo;
 }
 
+// Set bits in this lane's G-lane group of a ballot (G = 32: its half; G = 16:
+// its row), from scalar counts and selects.
+template <int G>
+__device__ __forceinline__ uint32_t group_popc(uint64_t m) {
+    if constexpr (G == 32) {
+        return half_popc(m);
+    } else {
+        const uint32_t r0 = static_cast<uint32_t>(__popc(static_cast<uint32_t>(m) & 0xFFFFu));
+        const uint32_t r1 = static_cast<uint32_t>(__popc(static_cast<uint32_t>(m) >> 16));
+        const uint32_t r2 = static_cast<uint32_t>(__popc(static_cast<uint32_t>(m >> 32) & 0xFFFFu));
+        const uint32_t r3 = static_cast<uint32_t>(__popc(static_cast<uint32_t>(m >> 48)));
+        const bool odd = lane_in(0xFFFF0000FFFF0000ull), high = lane_in(0xFFFFFFFF00000000ull);
+        return high ? (odd ? r3 : r2) : (odd ? r1 : r0);
+    }
+}
+
 // Lane i reads lane i ^ m, all lanes active.  m < 16 stays inside a 16-lane
 // row: DPP quad_perm (1, 2), half-row mirror then quad reverse
 // ((i^7)^3 = i^4), row rotate by 8 (i + 8 mod 16 = i^8).  16 and
@@ -1354,8 +1370,10 @@ __device__ __forceinline__ void exact_batch(const SearchParams &P, const G &g, i
 
 // The keep_k smallest valid (value, lane) pairs of each 32-lane half, as
 // warp_keep_topk_smallest_f32 (utils.cuh:251-267) selects them, found by
-// keep_k rounds of half-wave argmin instead of a 32-step rank count.  keep_k
-// is uniform within each half; valid lanes and the result are lane masks.
+// keep_k rounds of group argmin (G = 32: half-wave; 16: 16-lane row) instead
+// of a 32-step rank count.  keep_k is uniform within each group; valid lanes
+// and the result are lane masks.
+template <int G>
 __device__ __forceinline__ uint64_t select_smallest(float value, uint64_t valid, int keep_k, int max_k) {
     // order-preserving unsigned image of the float; -0 joins +0 so equal
     // values tie exactly as in the float comparison
@@ -1371,12 +1389,22 @@ __device__ __forceinline__ uint64_t select_smallest(float value, uint64_t valid,
         m = min(m, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(m), 0x4E, 0xF, 0xF, true)));
         m = min(m, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(m), 0x141, 0xF, 0xF, true)));
         m = min(m, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(m), 0x140, 0xF, 0xF, true)));
-        m = min16(m);
-        // the lowest lane of each half holding its half's minimum (x & -x on
-        // each 32-bit half of the mask), taken while the half keeps more
+        if constexpr (G == 32) m = min16(m);  // (G = 16: the row's minimum is the group's)
+        // the lowest lane of each group holding its group's minimum (x & -x on
+        // each G-bit part of the mask), taken while the group keeps more
         const uint64_t cand = ballot(key == m) & remaining;
-        const uint32_t c0 = static_cast<uint32_t>(cand), c1 = static_cast<uint32_t>(cand >> 32);
-        const uint64_t first = (static_cast<uint64_t>(c1 & (0u - c1)) << 32) | (c0 & (0u - c0));
+        uint64_t first;
+        if constexpr (G == 32) {
+            const uint32_t c0 = static_cast<uint32_t>(cand), c1 = static_cast<uint32_t>(cand >> 32);
+            first = (static_cast<uint64_t>(c1 & (0u - c1)) << 32) | (c0 & (0u - c0));
+        } else {
+            first = 0ull;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const uint32_t c = static_cast<uint32_t>(cand >> (16 * g)) & 0xFFFFu;
+                first |= static_cast<uint64_t>(c & (0u - c)) << (16 * g);
+            }
+        }
         const uint64_t take = first & ballot(r < keep_k);
         kept |= take;
         remaining &= ~take;
@@ -1768,8 +1796,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
             const int lim_full = uni(keep_limit(static_cast<uint32_t>(an_full), theta, ctl.rho));
             const int lim_last = an_last == an_full ? lim_full : uni(keep_limit(static_cast<uint32_t>(an_last), theta, ctl.rho));
             uint32_t compact = 0;
+            // A task (one 32-neighbour tile of one parent: one reference warp)
+            // takes G lanes: a 32-lane half, or for degree 16 a 16-lane row, so
+            // a wave runs TPW tasks at once; lane order is task order.
+            constexpr int G = DEG_T == 16 ? 16 : 32;
+            constexpr int TPW = 64 / G;
+            const int grp = lane / G, nlg = lane % G;
             for (int rbase = 0; rbase < tasks; rbase += kSearchWidth) {
-                constexpr int SR = kSearchWidth / 2;  // sub-rounds: two reference warps per wave
+                constexpr int SR = kSearchWidth / TPW;  // sub-rounds of TPW tasks
                 uint32_t cid[SR];
                 bool val[SR];
                 int an[SR], tsk[SR], pix[SR];
@@ -1787,11 +1821,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
                 int nsafe[SR];
 #pragma unroll
                 for (int sr = 0; sr < SR; ++sr) {
-                    const int task = rbase + 2 * sr + h;
+                    const int task = rbase + TPW * sr + grp;
                     const bool tact = task < tasks;
                     const int pidx = tact ? task / tiles : 0;
                     const int tile = tact ? task - pidx * tiles : 0;
-                    const int nidx = tile * 32 + nl;
+                    const int nidx = tile * 32 + nlg;
                     lact[sr] = tact && nidx < deg;
                     nsafe[sr] = nidx < deg ? nidx : deg - 1;
                     tsk[sr] = tact ? tile * 32 : -1;
@@ -1854,7 +1888,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
 #pragma unroll
                 for (int sr = 0; sr < SR; ++sr) {
                     valm[sr] = ballot(val[sr]);
-                    const int rvc = static_cast<int>(half_popc(valm[sr]));
+                    const int rvc = static_cast<int>(group_popc<G>(valm[sr]));
                     keep[sr] = an[sr] == an_full ? lim_full : lim_last;
                     needm[sr] = ballot(keep[sr] < rvc);
                     FG_COUNT(c_est += static_cast<uint32_t>(__popcll(needm[sr] & valm[sr])));
@@ -1875,7 +1909,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
                                                          pdist[pix[sr]]);
                         est = (lane_in(scored) && tx[sr] != FLT_MAX) ? e : FLT_MAX;
                     } else if (lane_in(scored) && tx[sr] != FLT_MAX) {
-                        const int nidx = tsk[sr] + nl;
+                        const int nidx = tsk[sr] + nlg;
                         const int32_t raw = raw_words(reinterpret_cast<const uint32_t *>(prw[sr] + g.code) +
                                                           static_cast<uint64_t>(nidx) * W,
                                                       planes, W, vec_ok, any_wrap);
@@ -1892,7 +1926,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
                     uint64_t kl = valm[sr];
                     if (needm[sr] != 0ull) {
                         const uint64_t belowm = kth_valid ? (valm[sr] & ballot(est <= kth)) : 0ull;
-                        const uint32_t near = half_popc(belowm);
+                        const uint32_t near = group_popc<G>(belowm);
                         const int kp = keep[sr];
                         const bool nd = lane_in(needm[sr]);
                         const int eff = nd ? keep_with_cutoff(kp, kth_valid, near) : kp;
@@ -1903,9 +1937,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
                         const uint64_t cutm =
                             kth_valid ? (needm[sr] & ballot(near >= 1u) & ballot(static_cast<int>(near) <= kp)) : 0ull;
                         const int rounds = (nd && !lane_in(cutm)) ? eff : 0;
-                        // uniform within each half: the larger of lanes 0 and 32
-                        const int maxk = max(__builtin_amdgcn_readlane(rounds, 0), __builtin_amdgcn_readlane(rounds, 32));
-                        const uint64_t selm = select_smallest(est, valm[sr], eff, maxk);
+                        // uniform within each group: the largest over the groups' first lanes
+                        int maxk = max(__builtin_amdgcn_readlane(rounds, 0), __builtin_amdgcn_readlane(rounds, 32));
+                        if constexpr (G == 16)
+                            maxk = max(maxk, max(__builtin_amdgcn_readlane(rounds, 16), __builtin_amdgcn_readlane(rounds, 48)));
+                        const uint64_t selm = select_smallest<G>(est, valm[sr], eff, maxk);
                         const uint64_t effm = ballot(eff > 0);
                         kl = (valm[sr] & ~needm[sr]) | (needm[sr] & valm[sr] & effm & ((cutm & belowm) | (selm & ~cutm)));
                     }
@@ -1915,7 +1951,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
                 uint32_t total = 0;
 #pragma unroll
                 for (int sr = 0; sr < SR; ++sr) {
-                    // tasks 2 sr and 2 sr + 1 are the two halves and follow
+                    // the sub-round's TPW tasks sit in lane order and follow
                     // each other in the list: a kept lane's place is the running
                     // total plus its rank among the kept lanes of the wave
                     if (lane_in(klm[sr])) {
