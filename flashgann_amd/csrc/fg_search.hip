@@ -426,7 +426,7 @@ __device__ __forceinline__ float beam_key(float d) {
 // y-lo, 1/width, 0.5)) (NaN -> 0), then the 7 popcount planes and the chunks
 // whose uint8 LUT entry would wrap.  Writes planes (8 x W words) and returns
 // low, width, sum_q.  `rot` is LDS scratch of B floats.
-__device__ void prepare_query(const float *__restrict__ query, const float *__restrict__ signs, int dim,
+__device__ __forceinline__ void prepare_query(const float *__restrict__ query, const float *__restrict__ signs, int dim,
                               int B, float *rot, float *qv, uint32_t *planes, float &low_out,
                               float &high_out, float &width_out, int &sumq_out, uint8_t *qdump) {
     const int lane = lane_id();
@@ -795,13 +795,13 @@ __device__ __forceinline__ void small_merge(int pbeam, uint2 *bp, const uint2 *m
 // writes outputs [d(t), d(t+1)) with d(t) = t * pbeam / active (at most 4,
 // since active >= pbeam / 4), its split point found by the reference's
 // binary search (utils.cuh:588-616); inside a segment beam entries go first
-// on ties (utils.cuh:652-671).  Lane l owns segments l*SPL .. l*SPL+SPL-1.
-// It searches its right boundaries; the left one is its neighbour's.  The
+// on ties (utils.cuh:652-671).  Each lane searches the right boundaries of
+// its segments; a left one is the previous segment's right one.  The
 // searches read the sentinel-padded arrays, so no bound needs a branch:
 // bp[-1], ms[-1] = -FLT_MAX and bp[pbeam], ms[32] = FLT_MAX stand for the
 // reference's out-of-range values.  Segments before `tbase` are not touched
 // (the caller has shown that they output the beam unchanged); lane l owns
-// segments tbase + l*SPL ...
+// segments tbase + l, tbase + 64 + l, ... (SPL of them).
 //
 // The splits valid at a diagonal d (i beam entries and d - i candidates,
 // with beam[i-1] <= cand[d-i] and cand[d-i-1] <= beam[i]) form an interval
@@ -819,15 +819,18 @@ __device__ __forceinline__ void merge_path(const SearchParams &P, uint2 *bp, con
                                            int tbase) {
     const int lane = lane_id_opaque();
     const int cbs = P.cbs, pbeam = P.pbeam, active = P.seg_active;
-    const int t0 = tbase + lane * SPL;
+    // step k of lane l: segment tbase + 64 k + l (consecutive lanes, and so
+    // nearby LDS addresses, in every step)
+    int tk[SPL], dl[SPL], dr[SPL], rl[SPL], rr[SPL];
+#pragma unroll
+    for (int k = 0; k < SPL; ++k) {
+        tk[k] = tbase + 64 * k + lane;
+        const int a = min(tk[k], active), b = min(tk[k] + 1, active);
+        dl[k] = static_cast<int>(__umulhi(static_cast<uint32_t>(a * pbeam), P.seg_magic));
+        dr[k] = static_cast<int>(__umulhi(static_cast<uint32_t>(b * pbeam), P.seg_magic));
+    }
     const float *bk = reinterpret_cast<const float *>(bp);  // key of entry i at bk[2 i]
     const float *mk = reinterpret_cast<const float *>(ms);
-    int dg[SPL + 1], res[SPL + 1];
-#pragma unroll
-    for (int k = 0; k <= SPL; ++k) {
-        const int t = min(t0 + k, active);
-        dg[k] = static_cast<int>(__umulhi(static_cast<uint32_t>(t * pbeam), P.seg_magic));
-    }
     bool replay = !fast_ok;
     if (fast_ok) {
         // pos holds a split with beam[pos-1] <= cand[d-pos] (true at lo0);
@@ -836,8 +839,8 @@ __device__ __forceinline__ void merge_path(const SearchParams &P, uint2 *bp, con
         int pos[SPL], hi[SPL], lo0[SPL], dd[SPL];
 #pragma unroll
         for (int k = 0; k < SPL; ++k) {
-            const bool act = t0 + k + 1 <= active;
-            dd[k] = act ? dg[k + 1] : 0;
+            const bool act = tk[k] + 1 <= active;
+            dd[k] = act ? dr[k] : 0;
             lo0[k] = max(dd[k] - cbs, 0);
             hi[k] = min(dd[k], pbeam);
             pos[k] = lo0[k];
@@ -857,7 +860,7 @@ __device__ __forceinline__ void merge_path(const SearchParams &P, uint2 *bp, con
             const bool below = r > lo0[k];  // then beam[r-1] and cand[d-r] both exist
             const float a = bk[2 * (below ? r : 1) - 2], b = mk[2 * (below ? dd[k] - r : 0)];
             tie |= below && a == b && a != FLT_MAX;
-            res[k + 1] = r;
+            rr[k] = r;
         }
         replay = any_lane(tie);
     }
@@ -866,10 +869,10 @@ __device__ __forceinline__ void merge_path(const SearchParams &P, uint2 *bp, con
         bool done[SPL];
 #pragma unroll
         for (int k = 0; k < SPL; ++k) {
-            lo[k] = max(dg[k + 1] - cbs, 0);
-            hi[k] = min(dg[k + 1], pbeam);
-            done[k] = t0 + k + 1 > active;
-            res[k + 1] = 0;
+            lo[k] = max(dr[k] - cbs, 0);
+            hi[k] = min(dr[k], pbeam);
+            done[k] = tk[k] + 1 > active;
+            rr[k] = 0;
         }
         for (;;) {
             bool live = false;
@@ -879,25 +882,31 @@ __device__ __forceinline__ void merge_path(const SearchParams &P, uint2 *bp, con
                 // trip, two ds_read2), then the reference's if / else-if / else
                 // picks the update
                 const bool exit_low = !done[k] && lo[k] > hi[k];  // loop exit: return low
-                res[k + 1] = exit_low ? lo[k] : res[k + 1];
+                rr[k] = exit_low ? lo[k] : rr[k];
                 done[k] = done[k] || exit_low;
                 const int ai = done[k] ? 0 : (lo[k] + hi[k]) >> 1;
-                const int bj = done[k] ? 0 : dg[k + 1] - ai;
+                const int bj = done[k] ? 0 : dr[k] - ai;
                 const float al = bk[2 * ai - 2], ar = bk[2 * ai];
                 const float bl = mk[2 * bj - 2], br = mk[2 * bj];
                 const bool go_left = al > br, go_right = !go_left && bl > ar;
                 const bool found = !done[k] && !go_left && !go_right;
                 hi[k] = (!done[k] && go_left) ? ai - 1 : hi[k];
                 lo[k] = (!done[k] && go_right) ? ai + 1 : lo[k];
-                res[k + 1] = found ? ai : res[k + 1];
+                rr[k] = found ? ai : rr[k];
                 done[k] = done[k] || found;
                 live |= !done[k];
             }
             if (!any_lane(live)) break;
         }
     }
-    res[0] = __builtin_amdgcn_update_dpp(0, res[SPL], 0x138, 0xF, 0xF, false);  // DPP wave_shr:1; lane 0 reads 0
-    if (lane == 0) res[0] = dg[0];  // segment tbase starts with beam entries only (d(0) = 0)
+    // left boundaries: the right boundary of the previous segment, on the
+    // lane below (DPP wave_shr:1), or for lane 0 on lane 63 of the previous
+    // step; segment tbase starts with beam entries only (d(0) = 0)
+#pragma unroll
+    for (int k = 0; k < SPL; ++k) {
+        rl[k] = __builtin_amdgcn_update_dpp(0, rr[k], 0x138, 0xF, 0xF, false);
+        if (lane == 0) rl[k] = k == 0 ? dl[0] : __builtin_amdgcn_readlane(rr[k > 0 ? k - 1 : 0], 63);
+    }
     // Each segment's na beam entries and nb candidates (na + nb <= 4) are
     // read into 4 slots: slot s is beam entry tb + s for s < na, candidate
     // cb + s - na after.  Output position of a slot = d(t) + the number of
@@ -908,23 +917,23 @@ __device__ __forceinline__ void merge_path(const SearchParams &P, uint2 *bp, con
     int nsl[SPL];
 #pragma unroll
     for (int k = 0; k < SPL; ++k) {
-        const bool act = t0 + k < active;
-        const int tb = act ? res[k] : 0;
-        const int cb = act ? dg[k] - res[k] : 0;
-        nsl[k] = act ? dg[k + 1] - dg[k] : 0;
+        const bool act = tk[k] < active;
+        const int tb = act ? rl[k] : 0;
+        const int cb = act ? dl[k] - rl[k] : 0;
+        nsl[k] = act ? dr[k] - dl[k] : 0;
         // The bisection resolves equal keys at each boundary on its own, so
         // two boundaries can disagree (seen at the first merge, where every
         // entry is the empty pair): more than nsl beam entries, or fewer
         // than none.  The reference's output loop then takes only beam
         // entries, or only candidates from cb on (utils.cuh:660-671), which is
         // what the count clamped to [0, nsl] gives.
-        const int na = act ? min(max(res[k + 1] - res[k], 0), nsl[k]) : 0;
+        const int na = act ? min(max(rr[k] - rl[k], 0), nsl[k]) : 0;
         bool ina[4];
 #pragma unroll
         for (int s2 = 0; s2 < 4; ++s2) {
             ina[s2] = s2 < na;
             slot[k][s2] = ina[s2] ? bp[tb + s2] : ms[cb + s2 - na];
-            pos[k][s2] = dg[k];
+            pos[k][s2] = dl[k];
         }
 #pragma unroll
         for (int s2 = 0; s2 < 4; ++s2)
