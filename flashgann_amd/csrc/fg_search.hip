@@ -1627,10 +1627,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
         // the picked entries' ids and distances go straight to the parent
         // lists (an unexpanded entry's id has the top bit clear)
         // Beams up to 256: lane l reads entry base + l (64 per step).  Larger
-        // beams, where the first unexpanded entry sits about halfway down:
-        // lane l scans entries base + 4 l .. base + 4 l + 3 (256 per step, in
-        // index order across lanes); a lane's rank offset is the exclusive
-        // prefix of the per-lane counts, summed from the ballots of their bits.
+        // beams, where the first unexpanded entry sits about halfway down: 256
+        // entries per step, from the first entry that can be unexpanded.
         uint32_t nexp = 0;
         if (beam_sz <= 256) {
             for (int base = 0; base < beam_sz; base += 64) {
@@ -1655,33 +1653,33 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
         } else {
           int lastj = -1;  // the entry that took rank theta - 1
           for (int base = scan_from; base < beam_sz; base += 256) {
-            const int j0 = base + 4 * lane;
+            // entry base + 64 k + l on lane l (each read covers 64
+            // consecutive entries); index order is k, then lane
             uint2 e[4];
-            bool fresh[4];
-            uint32_t cnt = 0;
+            uint64_t m[4];
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                const int j = j0 + k;
+                const int j = base + 64 * k + lane;
                 e[k] = bp[j < pbeam ? j : pbeam];  // unconditional read; bp[pbeam] is a sentinel
-                fresh[k] = j < beam_sz && (e[k].y & kMsb) == 0;
-                cnt += fresh[k] ? 1u : 0u;
+                m[k] = ballot(j < beam_sz && (e[k].y & kMsb) == 0);
             }
-            const uint64_t b0 = ballot(cnt & 1u), b1 = ballot(cnt & 2u), b2 = ballot(cnt & 4u);
             const uint64_t lt = (1ull << lane) - 1ull;
-            uint32_t r = nexp + static_cast<uint32_t>(__popcll(b0 & lt) + 2 * __popcll(b1 & lt) + 4 * __popcll(b2 & lt));
+            uint32_t before = nexp;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                if (fresh[k]) {
+                if (lane_in(m[k])) {
+                    const uint32_t r = before + static_cast<uint32_t>(__popcll(m[k] & lt));
                     if (r < static_cast<uint32_t>(theta)) {
+                        const int j = base + 64 * k + lane;
                         pnode[r] = e[k].y;
                         pdist[r] = __uint_as_float(e[k].x);
-                        bp[j0 + k].y = e[k].y | kMsb;
-                        if (r + 1 == static_cast<uint32_t>(theta)) lastj = j0 + k;
+                        bp[j].y = e[k].y | kMsb;
+                        if (r + 1 == static_cast<uint32_t>(theta)) lastj = j;
                     }
-                    ++r;
                 }
+                before += static_cast<uint32_t>(__popcll(m[k]));
             }
-            nexp += static_cast<uint32_t>(__popcll(b0) + 2 * __popcll(b1) + 4 * __popcll(b2));
+            nexp = before;
             if (nexp >= static_cast<uint32_t>(theta)) {
                 nexp = static_cast<uint32_t>(theta);
                 break;
