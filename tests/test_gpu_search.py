@@ -32,7 +32,8 @@ def _assert_equal(ids, cnt, ref_ids, ref_cnt, label):
 
 
 @pytest.mark.parametrize("K,beam", [(10, 16), (10, 64), (100, 100), (100, 128), (100, 256),
-                                    (100, 384), (100, 1000), (10, 1), (64, 32), (100, 1024)])
+                                    (100, 384), (100, 1000), (10, 1), (64, 32), (100, 1024),
+                                    (100, 257), (100, 300), (100, 640), (100, 896), (50, 777)])
 def test_search_int128_beams(gpu_available, K, beam):
     cb, q, _ = small_index()
     ids, cnt, rids, rcnt = _run(cb, q, K, beam)
