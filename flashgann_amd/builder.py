@@ -131,6 +131,7 @@ def knn_partitioned(x: torch.Tensor, k: int, cells: int | None = None, probes: i
     n, dim = x.shape
     dev = x.device
     cells = cells or max(1, min(n // 2500, 1 << 16))
+    probes = max(1, min(probes, cells))
     t0 = time.time()
     cen = kmeans(x, cells, seed=seed)
     near = _nearest_cells(x, cen, probes)

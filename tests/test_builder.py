@@ -157,6 +157,15 @@ def test_partitioned_knn_reduces_to_exact_knn():
     assert torch.equal(a_ids, b_ids) and torch.equal(a_d, b_d)
 
 
+def test_partitioned_knn_small_set_is_one_cell():
+    """Under 2,500 points the partition is one cell, searched exactly."""
+    import torch
+    from flashgann_amd import builder, datasets
+    base, _ = datasets.integer_mixture(1000, 1, 64, 4, config=1)
+    x = torch.as_tensor(base)
+    assert torch.equal(builder.knn(x, 16)[0], builder.knn_partitioned(x, 16)[0])
+
+
 def test_partitioned_knn_overlap_on_c5_mixture():
     """Two probed cells of eight find nearly all exact neighbours of the C5
     generator's well-separated anisotropic components."""
