@@ -45,7 +45,7 @@ constexpr int kMaxIterations = 1024;  // MAX_ITERATIONS (adaptive_search_config.
 constexpr int kHashReset = 16;        // SMALL_HASH_RESET_INTERVAL (utils.cuh:683)
 constexpr int kRefBlock = 256;        // reference block size: fixes merge-path segmentation
 constexpr int kMaxBeam = 1024;
-constexpr int kMaxDegree = 64;
+constexpr int kMaxDegree = 1024;
 constexpr int kMaxPaddedDim = 2048;
 constexpr float kPhase1Rho = 0.25f;   // PHASE1_RHO
 constexpr float kRhoMax = 0.99f;      // RHO_MAX
@@ -2198,7 +2198,7 @@ void compute_offsets(fg_index *ix) {
 int check_shape(uint32_t dim, uint32_t degree) {
     if (dim < 33 || dim > static_cast<uint32_t>(kMaxPaddedDim))
         return fail(FG_EINVAL, "dim must be in [33, 2048] (the code layout needs padded_dim >= 64)");
-    if (degree < 1 || degree > static_cast<uint32_t>(kMaxDegree)) return fail(FG_EINVAL, "degree must be in [1, 64]");
+    if (degree < 1 || degree > static_cast<uint32_t>(kMaxDegree)) return fail(FG_EINVAL, "degree must be in [1, 1024]");
     return FG_OK;
 }
 
@@ -2296,6 +2296,23 @@ int make_params(fg_index *ix, uint32_t nq, uint32_t K, uint32_t beam, SearchPara
     P.cbs = static_cast<int>(round_up_pow2(cap));
     P.collect_cap = P.cbs < kBufferBound ? P.cbs : kBufferBound;
     P.buckets = static_cast<int>(visited_buckets(beam, ix->degree));
+    // The reference's visited table has 2^bitlen slots with bitlen sized for
+    // 32 inserts per iteration (utils.cuh:137-151): 2048 at every beam up to
+    // 1024.  Between two resets it receives at most beam + 16 * 32 * tiles
+    // distinct keys; above 64 neighbours that can exceed its slots, and a full
+    // table reports new keys as visited, which no exact set reproduces.  Such
+    // (beam, degree) pairs are refused; every degree up to 64 fits.
+    {
+        const uint32_t tiles = (ix->degree + 31u) / 32u;
+        const uint32_t need = beam + 16u * 32u * tiles;
+        uint32_t target = ((static_cast<uint32_t>(P.pbeam) + 32u * 16u) * 4u + 2u) / 3u, cap = 1u << 11;
+        while (cap < target) cap <<= 1;
+        if (need > cap)
+            return fail(FG_EINVAL, "degree " + std::to_string(ix->degree) + " at beam " + std::to_string(beam) +
+                                       ": up to " + std::to_string(need) + " visited keys between resets exceed the " +
+                                       std::to_string(cap) + "-slot table whose overflow the search reproduces "
+                                       "(use a smaller beam or degree)");
+    }
     P.max_iter = static_cast<int>((beam * 11 + 9) / 10);  // gpu_search_adaptive.cu:96
     // merge-path segmentation of the reference's 256-thread block
     // (utils.cuh:633-641): ceil(pbeam / 4) rounded up to a multiple of 32

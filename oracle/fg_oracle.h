@@ -38,7 +38,7 @@ extern "C" {
 #define FGO_HASH_RESET 16         /* utils.cuh:683 */
 #define FGO_BQUERY 6              /* common.hpp:17 */
 #define FGO_MAX_BEAM 1024
-#define FGO_MAX_DEGREE 64
+#define FGO_MAX_DEGREE 1024
 #define FGO_MAX_PADDED_DIM 2048
 
 /* Codebook geometry (qg.hpp:66-73), all offsets in floats. */

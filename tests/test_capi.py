@@ -36,7 +36,7 @@ def test_shape_checks_before_device_use():
                            signs.ctypes.data_as(C.POINTER(C.c_float)), 0, 0, C.byref(h))
     assert rc == _lib.FG_EINVAL
     assert b"dim" in L.fg_last_error()
-    rc = L.fg_index_create(rows.ctypes.data_as(C.POINTER(C.c_float)), 4, 128, 65,
+    rc = L.fg_index_create(rows.ctypes.data_as(C.POINTER(C.c_float)), 4, 128, 1025,
                            signs.ctypes.data_as(C.POINTER(C.c_float)), 0, 0, C.byref(h))
     assert rc == _lib.FG_EINVAL and b"degree" in L.fg_last_error()
 

@@ -186,6 +186,29 @@ def test_search_degree_64(gpu_available):
     _degree_case(64)
 
 
+@pytest.mark.parametrize("degree,beam", [(80, 256), (96, 500)])
+def test_search_degree_above_64(gpu_available, degree, beam):
+    """Three 32-neighbour tiles per parent (three stage-II rounds per
+    iteration, compaction overflow reachable), at beams where the reference's
+    2048-slot visited table cannot fill."""
+    cb, q, _ = small_index(n=1500, nq=12, degree=degree)
+    ids, cnt, rids, rcnt = _run(cb, q, 100, beam)
+    _assert_equal(ids, cnt, rids, rcnt, f"degree={degree} beam={beam}")
+
+
+@pytest.mark.parametrize("degree,beam", [(96, 600), (128, 16)])
+def test_search_degree_table_overflow_rejected(gpu_available, degree, beam):
+    """Where the reference's visited table could fill (beam + 512 x tiles
+    keys above its 2048 slots), the search is refused before any launch."""
+    from flashgann_amd import FlashGannError, Index, _lib
+    cb, q, _ = small_index(n=600, nq=4, degree=degree)
+    ix = Index.from_codebook(cb)
+    with pytest.raises(FlashGannError) as e:
+        ix.search(q, 10, beam)
+    ix.close()
+    assert e.value.code == _lib.FG_EINVAL and "slot table" in str(e.value)
+
+
 def test_search_inner_product_generic(gpu_available):
     """Inner product on the generic geometry (300-d: padded dimension 512)."""
     cb, q, _ = small_index(n=1200, nq=8, dim=300, comps=8, kind="unit", use_ip=True)
