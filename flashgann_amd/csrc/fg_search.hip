@@ -962,6 +962,8 @@ __device__ __forceinline__ void merge_path(const SearchParams &P, uint2 *bp, con
 // every pair merged into this beam has a key in (-FLT_MAX, FLT_MAX) or is the
 // empty (FLT_MAX, MAX_INDEX) pair (merge_path's condition for its split
 // search).
+// BIG: pbeam > 256 (the merge-path with two or more segments per lane).
+template <bool BIG>
 __device__ __forceinline__ void merge_beam(const SearchParams &P, uint2 *bp, uint2 *ms, const float *cd,
                                            const uint32_t *ci, int span, bool &fast_ok, int &lb_out) {
     const int lane = lane_id_opaque();
@@ -978,14 +980,16 @@ __device__ __forceinline__ void merge_beam(const SearchParams &P, uint2 *bp, uin
     else sort32(ck, cv);
     if (h == 0) ms[nl] = make_uint2(__float_as_uint(ck), cv);
     __syncthreads();
-    if (pbeam == 128) {
-        small_merge<2, false>(pbeam, bp, ms, 2 * lane, true);
-    } else if (pbeam == 64) {
-        small_merge<1, false>(pbeam, bp, ms, lane, true);
-    } else if (pbeam == 32) {
-        small_merge<1, true>(pbeam, bp, ms, nl, h == 0);
-    } else if (P.seg_active <= 64) {
-        merge_path<1>(P, bp, ms, fast_ok, 0);  // one segment per lane: nothing to save
+    if constexpr (!BIG) {
+        if (pbeam == 128) {
+            small_merge<2, false>(pbeam, bp, ms, 2 * lane, true);
+        } else if (pbeam == 64) {
+            small_merge<1, false>(pbeam, bp, ms, lane, true);
+        } else if (pbeam == 32) {
+            small_merge<1, true>(pbeam, bp, ms, nl, h == 0);
+        } else {
+            merge_path<1>(P, bp, ms, fast_ok, 0);  // one segment per lane: nothing to save
+        }
     } else {
         // Segments whose outputs lie wholly at or before position lb, the
         // number of beam entries with a key below the smallest candidate's,
@@ -1479,7 +1483,7 @@ __device__ __forceinline__ void hash_contains_n(const uint32_t *t, uint32_t nb, 
 // >= 256) gets 4 (<= 128 VGPRs) for its wider load batches: at padded
 // dimension 1024 and up its LDS (raw query, planes, rotation scratch) holds
 // it to fewer waves than that anyway.
-template <int WT, int DPL, int DIM_T, int DEG_T, bool COUNT, bool PROF>
+template <int WT, int DPL, int DIM_T, int DEG_T, bool COUNT, bool PROF, bool BIG>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 : 5))) void fg_search_kernel(SearchParams P) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int qid = blockIdx.x;
@@ -1609,8 +1613,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
         // A search that runs all kMaxIterations iterations (max_iter > 1024,
         // i.e. beam >= 931) leaves the loop without passing here again and
         // merges after it.
-        merge_beam(P, bp, ms, cd, ci, cand_span, split_fast, lb_merge);
-        scan_from = min(scan_from, lb_merge);
+        merge_beam<BIG>(P, bp, ms, cd, ci, cand_span, split_fast, lb_merge);
+        if constexpr (BIG) scan_from = min(scan_from, lb_merge);
         FG_PHASE(2);
         if (iter >= P.max_iter) break;
         for (int i = beam_sz + lane; i < pbeam; i += 64) bp[i] = kEmpty;
@@ -1630,7 +1634,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
         // beams, where the first unexpanded entry sits about halfway down: 256
         // entries per step, from the first entry that can be unexpanded.
         uint32_t nexp = 0;
-        if (beam_sz <= 256) {
+        if constexpr (!BIG) {
             for (int base = 0; base < beam_sz; base += 64) {
                 const int j = base + lane;
                 const uint2 e = bp[j < pbeam ? j : pbeam];  // unconditional read; bp[pbeam] is a sentinel
@@ -2008,7 +2012,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 
     }
     // the loop ran out at kMaxIterations: the last iteration's exact-scored
     // candidates are still in the buffer (adaptive_search.cuh:449-451)
-    if (iter == kMaxIterations) merge_beam(P, bp, ms, cd, ci, cand_span, split_fast, lb_merge);
+    if (iter == kMaxIterations) merge_beam<BIG>(P, bp, ms, cd, ci, cand_span, split_fast, lb_merge);
 
     FG_PHASE(3);
     // result writer (adaptive_search.cuh:455-464)
@@ -2338,16 +2342,26 @@ int make_params(fg_index *ix, uint32_t nq, uint32_t K, uint32_t beam, SearchPara
     return FG_OK;
 }
 
-template <int WT, int DPL, int DIM_T, int DEG_T>
-void launch_geo(const SearchParams &P, hipStream_t stream, bool count, bool prof) {
+template <int WT, int DPL, int DIM_T, int DEG_T, bool BIG>
+void launch_geo_b(const SearchParams &P, hipStream_t stream, bool count, bool prof) {
     const dim3 grid(P.nq), block(64);
     if (prof)
-        hipLaunchKernelGGL((fg_search_kernel<WT, DPL, DIM_T, DEG_T, false, true>), grid, block, P.lds.total_prof,
-                           stream, P);
+        hipLaunchKernelGGL((fg_search_kernel<WT, DPL, DIM_T, DEG_T, false, true, BIG>), grid, block,
+                           P.lds.total_prof, stream, P);
     else if (count)
-        hipLaunchKernelGGL((fg_search_kernel<WT, DPL, DIM_T, DEG_T, true, false>), grid, block, P.lds.total, stream, P);
+        hipLaunchKernelGGL((fg_search_kernel<WT, DPL, DIM_T, DEG_T, true, false, BIG>), grid, block, P.lds.total,
+                           stream, P);
     else
-        hipLaunchKernelGGL((fg_search_kernel<WT, DPL, DIM_T, DEG_T, false, false>), grid, block, P.lds.total, stream, P);
+        hipLaunchKernelGGL((fg_search_kernel<WT, DPL, DIM_T, DEG_T, false, false, BIG>), grid, block, P.lds.total,
+                           stream, P);
+}
+
+// Beams over 256 (two or more merge-path segments per lane, the pick's wide
+// scan) and smaller ones run separately compiled kernels.
+template <int WT, int DPL, int DIM_T, int DEG_T>
+void launch_geo(const SearchParams &P, hipStream_t stream, bool count, bool prof) {
+    if (P.pbeam > 256) launch_geo_b<WT, DPL, DIM_T, DEG_T, true>(P, stream, count, prof);
+    else launch_geo_b<WT, DPL, DIM_T, DEG_T, false>(P, stream, count, prof);
 }
 
 // Shape classes: the benchmark shapes (d 128 / deg 32; d 96 / deg 32 and 16)
