@@ -518,58 +518,65 @@ __device__ __forceinline__ int32_t raw_partial(const uint32_t *__restrict__ code
     return static_cast<int32_t>(raw - 256u * wraps);
 }
 
+// sum_p 2^p popcount(c & plane_p) over NB code words starting at word w0,
+// plus the count of wrapped chunks among them.  NB is a compile-time width,
+// so the plane reads carry no per-step condition and can be issued ahead of
+// the popcounts that consume them.
+template <int NB>
+__device__ __forceinline__ void raw_span(const uint32_t *__restrict__ code, const uint32_t *planes, int W, int w0,
+                                         bool vec_ok, bool any_wrap, uint32_t &raw, uint32_t &wraps) {
+    uint32_t c[NB];
+    if (vec_ok) {
+#pragma unroll
+        for (int j = 0; j < NB / 4; ++j) {
+            const uint4 v = reinterpret_cast<const uint4 *>(code + w0)[j];
+            c[4 * j] = v.x; c[4 * j + 1] = v.y; c[4 * j + 2] = v.z; c[4 * j + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < NB; ++j) c[j] = code[w0 + j];
+    }
+    // top plane first (Horner's rule, one accumulate chain)
+    uint32_t hb = 0;
+#pragma unroll
+    for (int p = kPlanes - 1; p >= 0; --p) {
+        const uint4 *pl = reinterpret_cast<const uint4 *>(planes + p * W + w0);
+        uint32_t a = hb << 1;
+#pragma unroll
+        for (int j = 0; j < NB / 4; ++j) {
+            const uint4 q = pl[j];
+            a = bcnt_acc(c[4 * j] & q.x, a);
+            a = bcnt_acc(c[4 * j + 1] & q.y, a);
+            a = bcnt_acc(c[4 * j + 2] & q.z, a);
+            a = bcnt_acc(c[4 * j + 3] & q.w, a);
+        }
+        hb = a;
+    }
+    raw += hb;
+    if (any_wrap) {
+        const uint32_t *wp = planes + kPlanes * W + w0;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const uint32_t x = c[j] & wp[j];
+            wraps += __popc(x & (x >> 1) & (x >> 2) & (x >> 3) & 0x11111111u);
+        }
+    }
+}
+
 // raw for one neighbour code of W words (W a power of two >= 8: padded
 // dimension >= 256), the same sum as raw_partial over [0, W): the code words
 // are loaded 32 at a time (eight 16-byte loads when the row layout keeps
-// codes 16-byte aligned), issued together, and each plane's matching words
-// come from LDS as 16-byte reads.
+// codes 16-byte aligned), and each plane's matching words come from LDS as
+// 16-byte reads.
 __device__ __forceinline__ int32_t raw_words(const uint32_t *__restrict__ code, const uint32_t *planes, int W,
                                              bool vec_ok, bool any_wrap) {
-    uint32_t raw = 0;
-    uint32_t wraps = 0;
-    const int nb = W < 32 ? W : 32;  // words per batch: 8, 16 or 32
-    for (int w0 = 0; w0 < W; w0 += nb) {
-        uint32_t c[32];
-        if (vec_ok) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const uint4 v = j * 4 < nb ? reinterpret_cast<const uint4 *>(code + w0)[j] : make_uint4(0u, 0u, 0u, 0u);
-                c[4 * j] = v.x; c[4 * j + 1] = v.y; c[4 * j + 2] = v.z; c[4 * j + 3] = v.w;
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 32; ++j) c[j] = j < nb ? code[w0 + j] : 0u;
-        }
-        // this batch's sum_p 2^p popcount(c & plane_p), top plane first
-        // (Horner's rule, one accumulate chain)
-        uint32_t hb = 0;
-#pragma unroll
-        for (int p = kPlanes - 1; p >= 0; --p) {
-            const uint4 *pl = reinterpret_cast<const uint4 *>(planes + p * W + w0);
-            uint32_t a = hb << 1;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                if (j * 4 < nb) {
-                    const uint4 q = pl[j];
-                    a = bcnt_acc(c[4 * j] & q.x, a);
-                    a = bcnt_acc(c[4 * j + 1] & q.y, a);
-                    a = bcnt_acc(c[4 * j + 2] & q.z, a);
-                    a = bcnt_acc(c[4 * j + 3] & q.w, a);
-                }
-            }
-            hb = a;
-        }
-        raw += hb;
-        if (any_wrap) {
-            const uint32_t *wp = planes + kPlanes * W + w0;
-#pragma unroll
-            for (int j = 0; j < 32; ++j) {
-                if (j < nb) {
-                    const uint32_t x = c[j] & wp[j];
-                    wraps += __popc(x & (x >> 1) & (x >> 2) & (x >> 3) & 0x11111111u);
-                }
-            }
-        }
+    uint32_t raw = 0, wraps = 0;
+    if (W >= 32) {
+        for (int w0 = 0; w0 < W; w0 += 32) raw_span<32>(code, planes, W, w0, vec_ok, any_wrap, raw, wraps);
+    } else if (W == 16) {
+        raw_span<16>(code, planes, W, 0, vec_ok, any_wrap, raw, wraps);
+    } else {
+        raw_span<8>(code, planes, W, 0, vec_ok, any_wrap, raw, wraps);
     }
     return static_cast<int32_t>(raw - 256u * wraps);
 }

@@ -84,12 +84,15 @@ def _wrap_queries(signs, B, count, seed=12):
     return np.stack(out)
 
 
-def test_wrap_chunks_scores_and_search(gpu_available):
-    """The popcount planes' wrap correction reproduces the uint8 LUT."""
+@pytest.mark.parametrize("dim", [64, 256, 512, 1024, 2048])
+def test_wrap_chunks_scores_and_search(gpu_available, dim):
+    """The popcount planes' wrap correction reproduces the uint8 LUT, for
+    each code width the estimators have: 2 words (fixed geometry) and 8, 16,
+    32 and 2 x 32 words (generic geometry)."""
     from flashgann_amd import Index
     from oracle import oracle as O
-    cb, _, _ = small_index(n=1200, nq=4, dim=64, comps=8)
-    q = _wrap_queries(cb.signs, 64, 6)
+    cb, _, _ = small_index(n=1200, nq=4, dim=dim, comps=8)
+    q = _wrap_queries(cb.signs, dim, 6)
     ix = Index.from_codebook(cb)
     rng = np.random.default_rng(3)
     n = 200
@@ -100,11 +103,11 @@ def test_wrap_chunks_scores_and_search(gpu_available):
     L = O.lib()
     codes, fac = cb.codes(), cb.factors()
     for t in range(n):
-        qf = O.query_prepare(q[qi[t]], cb.signs, 64, 64)
-        pd = L.fgo_warp_l2(64, O.ptr(np.ascontiguousarray(q[qi[t]]), C.c_float),
-                           O.ptr(np.ascontiguousarray(cb.rows[pa[t], :64]), C.c_float))
+        qf = O.query_prepare(q[qi[t]], cb.signs, dim, dim)
+        pd = L.fgo_warp_l2(dim, O.ptr(np.ascontiguousarray(q[qi[t]]), C.c_float),
+                           O.ptr(np.ascontiguousarray(cb.rows[pa[t], :dim]), C.c_float))
         code = np.ascontiguousarray(codes[pa[t], sl[t]])
-        args = (float(fac[pa[t], 0, sl[t]]), float(fac[pa[t], 1, sl[t]]), float(fac[pa[t], 2, sl[t]]), pd, 64)
+        args = (float(fac[pa[t], 0, sl[t]]), float(fac[pa[t], 1, sl[t]]), float(fac[pa[t], 2, sl[t]]), pd, dim)
         assert np.float32(el[t]) == np.float32(L.fgo_estimate_lanes(C.byref(qf), O.ptr(code, C.c_uint8), *args))
         assert np.float32(es[t]) == np.float32(L.fgo_estimate_seq(C.byref(qf), O.ptr(code, C.c_uint8), *args))
     ids, _, cnt = ix.search(q, 10, 64, counters=True)
