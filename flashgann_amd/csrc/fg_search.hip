@@ -634,6 +634,38 @@ __device__ __forceinline__ float half_reduce(float val) {
 // half_distance), with the loads of KB consecutive steps of every child
 // issued together.  Indices past the row's dimension are clamped to its last
 // dimension and their terms skipped.
+// KB dimension steps of PB rows per half (lane nl: dimensions nl + 32 k in
+// turn).  CHECK: some step may lie past dim; such a step reads a valid
+// element and leaves the sum as it is.
+template <int PB, int KB, bool IP, bool CHECK>
+__device__ __forceinline__ void exact_generic_batch(const float *const (&rows)[PB], const float *qv, int dim, int nl,
+                                                    int k0, float (&acc)[PB]) {
+    float q[KB], v[PB][KB];
+    bool ok[KB];
+#pragma unroll
+    for (int kk = 0; kk < KB; ++kk) {
+        const int i = nl + 32 * (k0 + kk);
+        ok[kk] = !CHECK || i < dim;
+        const int is = ok[kk] ? i : dim - 1;
+        q[kk] = qv[is];
+#pragma unroll
+        for (int j = 0; j < PB; ++j) v[j][kk] = rows[j][is];
+    }
+#pragma unroll
+    for (int kk = 0; kk < KB; ++kk)
+#pragma unroll
+        for (int j = 0; j < PB; ++j) {
+            float t;
+            if constexpr (IP) {
+                t = fmaf(q[kk], v[j][kk], acc[j]);
+            } else {
+                const float d = q[kk] - v[j][kk];
+                t = fmaf(d, d, acc[j]);
+            }
+            acc[j] = ok[kk] ? t : acc[j];
+        }
+}
+
 template <int PB, int KB>
 __device__ __forceinline__ void exact_generic_pass(const SearchParams &P, uint64_t row_floats, int dim, int e0, int n,
                                                    const uint32_t *slot_list, float *cd, const uint32_t *ci,
@@ -651,32 +683,19 @@ __device__ __forceinline__ void exact_generic_pass(const SearchParams &P, uint64
     float acc[PB];
 #pragma unroll
     for (int j = 0; j < PB; ++j) acc[j] = 0.0f;
+    // the metric and the test for a step past the last dimension are taken
+    // outside the loops (inside, each dimension became both updates and two
+    // selects); only a batch that reaches past dim tests its steps
     const int steps = (dim + 31) >> 5;
     for (int k0 = 0; k0 < steps; k0 += KB) {
-        float q[KB], v[PB][KB];
-        bool ok[KB];
-#pragma unroll
-        for (int kk = 0; kk < KB; ++kk) {
-            const int i = nl + 32 * (k0 + kk);
-            ok[kk] = i < dim;
-            const int is = ok[kk] ? i : dim - 1;
-            q[kk] = qv[is];
-#pragma unroll
-            for (int j = 0; j < PB; ++j) v[j][kk] = rows[j][is];
+        const bool full = (k0 + KB) * 32 <= dim;
+        if (ip) {
+            if (full) exact_generic_batch<PB, KB, true, false>(rows, qv, dim, nl, k0, acc);
+            else exact_generic_batch<PB, KB, true, true>(rows, qv, dim, nl, k0, acc);
+        } else {
+            if (full) exact_generic_batch<PB, KB, false, false>(rows, qv, dim, nl, k0, acc);
+            else exact_generic_batch<PB, KB, false, true>(rows, qv, dim, nl, k0, acc);
         }
-#pragma unroll
-        for (int kk = 0; kk < KB; ++kk)
-#pragma unroll
-            for (int j = 0; j < PB; ++j) {
-                float t;
-                if (ip) {
-                    t = fmaf(q[kk], v[j][kk], acc[j]);
-                } else {
-                    const float d = q[kk] - v[j][kk];
-                    t = fmaf(d, d, acc[j]);
-                }
-                acc[j] = ok[kk] ? t : acc[j];
-            }
     }
 #pragma unroll
     for (int j = 0; j < PB; ++j) {
