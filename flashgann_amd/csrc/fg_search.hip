@@ -536,22 +536,37 @@ __device__ __forceinline__ void raw_span(const uint32_t *__restrict__ code, cons
 #pragma unroll
         for (int j = 0; j < NB; ++j) c[j] = code[w0 + j];
     }
-    // top plane first (Horner's rule, one accumulate chain)
-    uint32_t hb = 0;
+    // one accumulator per plane (seven independent chains), four words at
+    // a time: the seven plane reads of a group are in flight together, and
+    // the next group's reads are issued before this group's popcounts
+    uint32_t acc[kPlanes];
 #pragma unroll
-    for (int p = kPlanes - 1; p >= 0; --p) {
-        const uint4 *pl = reinterpret_cast<const uint4 *>(planes + p * W + w0);
-        uint32_t a = hb << 1;
+    for (int p = 0; p < kPlanes; ++p) acc[p] = 0;
+    uint4 cur[kPlanes], nxt[kPlanes];
 #pragma unroll
-        for (int j = 0; j < NB / 4; ++j) {
-            const uint4 q = pl[j];
-            a = bcnt_acc(c[4 * j] & q.x, a);
-            a = bcnt_acc(c[4 * j + 1] & q.y, a);
-            a = bcnt_acc(c[4 * j + 2] & q.z, a);
-            a = bcnt_acc(c[4 * j + 3] & q.w, a);
+    for (int p = 0; p < kPlanes; ++p) cur[p] = reinterpret_cast<const uint4 *>(planes + p * W + w0)[0];
+#pragma unroll
+    for (int j = 0; j < NB / 4; ++j) {
+        if (j + 1 < NB / 4) {
+#pragma unroll
+            for (int p = 0; p < kPlanes; ++p) nxt[p] = reinterpret_cast<const uint4 *>(planes + p * W + w0)[j + 1];
         }
-        hb = a;
+#pragma unroll
+        for (int p = 0; p < kPlanes; ++p) {
+            acc[p] = bcnt_acc(c[4 * j] & cur[p].x, acc[p]);
+            acc[p] = bcnt_acc(c[4 * j + 1] & cur[p].y, acc[p]);
+            acc[p] = bcnt_acc(c[4 * j + 2] & cur[p].z, acc[p]);
+            acc[p] = bcnt_acc(c[4 * j + 3] & cur[p].w, acc[p]);
+        }
+        if (j + 1 < NB / 4) {
+#pragma unroll
+            for (int p = 0; p < kPlanes; ++p) cur[p] = nxt[p];
+        }
     }
+    // sum_p 2^p acc[p], top plane first
+    uint32_t hb = acc[kPlanes - 1];
+#pragma unroll
+    for (int p = kPlanes - 2; p >= 0; --p) hb = (hb << 1) + acc[p];
     raw += hb;
     if (any_wrap) {
         const uint32_t *wp = planes + kPlanes * W + w0;
@@ -1506,11 +1521,12 @@ __device__ __forceinline__ void hash_contains_n(const uint32_t *t, uint32_t nb, 
 // (<= 96 VGPRs; the fixed-geometry kernels use 77-79, which leaves room for
 // a sixth), which LDS also allows for beams up to 256 (6,400 bytes a
 // workgroup at beam 256).  The generic-geometry instantiation (padded dimension
-// >= 256) gets 4 (<= 128 VGPRs) for its wider load batches: at padded
-// dimension 1024 and up its LDS (raw query, planes, rotation scratch) holds
-// it to fewer waves than that anyway.
+// >= 256) gets 3 (<= 168 VGPRs) for its wide code batches and the plane reads
+// it keeps in flight: at padded dimension 2048 its LDS (raw query, planes,
+// rotation scratch) holds it to 3 waves per SIMD anyway, and at 1024 a
+// 1,000-query launch fills one wave per SIMD.
 template <int WT, int DPL, int DIM_T, int DEG_T, bool COUNT, bool PROF, bool BIG>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 4 : 5))) void fg_search_kernel(SearchParams P) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 3 : 5))) void fg_search_kernel(SearchParams P) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int qid = blockIdx.x;
     if (qid >= P.nq) return;
