@@ -168,8 +168,12 @@ def knn_partitioned(x: torch.Tensor, k: int, cells: int | None = None, probes: i
             d.clamp_(min=0.0)
             d.masked_fill_(qp[:, None] == mem[None, :], float("inf"))
             dv, di = torch.topk(d, kk, dim=1, largest=False, sorted=False)
-            cid[qs, :kk] = mem[di].to(torch.int32)
-            cdist[qs, :kk] = dv
+            # a cell with fewer than kk other points returns the point itself
+            # (at distance inf): it is no neighbour
+            ids = mem[di]
+            own = ids == qp[:, None]
+            cid[qs, :kk] = torch.where(own, torch.full_like(ids, -1), ids).to(torch.int32)
+            cdist[qs, :kk] = torch.where(own, torch.full_like(dv, float("inf")), dv)
         if verbose and (c + 1) % 1000 == 0:
             print(f"[builder] cell {c + 1}/{cells} searched ({time.time() - t0:.1f}s)", flush=True)
     del order, qorder, xn

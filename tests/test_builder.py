@@ -166,6 +166,22 @@ def test_partitioned_knn_small_set_is_one_cell():
     assert torch.equal(builder.knn(x, 16)[0], builder.knn_partitioned(x, 16)[0])
 
 
+def test_partitioned_knn_never_returns_the_point_itself():
+    """Cells smaller than k + 1 points: a point's own row is never one of
+    its neighbours; slots without a candidate are -1 at distance inf."""
+    import torch
+    from flashgann_amd import builder, datasets
+    base, _ = datasets.integer_mixture(60, 1, 16, 4, config=1)
+    x = torch.as_tensor(base)
+    ids, d = builder.knn_partitioned(x, 40, cells=6, probes=2)
+    own = torch.arange(60)[:, None]
+    assert not (ids == own).any()
+    assert ((ids >= 0) | torch.isinf(d)).all()
+    assert torch.isinf(d[ids < 0]).all()
+    g = builder.build_graph(x, 16, knn_method="partitioned")
+    assert not (g == own).any()
+
+
 def test_partitioned_knn_overlap_on_c5_mixture():
     """Two probed cells of eight find nearly all exact neighbours of the C5
     generator's well-separated anisotropic components."""
