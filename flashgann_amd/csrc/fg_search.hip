@@ -50,7 +50,9 @@ constexpr int kMaxPaddedDim = 2048;
 constexpr float kPhase1Rho = 0.25f;   // PHASE1_RHO
 constexpr float kRhoMax = 0.99f;      // RHO_MAX
 constexpr int kStallIters = 4;        // TOP1_WARMUP_STALL_ITERS
-constexpr int kPlanes = 7;            // q in [1, 64] needs 7 bit-planes
+constexpr int kPlanes = 6;            // q in [1, 64]: q - 1 needs 6 bit-planes
+constexpr int kWrapPlane = 6;         // chunks whose four levels are all 64
+constexpr int kZeroPlane = 7;         // levels that are 0 (a degenerate query only)
 
 // ------------------------------------------------------------ host+device
 
@@ -471,15 +473,22 @@ __device__ __forceinline__ void prepare_query(const float *__restrict__ query, c
         const uint32_t q = isnan(scaled) ? 0u : static_cast<uint32_t>(roundf(scaled));
         if (qdump) qdump[i] = static_cast<uint8_t>(q);
         sum += static_cast<int>(q);
+        // planes of q - 1: a code's sum over its set bits is then
+        // popcount(code) + sum_p 2^p popcount(code & plane_p), minus the set
+        // bits at level 0 (plane kZeroPlane; only a query whose rotation is
+        // constant or not finite has such levels, and then all of them)
+        const uint32_t r = q != 0u ? q - 1u : 0u;
         for (int p = 0; p < kPlanes; ++p) {
-            const uint64_t m = ballot(((q >> p) & 1u) != 0u);
+            const uint64_t m = ballot(((r >> p) & 1u) != 0u);
             if (nl == 0) planes[p * W + w] = half_bits(m, h);
         }
+        const uint64_t zm = ballot(q == 0u);
+        if (nl == 0) planes[kZeroPlane * W + w] = half_bits(zm, h);
         // a chunk's full-nibble LUT entry is (q0+q1+q2+q3) mod 256 (utils.cuh:913-917)
         uint32_t s = q + xshfl(q, 1);
         s += xshfl(s, 2);
         const uint64_t wm = ballot(s >= 256u);
-        if (nl == 0) planes[kPlanes * W + w] = half_bits(wm, h);
+        if (nl == 0) planes[kWrapPlane * W + w] = half_bits(wm, h);
     }
     sumq_out = uni(wave_sum(sum));
     low_out = lo;
@@ -498,33 +507,38 @@ __device__ __forceinline__ uint32_t bcnt_acc(uint32_t x, uint32_t acc) {
     return r;
 }
 
-// raw = sum_cb LUT[cb][nibble] (utils.cuh:976-980) over code words [w0, w1).
+// raw = sum_cb LUT[cb][nibble] (utils.cuh:976-980) over code words [w0, w1):
+// popcount(code) + sum_p 2^p popcount(code & plane_p) (the planes hold
+// q - 1), less the set bits at level 0 and 256 per wrapped chunk.
 __device__ __forceinline__ int32_t raw_partial(const uint32_t *__restrict__ code, int w0, int w1,
                                                const uint32_t *planes, int W) {
     uint32_t acc[kPlanes];
 #pragma unroll
     for (int p = 0; p < kPlanes; ++p) acc[p] = 0;
-    uint32_t wraps = 0;
+    uint32_t ones = 0, zeros = 0, wraps = 0;
     for (int w = w0; w < w1; ++w) {
         const uint32_t c = code[w];
 #pragma unroll
         for (int p = 0; p < kPlanes; ++p) acc[p] += __popc(c & planes[p * W + w]);
-        const uint32_t x = c & planes[kPlanes * W + w];
+        ones += __popc(c);
+        zeros += __popc(c & planes[kZeroPlane * W + w]);
+        const uint32_t x = c & planes[kWrapPlane * W + w];
         wraps += __popc(x & (x >> 1) & (x >> 2) & (x >> 3) & 0x11111111u);
     }
-    uint32_t raw = 0;
+    uint32_t raw = ones - zeros;
 #pragma unroll
     for (int p = 0; p < kPlanes; ++p) raw += acc[p] << p;
     return static_cast<int32_t>(raw - 256u * wraps);
 }
 
-// sum_p 2^p popcount(c & plane_p) over NB code words starting at word w0,
-// plus the count of wrapped chunks among them.  NB is a compile-time width,
+// popcount(c) + sum_p 2^p popcount(c & plane_p) - popcount(c & zero plane)
+// over NB code words starting at word w0 (added to raw), and the count of
+// wrapped chunks among them (added to wraps).  NB is a compile-time width,
 // so the plane reads carry no per-step condition and can be issued ahead of
 // the popcounts that consume them.
 template <int NB>
 __device__ __forceinline__ void raw_span(const uint32_t *__restrict__ code, const uint32_t *planes, int W, int w0,
-                                         bool vec_ok, bool any_wrap, uint32_t &raw, uint32_t &wraps) {
+                                         bool vec_ok, bool any_wrap, bool any_zero, uint32_t &raw, uint32_t &wraps) {
     uint32_t c[NB];
     if (vec_ok) {
 #pragma unroll
@@ -536,12 +550,15 @@ __device__ __forceinline__ void raw_span(const uint32_t *__restrict__ code, cons
 #pragma unroll
         for (int j = 0; j < NB; ++j) c[j] = code[w0 + j];
     }
-    // one accumulator per plane (seven independent chains), four words at
-    // a time: the seven plane reads of a group are in flight together, and
-    // the next group's reads are issued before this group's popcounts
+    // one accumulator per plane (six independent chains), four words at a
+    // time: the six plane reads of a group are in flight together, and the
+    // next group's reads are issued before this group's popcounts; the
+    // code's own popcount (the level offset 1) joins plane 0's chain
     uint32_t acc[kPlanes];
 #pragma unroll
     for (int p = 0; p < kPlanes; ++p) acc[p] = 0;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[0] = bcnt_acc(c[j], acc[0]);
     uint4 cur[kPlanes], nxt[kPlanes];
 #pragma unroll
     for (int p = 0; p < kPlanes; ++p) cur[p] = reinterpret_cast<const uint4 *>(planes + p * W + w0)[0];
@@ -568,8 +585,13 @@ __device__ __forceinline__ void raw_span(const uint32_t *__restrict__ code, cons
 #pragma unroll
     for (int p = kPlanes - 2; p >= 0; --p) hb = (hb << 1) + acc[p];
     raw += hb;
+    if (any_zero) {
+        const uint32_t *zp = planes + kZeroPlane * W + w0;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) raw -= static_cast<uint32_t>(__popc(c[j] & zp[j]));
+    }
     if (any_wrap) {
-        const uint32_t *wp = planes + kPlanes * W + w0;
+        const uint32_t *wp = planes + kWrapPlane * W + w0;
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
             const uint32_t x = c[j] & wp[j];
@@ -584,14 +606,14 @@ __device__ __forceinline__ void raw_span(const uint32_t *__restrict__ code, cons
 // codes 16-byte aligned), and each plane's matching words come from LDS as
 // 16-byte reads.
 __device__ __forceinline__ int32_t raw_words(const uint32_t *__restrict__ code, const uint32_t *planes, int W,
-                                             bool vec_ok, bool any_wrap) {
+                                             bool vec_ok, bool any_wrap, bool any_zero) {
     uint32_t raw = 0, wraps = 0;
     if (W >= 32) {
-        for (int w0 = 0; w0 < W; w0 += 32) raw_span<32>(code, planes, W, w0, vec_ok, any_wrap, raw, wraps);
+        for (int w0 = 0; w0 < W; w0 += 32) raw_span<32>(code, planes, W, w0, vec_ok, any_wrap, any_zero, raw, wraps);
     } else if (W == 16) {
-        raw_span<16>(code, planes, W, 0, vec_ok, any_wrap, raw, wraps);
+        raw_span<16>(code, planes, W, 0, vec_ok, any_wrap, any_zero, raw, wraps);
     } else {
-        raw_span<8>(code, planes, W, 0, vec_ok, any_wrap, raw, wraps);
+        raw_span<8>(code, planes, W, 0, vec_ok, any_wrap, any_zero, raw, wraps);
     }
     return static_cast<int32_t>(raw - 256u * wraps);
 }
@@ -1231,12 +1253,13 @@ __device__ __forceinline__ uint32_t plane_step(const uint32_t *c, const uint32_t
 }
 
 // raw for NB code blocks at once, walking the planes one at a time from LDS
-// (one plane's WT words live at a time), top plane first: raw_b = sum_p 2^p
-// popcount(code_b & plane_p) - 256 * wraps_b, the powers of two by Horner's
-// rule (one shift per plane and block).
+// (one plane's WT words live at a time), top plane first: raw_b =
+// popcount(code_b) + sum_p 2^p popcount(code_b & plane_p) (the planes hold
+// q - 1) - popcount(code_b & zero plane) - 256 * wraps_b, the powers of two
+// by Horner's rule (one shift per plane and block).
 template <int NB, int WT>
 __device__ __forceinline__ void raw_batch(const uint32_t (&c)[NB][WT], const uint32_t *planes, bool any_wrap,
-                                          int32_t (&raw)[NB]) {
+                                          bool any_zero, int32_t (&raw)[NB]) {
     uint32_t acc[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[b] = 0;
@@ -1248,10 +1271,23 @@ __device__ __forceinline__ void raw_batch(const uint32_t (&c)[NB][WT], const uin
 #pragma unroll
         for (int b = 0; b < NB; ++b) acc[b] = plane_step<WT>(c[b], pw, acc[b], p == kPlanes - 1);
     }
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int w = 0; w < WT; ++w) acc[b] = bcnt_acc(c[b][w], acc[b]);
+    if (any_zero) {
+        uint32_t pw[WT];
+#pragma unroll
+        for (int w = 0; w < WT; ++w) pw[w] = planes[kZeroPlane * WT + w];
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int w = 0; w < WT; ++w) acc[b] -= static_cast<uint32_t>(__popc(c[b][w] & pw[w]));
+    }
     if (any_wrap) {
         uint32_t pw[WT];
 #pragma unroll
-        for (int w = 0; w < WT; ++w) pw[w] = planes[kPlanes * WT + w];
+        for (int w = 0; w < WT; ++w) pw[w] = planes[kWrapPlane * WT + w];
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
             uint32_t wr = 0;
@@ -1578,16 +1614,24 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 3 
     constexpr int WTR = WT > 0 ? WT : 1;
     // whether any chunk of the quantized query wraps the reference's uint8
     // LUT entry (then the estimates subtract the wrapped chunks)
-    bool any_wrap = false;
+    bool any_wrap = false, any_zero = false;
     if constexpr (WT > 0) {
-        uint32_t wor = 0;
+        uint32_t wor = 0, zor = 0;
 #pragma unroll
-        for (int w = 0; w < WT; ++w) wor |= planes[kPlanes * WT + w];
+        for (int w = 0; w < WT; ++w) {
+            wor |= planes[kWrapPlane * WT + w];
+            zor |= planes[kZeroPlane * WT + w];
+        }
         any_wrap = uni(wor) != 0u;
+        any_zero = uni(zor) != 0u;
     } else {
-        uint32_t wor = 0;
-        for (int w = lane; w < W; w += 64) wor |= planes[kPlanes * W + w];
+        uint32_t wor = 0, zor = 0;
+        for (int w = lane; w < W; w += 64) {
+            wor |= planes[kWrapPlane * W + w];
+            zor |= planes[kZeroPlane * W + w];
+        }
         any_wrap = any_lane(wor != 0u);
+        any_zero = any_lane(zor != 0u);
     }
     constexpr int DPLR = DPL > 0 ? DPL : 1;
     float qr[DPLR];
@@ -1785,10 +1829,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 3 
                 int32_t r1[1] = {0};
                 if constexpr (WT > 0) {
                     // computed on every lane, selected for the valid ones
-                    raw_batch<1, WT>(c1, planes, any_wrap, r1);
+                    raw_batch<1, WT>(c1, planes, any_wrap, any_zero, r1);
                     est = tx == FLT_MAX ? 0.0f : estimate_formula(r1[0], sum_q, qwidth, qlow, tx, fdq, fvq, pd0);
                 } else if (valid) {
-                    const int32_t raw = raw_words(codes + static_cast<uint64_t>(nsafe) * W, planes, W, vec_ok, any_wrap);
+                    const int32_t raw = raw_words(codes + static_cast<uint64_t>(nsafe) * W, planes, W, vec_ok, any_wrap, any_zero);
                     est = tx == FLT_MAX ? 0.0f : estimate_formula(raw, sum_q, qwidth, qlow, tx, fdq, fvq, pd0);
                 }
                 const bool fin = isfinite(est);
@@ -1950,7 +1994,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 3 
                 // (d) estimates, kth-near counts, keep decisions
                 uint64_t klm[SR];
                 int32_t rawb[SR];
-                if constexpr (WT > 0) raw_batch<SR, WT>(code, planes, any_wrap, rawb);
+                if constexpr (WT > 0) raw_batch<SR, WT>(code, planes, any_wrap, any_zero, rawb);
 #pragma unroll
                 for (int sr = 0; sr < SR; ++sr) {
                     float est = FLT_MAX;
@@ -1965,7 +2009,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 3 
                         const int nidx = tsk[sr] + nlg;
                         const int32_t raw = raw_words(reinterpret_cast<const uint32_t *>(prw[sr] + g.code) +
                                                           static_cast<uint64_t>(nidx) * W,
-                                                      planes, W, vec_ok, any_wrap);
+                                                      planes, W, vec_ok, any_wrap, any_zero);
                         est = estimate_formula(raw, sum_q, qwidth, qlow, tx[sr], fdq[sr], fvq[sr], pdist[pix[sr]]);
                     }
                     // a scored child with a non-finite estimate is dropped
@@ -2145,24 +2189,27 @@ __global__ __launch_bounds__(64) void fg_score_kernel(ScoreParams S) {
     // the search kernel's own routines: raw_batch for padded dimensions 64 and
     // 128 (W = 2, 4; the fixed geometries), raw_words for W >= 8
     const bool vec_ok = S.row_offset % 4 == 0 && S.code_offset % 4 == 0;
-    uint32_t wor = 0;
-    for (int w = 0; w < W; ++w) wor |= planes[kPlanes * W + w];
-    const bool any_wrap = uni(wor) != 0u;
+    uint32_t wor = 0, zor = 0;
+    for (int w = 0; w < W; ++w) {
+        wor |= planes[kWrapPlane * W + w];
+        zor |= planes[kZeroPlane * W + w];
+    }
+    const bool any_wrap = uni(wor) != 0u, any_zero = uni(zor) != 0u;
     int32_t raw_full;
     if (W == 4 || W == 2) {
         int32_t r[1];
         if (W == 4) {
             uint32_t c[1][4];
             load_code<4>(code, vec_ok, c[0]);
-            raw_batch<1, 4>(c, planes, any_wrap, r);
+            raw_batch<1, 4>(c, planes, any_wrap, any_zero, r);
         } else {
             uint32_t c[1][2];
             load_code<2>(code, vec_ok, c[0]);
-            raw_batch<1, 2>(c, planes, any_wrap, r);
+            raw_batch<1, 2>(c, planes, any_wrap, any_zero, r);
         }
         raw_full = r[0];
     } else {
-        raw_full = raw_words(code, planes, W, vec_ok, any_wrap);
+        raw_full = raw_words(code, planes, W, vec_ok, any_wrap, any_zero);
     }
     const float el = tx == FLT_MAX ? 0.0f : estimate_formula(raw_split, sq, w, lo, tx, fdq, fvq, pd);
     const float es = tx == FLT_MAX ? FLT_MAX : estimate_formula(raw_full, sq, w, lo, tx, fdq, fvq, pd);

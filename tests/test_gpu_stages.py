@@ -115,3 +115,39 @@ def test_wrap_chunks_scores_and_search(gpu_available, dim):
     assert np.array_equal(ids, rids)
     assert np.array_equal(cnt, rcnt.view(np.uint32).reshape(-1, 6))
     ix.close()
+
+
+@pytest.mark.parametrize("kind,dim,n", [("int", 64, 1200), ("int", 128, 1500), ("unit", 96, 1500), ("box", 960, 1500)])
+def test_zero_level_query_scores_and_search(gpu_available, kind, dim, n):
+    """A query whose rotation is constant (the zero vector: width 0)
+    quantizes every level to 0, so the estimator's level-0 correction is the
+    whole sum: scores equal the oracle's bit for bit, and so do the search's
+    ids and counters, for code widths of 2, 4 and 32 words."""
+    from flashgann_amd import Index
+    from oracle import oracle as O
+    cb, q, _ = small_index(n=n, nq=4, dim=dim, comps=8, kind=kind)
+    zq = np.concatenate([np.zeros((2, dim), np.float32), q[:2]])
+    ix = Index.from_codebook(cb)
+    rng = np.random.default_rng(8)
+    m = 120
+    qi = rng.integers(0, 2, m).astype(np.uint32)
+    pa = rng.integers(0, cb.npoints, m).astype(np.uint32)
+    sl = rng.integers(0, cb.layout.degree, m).astype(np.uint32)
+    el, es, _ = ix.score_edges(zq, qi, pa, sl)
+    L = O.lib()
+    codes, fac = cb.codes(), cb.factors()
+    B = cb.layout.padded_dim
+    for t in range(m):
+        qf = O.query_prepare(zq[qi[t]], cb.signs, dim, B)
+        assert np.ctypeslib.as_array(qf.q)[:B].max() == 0
+        pd = L.fgo_warp_l2(dim, O.ptr(np.ascontiguousarray(zq[qi[t]]), C.c_float),
+                           O.ptr(np.ascontiguousarray(cb.rows[pa[t], :dim]), C.c_float))
+        code = np.ascontiguousarray(codes[pa[t], sl[t]])
+        args = (float(fac[pa[t], 0, sl[t]]), float(fac[pa[t], 1, sl[t]]), float(fac[pa[t], 2, sl[t]]), pd, B)
+        assert np.float32(el[t]) == np.float32(L.fgo_estimate_lanes(C.byref(qf), O.ptr(code, C.c_uint8), *args))
+        assert np.float32(es[t]) == np.float32(L.fgo_estimate_seq(C.byref(qf), O.ptr(code, C.c_uint8), *args))
+    ids, _, cnt = ix.search(zq, 10, 64, counters=True)
+    rids, rcnt = O.OracleIndex.from_codebook(cb).search(zq, 10, 64)
+    assert np.array_equal(ids, rids)
+    assert np.array_equal(cnt, rcnt.view(np.uint32).reshape(-1, 6))
+    ix.close()
