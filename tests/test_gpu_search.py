@@ -86,6 +86,16 @@ def test_search_dim1536(gpu_available):
     _assert_equal(ids, cnt, rids, rcnt, "aniso1536 beam 32")
 
 
+@pytest.mark.parametrize("dim,kind,n,K,beam", [(960, "box", 1500, 100, 384), (960, "box", 1500, 100, 640),
+                                               (1536, "aniso", 1200, 100, 768), (300, "unit", 1200, 10, 1000)])
+def test_search_generic_large_beams(gpu_available, dim, kind, n, K, beam):
+    """The generic geometry's beams over 256 (its merge over segment-strided
+    lanes and the wide pick), as the C4 and C5 operating points run them."""
+    cb, q, _ = small_index(n=n, nq=8, dim=dim, comps=8, kind=kind)
+    ids, cnt, rids, rcnt = _run(cb, q, K, beam)
+    _assert_equal(ids, cnt, rids, rcnt, f"{kind}{dim} beam {beam}")
+
+
 @pytest.mark.parametrize("bad", ["inf", "nan"])
 def test_search_non_finite_distances(gpu_available, bad):
     """One row in twenty gets a vector that overflows (1e30: exact distances
