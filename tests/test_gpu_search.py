@@ -70,6 +70,15 @@ def test_search_inner_product(gpu_available):
     _assert_equal(ids, cnt, rids, rcnt, "ip96")
 
 
+@pytest.mark.parametrize("dim,kind,K,beam", [(128, "unit", 100, 256), (128, "unit", 100, 512), (960, "box", 100, 384)])
+def test_search_inner_product_beams(gpu_available, dim, kind, K, beam):
+    """Inner product on the headline's fixed 128-d kernel (both merge builds)
+    and on the generic geometry at a beam over 256."""
+    cb, q, _ = small_index(n=2000 if dim == 128 else 1500, nq=8, dim=dim, comps=16, kind=kind, use_ip=True)
+    ids, cnt, rids, rcnt = _run(cb, q, K, beam, metric=1)
+    _assert_equal(ids, cnt, rids, rcnt, f"ip{dim} beam {beam}")
+
+
 def test_search_dim960(gpu_available):
     cb, q, _ = small_index(n=1500, nq=8, dim=960, comps=8, kind="box")
     ids, cnt, rids, rcnt = _run(cb, q, 100, 128)
