@@ -129,7 +129,7 @@ __host__ __device__ inline uint32_t visited_buckets(uint32_t beam, uint32_t degr
 
 struct LdsLayout {
     uint32_t hash_off, beam_off, cand_off, msort_off, query_off, plane_off, scratch_off, prof_off, total,
-        total_prof;
+        total_prof, team_off, total_team;
 };
 
 // Sorted-candidate staging for the beam merge: (distance, id) pairs at
@@ -142,6 +142,36 @@ constexpr uint32_t kMsortPairs = 38;
 // entries (segment reads may run up to 3 past pbeam; the merge's unused
 // slots are written to pbeam + 2).
 constexpr uint32_t kBeamPad = 4;
+
+// A team launch runs each query on two waves: the lead wave runs the search,
+// the helper takes half of every stage-II round (visited tests, estimates
+// and keep decisions of its tasks) and half of every exact-distance batch.
+// They meet at workgroup barriers and exchange through this LDS block.
+struct TeamBlock {
+    // per iteration, from the lead wave: stop flag, theta, rho, K-th cutoff,
+    // number of expanders; then the exact batch's size and list kind
+    uint32_t stop, theta, nexp, kth_bits, rho_bits, ex_n, ex_alist, pad0;
+    // per query (written once): the quantised query's constants
+    uint32_t sum_q, qwidth_bits, qlow_bits, any_wrap, any_zero;
+    // the helper's work counters (counting build)
+    uint32_t c_ids, c_est, pad1;
+    // the helper's stage-II results: kept-lane masks and child ids of its
+    // sub-rounds
+    uint64_t klm[2];
+    uint32_t cid[2][64];
+};
+constexpr uint32_t kTeamBytes = 640;
+static_assert(sizeof(TeamBlock) <= kTeamBytes, "team block");
+
+// The lead wave's way out of the search loop in the team form: it tells the
+// helper to stop at their meeting point (the helper then leaves too).
+template <int NW>
+__device__ __forceinline__ void team_stop(TeamBlock *tb, int lane) {
+    if constexpr (NW > 1) {
+        if (lane == 0) tb->stop = 1u;
+        __syncthreads();
+    }
+}
 
 
 // Per-query LDS: visited table and beam (aliased by the rotated query during
@@ -180,6 +210,9 @@ __host__ __device__ constexpr LdsLayout lds_layout(uint32_t dim, uint32_t padded
     // phase timers of the profiling build only, past the end of the rest
     L.prof_off = L.total;
     L.total_prof = L.total + 16u * 8u;
+    // a team launch's exchange block (the profiling build has no team form)
+    L.team_off = L.total;
+    L.total_team = L.total + kTeamBytes;
     return L;
 }
 
@@ -202,6 +235,7 @@ struct SearchParams {
     int dup_free;
     int vec_ok;
     int runtime_geo;  // host only: run the runtime-geometry kernels
+    int team;         // host only: the team form (two waves per query) may run
     uint32_t entry;
     int nq;
     LdsLayout lds;
@@ -423,11 +457,29 @@ __device__ __forceinline__ float beam_key(float d) {
 
 // ------------------------------------------------------------ query preparation
 
+// Orders the LDS accesses of code that the search's lead wave runs alone.
+// NW = 1 (one wave per workgroup): the workgroup barrier, which the compiler
+// reduces to a wave barrier.  NW > 1 (a team of waves per query, the others
+// waiting at a workgroup barrier meanwhile): a wavefront-scope fence, since
+// one wave's LDS operations complete in issue order.
+template <int NW>
+__device__ __forceinline__ void lead_sync() {
+    if constexpr (NW == 1) {
+        __syncthreads();
+    } else {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+}
+
 // utils.cuh:790-939 for one wave: rotate (x*signs, pad, FWHT len = 1..B/2 with
 // butterflies (u+v, u-v)), min/max, width = (hi-lo)*fl(1/63), q = round(fma(
-// y-lo, 1/width, 0.5)) (NaN -> 0), then the 7 popcount planes and the chunks
-// whose uint8 LUT entry would wrap.  Writes planes (8 x W words) and returns
-// low, width, sum_q.  `rot` is LDS scratch of B floats.
+// y-lo, 1/width, 0.5)) (NaN -> 0), then the 6 popcount planes of q - 1, the
+// level-0 mask and the chunks whose uint8 LUT entry would wrap.  Writes
+// planes (8 x W words) and returns low, width, sum_q.  `rot` is LDS scratch
+// of B floats.
+template <int NW = 1>
 __device__ __forceinline__ void prepare_query(const float *__restrict__ query, const float *__restrict__ signs, int dim,
                               int B, float *rot, float *qv, uint32_t *planes, float &low_out,
                               float &high_out, float &width_out, int &sumq_out, uint8_t *qdump) {
@@ -441,7 +493,7 @@ __device__ __forceinline__ void prepare_query(const float *__restrict__ query, c
         }
         rot[i] = x;
     }
-    __syncthreads();
+    lead_sync<NW>();
     for (int len = 1; len < B; len <<= 1) {
         for (int p = lane; p < (B >> 1); p += 64) {
             const int blk = p / len, j = p - blk * len;
@@ -450,7 +502,7 @@ __device__ __forceinline__ void prepare_query(const float *__restrict__ query, c
             rot[i1] = u + v;
             rot[i2] = u - v;
         }
-        __syncthreads();
+        lead_sync<NW>();
     }
     float lo = FLT_MAX, hi = -FLT_MAX;
     for (int i = lane; i < B; i += 64) {
@@ -494,7 +546,7 @@ __device__ __forceinline__ void prepare_query(const float *__restrict__ query, c
     low_out = lo;
     high_out = hi;
     width_out = width;
-    __syncthreads();
+    lead_sync<NW>();
 }
 
 // popcount(x) + acc as one v_bcnt_u32_b32.  Written as an instruction so a
@@ -877,7 +929,7 @@ __device__ __forceinline__ void small_merge(int pbeam, uint2 *bp, const uint2 *m
 // outside (-FLT_MAX, FLT_MAX) has been merged into this beam), and every
 // split of such a tie gives the same output.  Any other equal pair sends the
 // whole wave through the reference's bisection, replayed step by step.
-template <int SPL>
+template <int SPL, int NW = 1>
 __device__ __forceinline__ void merge_path(const SearchParams &P, uint2 *bp, const uint2 *ms, bool fast_ok,
                                            int tbase) {
     const int lane = lane_id_opaque();
@@ -1010,7 +1062,7 @@ __device__ __forceinline__ void merge_path(const SearchParams &P, uint2 *bp, con
             }
     }
     // every lane has read its inputs before any output overwrites them
-    __syncthreads();
+    lead_sync<NW>();
 #pragma unroll
     for (int k = 0; k < SPL; ++k)
 #pragma unroll
@@ -1026,7 +1078,7 @@ __device__ __forceinline__ void merge_path(const SearchParams &P, uint2 *bp, con
 // empty (FLT_MAX, MAX_INDEX) pair (merge_path's condition for its split
 // search).
 // BIG: pbeam > 256 (the merge-path with two or more segments per lane).
-template <bool BIG>
+template <bool BIG, int NW = 1>
 __device__ __forceinline__ void merge_beam(const SearchParams &P, uint2 *bp, uint2 *ms, const float *cd,
                                            const uint32_t *ci, int span, bool &fast_ok, int &lb_out) {
     const int lane = lane_id_opaque();
@@ -1042,7 +1094,7 @@ __device__ __forceinline__ void merge_beam(const SearchParams &P, uint2 *bp, uin
     else if (short_ok && span <= 16) sort32<16>(ck, cv);
     else sort32(ck, cv);
     if (h == 0) ms[nl] = make_uint2(__float_as_uint(ck), cv);
-    __syncthreads();
+    lead_sync<NW>();
     if constexpr (!BIG) {
         if (pbeam == 128) {
             small_merge<2, false>(pbeam, bp, ms, 2 * lane, true);
@@ -1051,7 +1103,7 @@ __device__ __forceinline__ void merge_beam(const SearchParams &P, uint2 *bp, uin
         } else if (pbeam == 32) {
             small_merge<1, true>(pbeam, bp, ms, nl, h == 0);
         } else {
-            merge_path<1>(P, bp, ms, fast_ok, 0);  // one segment per lane: nothing to save
+            merge_path<1, NW>(P, bp, ms, fast_ok, 0);  // one segment per lane: nothing to save
         }
     } else {
         // Segments whose outputs lie wholly at or before position lb, the
@@ -1077,11 +1129,11 @@ __device__ __forceinline__ void merge_beam(const SearchParams &P, uint2 *bp, uin
         };
         if (tf < active && seg_end(tf + 1) <= lb) ++tf;
         const int spl = (active - tf + 63) / 64;
-        if (spl == 1) merge_path<1>(P, bp, ms, fast_ok, tf);
-        else if (spl == 2) merge_path<2>(P, bp, ms, fast_ok, tf);
-        else if (spl > 2) merge_path<4>(P, bp, ms, fast_ok, tf);
+        if (spl == 1) merge_path<1, NW>(P, bp, ms, fast_ok, tf);
+        else if (spl == 2) merge_path<2, NW>(P, bp, ms, fast_ok, tf);
+        else if (spl > 2) merge_path<4, NW>(P, bp, ms, fast_ok, tf);
     }
-    __syncthreads();
+    lead_sync<NW>();
 }
 
 // ------------------------------------------------------------ visited table
@@ -1431,18 +1483,20 @@ __device__ __forceinline__ void exact_pass(const SearchParams &P, const G &g, in
     }
 }
 
-// Exact distances for n children held in cd/ci at slots slot_list[0..n)
-// (or 0..n when slot_list is null): passes of 16 children, the last one
-// sized to what is left (DPL > 0: dims per lane known at compile time;
-// DPL == 0: generic geometry, exact_generic_pass).
+// Exact distances for children lo .. n-1 held in cd/ci at slots
+// slot_list[lo..n) (or lo..n when slot_list is null): passes of 16
+// children, the last one sized to what is left (DPL > 0: dims per lane known
+// at compile time; DPL == 0: generic geometry, exact_generic_pass).
+// exact_batch: all n (lo = 0).
 template <int DPL, class G>
-__device__ __forceinline__ void exact_batch(const SearchParams &P, const G &g, int n, const uint32_t *slot_list, float *cd,
-                            const uint32_t *ci, const float (&qr)[DPL > 0 ? DPL : 1], const float *qv) {
+__device__ __forceinline__ void exact_batch_range(const SearchParams &P, const G &g, int lo, int n,
+                                                  const uint32_t *slot_list, float *cd, const uint32_t *ci,
+                                                  const float (&qr)[DPL > 0 ? DPL : 1], const float *qv) {
     const int lane = lane_id();
     const int h = lane >> 5, nl = lane & 31;
     const bool ip = P.use_ip != 0;
     if constexpr (DPL > 0) {
-        int e0 = 0;
+        int e0 = lo;
         for (; n - e0 > 8; e0 += 16) exact_pass<8, DPL>(P, g, e0, n, slot_list, cd, ci, qr, ip);
         const int rem = n - e0;
         if (rem > 4) exact_pass<4, DPL>(P, g, e0, n, slot_list, cd, ci, qr, ip);
@@ -1451,11 +1505,17 @@ __device__ __forceinline__ void exact_batch(const SearchParams &P, const G &g, i
     } else {
         // six children per pass (three per half), 16 dimension steps per
         // load batch; the last pass sized to what is left
-        int e0 = 0;
+        int e0 = lo;
         for (; n - e0 > 4; e0 += 6) exact_generic_pass<3, 16>(P, g.row, g.dim, e0, n, slot_list, cd, ci, qv, ip);
         if (n - e0 > 2) exact_generic_pass<2, 16>(P, g.row, g.dim, e0, n, slot_list, cd, ci, qv, ip);
         else if (e0 < n) exact_generic_pass<1, 16>(P, g.row, g.dim, e0, n, slot_list, cd, ci, qv, ip);
     }
+}
+
+template <int DPL, class G>
+__device__ __forceinline__ void exact_batch(const SearchParams &P, const G &g, int n, const uint32_t *slot_list, float *cd,
+                                            const uint32_t *ci, const float (&qr)[DPL > 0 ? DPL : 1], const float *qv) {
+    exact_batch_range<DPL>(P, g, 0, n, slot_list, cd, ci, qr, qv);
 }
 
 // The keep_k smallest valid (value, lane) pairs of each 32-lane half, as
@@ -1561,12 +1621,22 @@ __device__ __forceinline__ void hash_contains_n(const uint32_t *t, uint32_t nb, 
 // it keeps in flight: at padded dimension 2048 its LDS (raw query, planes,
 // rotation scratch) holds it to 3 waves per SIMD anyway, and at 1024 a
 // 1,000-query launch fills one wave per SIMD.
-template <int WT, int DPL, int DIM_T, int DEG_T, bool COUNT, bool PROF, bool BIG>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 3 : 5))) void fg_search_kernel(SearchParams P) {
+// NW = 2: the team form (two waves per query; see TeamBlock).  Wave 0 leads:
+// it runs every phase, the helper wave joins it in stage II's rounds and the
+// exact distances; `lead_sync` orders the lead wave's own LDS accesses and
+// the workgroup barriers mark the meeting points.
+template <int WT, int DPL, int DIM_T, int DEG_T, bool COUNT, bool PROF, bool BIG, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 3 : 5))) void fg_search_kernel(SearchParams P) {
+    static_assert(NW == 1 || (NW == 2 && !PROF), "team form: two waves, no profiling build");
     extern __shared__ __align__(16) unsigned char smem[];
     const int qid = blockIdx.x;
     if (qid >= P.nq) return;
     const int lane = lane_id();
+    // wave index within the team (0 for the one-wave form)
+    const int wv = NW > 1 ? (__builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x)) >> 6) : 0;
+    const bool lead = NW == 1 || wv == 0;
+    TeamBlock *tb = reinterpret_cast<TeamBlock *>(smem + P.lds.team_off);
+    (void)tb;
     const int h = lane >> 5, nl = lane & 31;
     const Geo<DIM_T, DEG_T> g(P);
     const int B = g.B, W = B >> 5;
@@ -1604,10 +1674,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 3 
     }
 
     // ---- query preparation (the visited table's LDS holds the rotation)
-    float qlow, qhigh, qwidth;
-    int sum_q;
-    prepare_query(P.queries + static_cast<uint64_t>(qid) * g.dim, P.signs, g.dim, B, reinterpret_cast<float *>(H),
-                  WT == 0 ? nullptr : qv, planes, qlow, qhigh, qwidth, sum_q, nullptr);
+    float qlow = 0.0f, qhigh = 0.0f, qwidth = 0.0f;
+    int sum_q = 0;
+    if (lead)
+        prepare_query<NW>(P.queries + static_cast<uint64_t>(qid) * g.dim, P.signs, g.dim, B,
+                          reinterpret_cast<float *>(H), WT == 0 ? nullptr : qv, planes, qlow, qhigh, qwidth, sum_q,
+                          nullptr);
     // the generic geometry reads the query from global memory (it stays
     // cached), the others keep it in registers (qr below)
     const float *qsrc = WT == 0 ? P.queries + static_cast<uint64_t>(qid) * g.dim : qv;
@@ -1615,55 +1687,81 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 3 
     // whether any chunk of the quantized query wraps the reference's uint8
     // LUT entry (then the estimates subtract the wrapped chunks)
     bool any_wrap = false, any_zero = false;
-    if constexpr (WT > 0) {
-        uint32_t wor = 0, zor = 0;
+    if (lead) {
+        if constexpr (WT > 0) {
+            uint32_t wor = 0, zor = 0;
 #pragma unroll
-        for (int w = 0; w < WT; ++w) {
-            wor |= planes[kWrapPlane * WT + w];
-            zor |= planes[kZeroPlane * WT + w];
+            for (int w = 0; w < WT; ++w) {
+                wor |= planes[kWrapPlane * WT + w];
+                zor |= planes[kZeroPlane * WT + w];
+            }
+            any_wrap = uni(wor) != 0u;
+            any_zero = uni(zor) != 0u;
+        } else {
+            uint32_t wor = 0, zor = 0;
+            for (int w = lane; w < W; w += 64) {
+                wor |= planes[kWrapPlane * W + w];
+                zor |= planes[kZeroPlane * W + w];
+            }
+            any_wrap = any_lane(wor != 0u);
+            any_zero = any_lane(zor != 0u);
         }
-        any_wrap = uni(wor) != 0u;
-        any_zero = uni(zor) != 0u;
-    } else {
-        uint32_t wor = 0, zor = 0;
-        for (int w = lane; w < W; w += 64) {
-            wor |= planes[kWrapPlane * W + w];
-            zor |= planes[kZeroPlane * W + w];
-        }
-        any_wrap = any_lane(wor != 0u);
-        any_zero = any_lane(zor != 0u);
     }
     constexpr int DPLR = DPL > 0 ? DPL : 1;
     float qr[DPLR];
+    // (the helper wave reads the query from global memory: the LDS copy is
+    // overwritten once the lead wave initialises the candidate area)
+    const float *qraw = lead ? qv : P.queries + static_cast<uint64_t>(qid) * g.dim;
 #pragma unroll
     for (int k = 0; k < DPLR; ++k) {
         const int i = nl + 32 * k;
-        qr[k] = (DPL > 0 && i < g.dim) ? qv[i] : 0.0f;
+        qr[k] = (DPL > 0 && i < g.dim) ? qraw[i] : 0.0f;
     }
 
-    const float entry_d = uni(beam_key(half_distance(P.data + static_cast<uint64_t>(P.entry) * g.row, qsrc, g.dim,
-                                                     nl, P.use_ip != 0, true)));
-    // the query's LDS copy may share the candidate and staging area: every
-    // lane is done reading it before that area is initialised
-    __syncthreads();
-
-    // ---- state (adaptive_search.cuh:67-107)
-    hash_reset(H, nbk);
     const uint2 kEmpty = make_uint2(__float_as_uint(FLT_MAX), kMaxIndex);
     const uint2 kLowSentinel = make_uint2(__float_as_uint(-FLT_MAX), kMaxIndex);
-    for (int i = lane - 1; i < P.pbeam + static_cast<int>(kBeamPad); i += 64) bp[i] = i < 0 ? kLowSentinel : kEmpty;
-    if (lane <= kMsortHi + 1) ms[lane - 1] = lane == 0 ? kLowSentinel : kEmpty;
-    if (lane < 32) {
-        cd[lane] = FLT_MAX;
-        ci[lane] = kMaxIndex;
+    float entry_d = 0.0f;
+    if (lead) {
+        entry_d = uni(beam_key(half_distance(P.data + static_cast<uint64_t>(P.entry) * g.row, qsrc, g.dim, nl,
+                                             P.use_ip != 0, true)));
+        // the query's LDS copy may share the candidate and staging area: every
+        // lane is done reading it before that area is initialised
+        lead_sync<NW>();
+
+        // ---- state (adaptive_search.cuh:67-107)
+        hash_reset(H, nbk);
+        for (int i = lane - 1; i < P.pbeam + static_cast<int>(kBeamPad); i += 64) bp[i] = i < 0 ? kLowSentinel : kEmpty;
+        if (lane <= kMsortHi + 1) ms[lane - 1] = lane == 0 ? kLowSentinel : kEmpty;
+        if (lane < 32) {
+            cd[lane] = FLT_MAX;
+            ci[lane] = kMaxIndex;
+        }
+        lead_sync<NW>();
+        if (lane == 0) {
+            cd[0] = entry_d;
+            ci[0] = P.entry;
+            hash_insert(H, nbk, P.entry);
+        }
+        lead_sync<NW>();
     }
-    __syncthreads();
-    if (lane == 0) {
-        cd[0] = entry_d;
-        ci[0] = P.entry;
-        hash_insert(H, nbk, P.entry);
+    if constexpr (NW > 1) {
+        // the quantised query's constants, for the helper
+        if (lead && lane == 0) {
+            tb->sum_q = static_cast<uint32_t>(sum_q);
+            tb->qwidth_bits = __float_as_uint(qwidth);
+            tb->qlow_bits = __float_as_uint(qlow);
+            tb->any_wrap = any_wrap ? 1u : 0u;
+            tb->any_zero = any_zero ? 1u : 0u;
+        }
+        __syncthreads();
+        if (!lead) {
+            sum_q = static_cast<int>(uni(tb->sum_q));
+            qwidth = __uint_as_float(uni(tb->qwidth_bits));
+            qlow = __uint_as_float(uni(tb->qlow_bits));
+            any_wrap = uni(tb->any_wrap) != 0u;
+            any_zero = uni(tb->any_zero) != 0u;
+        }
     }
-    __syncthreads();
 
     Controller ctl{1, kPhase1Rho, 0, kMaxIndex, 0, false, entry_d, FLT_MAX, FLT_MAX};
     uint32_t c_iters = 0, c_exp = 0, c_ids = 0, c_est = 0, c_exact = 1, c_st2 = kMaxIndex;
@@ -1684,108 +1782,139 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 3 
         // lane-derived values are recomputed in each iteration, not held
         const int lane = lane_id_opaque();
         const int h = lane >> 5, nl = lane & 31;
-        if (((iter + 1) % kHashReset) == 0) {  // adaptive_search.cuh:128-134
-            hash_reset(H, nbk);
-            __syncthreads();
-            for (int i = lane; i < beam_sz; i += 64) hash_insert(H, nbk, bp[i].y & ~kMsb);
-            __syncthreads();
-        }
-        FG_PHASE(1);
-        // The merge runs before the iteration-limit test, so a search stopped
-        // by max_iter merges its last candidates here (the reference's final
-        // merge, adaptive_search.cuh:447-451).  A search that stops because no
-        // beam entry is left to expand has merged them already: its final
-        // merge sees an empty candidate buffer and leaves the beam as it is.
-        // A search that runs all kMaxIterations iterations (max_iter > 1024,
-        // i.e. beam >= 931) leaves the loop without passing here again and
-        // merges after it.
-        merge_beam<BIG>(P, bp, ms, cd, ci, cand_span, split_fast, lb_merge);
-        if constexpr (BIG) scan_from = min(scan_from, lb_merge);
-        FG_PHASE(2);
-        if (iter >= P.max_iter) break;
-        for (int i = beam_sz + lane; i < pbeam; i += 64) bp[i] = kEmpty;
-        cd[nl] = FLT_MAX;  // both halves store the same values: no branch
-        ci[nl] = kMaxIndex;
-        __syncthreads();
-        float kth = FLT_MAX;  // adaptive_search_utils.cuh:25-30
-        if (bp[beam_sz - 1].y != kMaxIndex) kth = __uint_as_float(bp[(P.K < beam_sz ? P.K : beam_sz) - 1].x);
-        kth = uni(kth);
-        controller_step(ctl, uni(bp[0].y), P.phase2_rho);
-        const int theta = ctl.spec;
-
-        // pick_expanders (utils.cuh:752-787): first theta unexpanded entries
-        // the picked entries' ids and distances go straight to the parent
-        // lists (an unexpanded entry's id has the top bit clear)
-        // Beams up to 256: lane l reads entry base + l (64 per step).  Larger
-        // beams, where the first unexpanded entry sits about halfway down: 256
-        // entries per step, from the first entry that can be unexpanded.
+        // the iteration's uniform state; the lead wave computes it, a helper
+        // wave receives it at the meeting point below
+        float kth = FLT_MAX, rho = 0.0f;
+        int theta = 1;
         uint32_t nexp = 0;
-        if constexpr (!BIG) {
-            for (int base = 0; base < beam_sz; base += 64) {
-                const int j = base + lane;
-                const uint2 e = bp[j < pbeam ? j : pbeam];  // unconditional read; bp[pbeam] is a sentinel
-                const bool fresh = j < beam_sz && (e.y & kMsb) == 0;
-                const uint64_t m = ballot(fresh);
-                if (fresh) {
-                    const uint32_t r = static_cast<uint32_t>(__popcll(m & ((1ull << lane) - 1ull))) + nexp;
-                    if (r < static_cast<uint32_t>(theta)) {
-                        pnode[r] = e.y;
-                        pdist[r] = __uint_as_float(e.x);
-                        bp[j].y = e.y | kMsb;
+        if (lead) {
+            if (((iter + 1) % kHashReset) == 0) {  // adaptive_search.cuh:128-134
+                hash_reset(H, nbk);
+                lead_sync<NW>();
+                for (int i = lane; i < beam_sz; i += 64) hash_insert(H, nbk, bp[i].y & ~kMsb);
+                lead_sync<NW>();
+            }
+            FG_PHASE(1);
+            // The merge runs before the iteration-limit test, so a search stopped
+            // by max_iter merges its last candidates here (the reference's final
+            // merge, adaptive_search.cuh:447-451).  A search that stops because no
+            // beam entry is left to expand has merged them already: its final
+            // merge sees an empty candidate buffer and leaves the beam as it is.
+            // A search that runs all kMaxIterations iterations (max_iter > 1024,
+            // i.e. beam >= 931) leaves the loop without passing here again and
+            // merges after it.
+            merge_beam<BIG, NW>(P, bp, ms, cd, ci, cand_span, split_fast, lb_merge);
+            if constexpr (BIG) scan_from = min(scan_from, lb_merge);
+            FG_PHASE(2);
+            if (iter >= P.max_iter) {
+                team_stop<NW>(tb, lane);
+                break;
+            }
+            for (int i = beam_sz + lane; i < pbeam; i += 64) bp[i] = kEmpty;
+            cd[nl] = FLT_MAX;  // both halves store the same values: no branch
+            ci[nl] = kMaxIndex;
+            lead_sync<NW>();
+            kth = FLT_MAX;  // adaptive_search_utils.cuh:25-30
+            if (bp[beam_sz - 1].y != kMaxIndex) kth = __uint_as_float(bp[(P.K < beam_sz ? P.K : beam_sz) - 1].x);
+            kth = uni(kth);
+            controller_step(ctl, uni(bp[0].y), P.phase2_rho);
+            theta = ctl.spec;
+            rho = ctl.rho;
+
+            // pick_expanders (utils.cuh:752-787): first theta unexpanded entries
+            // the picked entries' ids and distances go straight to the parent
+            // lists (an unexpanded entry's id has the top bit clear)
+            // Beams up to 256: lane l reads entry base + l (64 per step).  Larger
+            // beams, where the first unexpanded entry sits about halfway down: 256
+            // entries per step, from the first entry that can be unexpanded.
+            nexp = 0;
+            if constexpr (!BIG) {
+                for (int base = 0; base < beam_sz; base += 64) {
+                    const int j = base + lane;
+                    const uint2 e = bp[j < pbeam ? j : pbeam];  // unconditional read; bp[pbeam] is a sentinel
+                    const bool fresh = j < beam_sz && (e.y & kMsb) == 0;
+                    const uint64_t m = ballot(fresh);
+                    if (fresh) {
+                        const uint32_t r = static_cast<uint32_t>(__popcll(m & ((1ull << lane) - 1ull))) + nexp;
+                        if (r < static_cast<uint32_t>(theta)) {
+                            pnode[r] = e.y;
+                            pdist[r] = __uint_as_float(e.x);
+                            bp[j].y = e.y | kMsb;
+                        }
+                    }
+                    nexp += static_cast<uint32_t>(__popcll(m));
+                    if (nexp >= static_cast<uint32_t>(theta)) {
+                        nexp = static_cast<uint32_t>(theta);
+                        break;
                     }
                 }
-                nexp += static_cast<uint32_t>(__popcll(m));
+            } else {
+              int lastj = -1;  // the entry that took rank theta - 1
+              for (int base = scan_from; base < beam_sz; base += 256) {
+                // entry base + 64 k + l on lane l (each read covers 64
+                // consecutive entries); index order is k, then lane
+                uint2 e[4];
+                uint64_t m[4];
+    #pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int j = base + 64 * k + lane;
+                    e[k] = bp[j < pbeam ? j : pbeam];  // unconditional read; bp[pbeam] is a sentinel
+                    m[k] = ballot(j < beam_sz && (e[k].y & kMsb) == 0);
+                }
+                const uint64_t lt = (1ull << lane) - 1ull;
+                uint32_t before = nexp;
+    #pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    if (lane_in(m[k])) {
+                        const uint32_t r = before + static_cast<uint32_t>(__popcll(m[k] & lt));
+                        if (r < static_cast<uint32_t>(theta)) {
+                            const int j = base + 64 * k + lane;
+                            pnode[r] = e[k].y;
+                            pdist[r] = __uint_as_float(e[k].x);
+                            bp[j].y = e[k].y | kMsb;
+                            if (r + 1 == static_cast<uint32_t>(theta)) lastj = j;
+                        }
+                    }
+                    before += static_cast<uint32_t>(__popcll(m[k]));
+                }
+                nexp = before;
                 if (nexp >= static_cast<uint32_t>(theta)) {
                     nexp = static_cast<uint32_t>(theta);
                     break;
                 }
+              }
+              // entries up to the last one picked are now all expanded
+              const uint64_t bl = ballot(lastj >= 0);
+              scan_from = bl ? __builtin_amdgcn_readlane(lastj, __builtin_ctzll(bl)) + 1 : beam_sz;
             }
-        } else {
-          int lastj = -1;  // the entry that took rank theta - 1
-          for (int base = scan_from; base < beam_sz; base += 256) {
-            // entry base + 64 k + l on lane l (each read covers 64
-            // consecutive entries); index order is k, then lane
-            uint2 e[4];
-            uint64_t m[4];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int j = base + 64 * k + lane;
-                e[k] = bp[j < pbeam ? j : pbeam];  // unconditional read; bp[pbeam] is a sentinel
-                m[k] = ballot(j < beam_sz && (e[k].y & kMsb) == 0);
-            }
-            const uint64_t lt = (1ull << lane) - 1ull;
-            uint32_t before = nexp;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                if (lane_in(m[k])) {
-                    const uint32_t r = before + static_cast<uint32_t>(__popcll(m[k] & lt));
-                    if (r < static_cast<uint32_t>(theta)) {
-                        const int j = base + 64 * k + lane;
-                        pnode[r] = e[k].y;
-                        pdist[r] = __uint_as_float(e[k].x);
-                        bp[j].y = e[k].y | kMsb;
-                        if (r + 1 == static_cast<uint32_t>(theta)) lastj = j;
-                    }
-                }
-                before += static_cast<uint32_t>(__popcll(m[k]));
-            }
-            nexp = before;
-            if (nexp >= static_cast<uint32_t>(theta)) {
-                nexp = static_cast<uint32_t>(theta);
+            lead_sync<NW>();
+            if (nexp == 0) {
+                team_stop<NW>(tb, lane);
                 break;
             }
-          }
-          // entries up to the last one picked are now all expanded
-          const uint64_t bl = ballot(lastj >= 0);
-          scan_from = bl ? __builtin_amdgcn_readlane(lastj, __builtin_ctzll(bl)) + 1 : beam_sz;
+            FG_COUNT(c_iters++);
+            FG_COUNT(c_exp += nexp);
+            // adaptive_search_utils.cuh:41-49
+            ctl.last_e = finite_below_max(ctl.cur_e) ? ctl.cur_e : ctl.entry_d;
+            ctl.cur_e = uni(pdist[nexp - 1]);
         }
-        __syncthreads();
-        if (nexp == 0) break;
-        FG_COUNT(c_iters++);
-        FG_COUNT(c_exp += nexp);
-        // adaptive_search_utils.cuh:41-49
-        ctl.last_e = finite_below_max(ctl.cur_e) ? ctl.cur_e : ctl.entry_d;
-        ctl.cur_e = uni(pdist[nexp - 1]);
+        if constexpr (NW > 1) {
+            if (lead && lane == 0) {
+                tb->stop = 0u;
+                tb->theta = static_cast<uint32_t>(theta);
+                tb->nexp = nexp;
+                tb->kth_bits = __float_as_uint(kth);
+                tb->rho_bits = __float_as_uint(rho);
+            }
+            __syncthreads();
+            if (!lead) {
+                if (uni(tb->stop) != 0u) break;
+                theta = static_cast<int>(uni(tb->theta));
+                nexp = uni(tb->nexp);
+                kth = __uint_as_float(uni(tb->kth_bits));
+                rho = __uint_as_float(uni(tb->rho_bits));
+            }
+        }
         const bool kth_valid = finite_below_max(kth);
         FG_PHASE(3);
 
@@ -1793,94 +1922,97 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 3 
         int ex_n = 0;
         const uint32_t *ex_list = nullptr;
         if (theta <= 1) {
-            // ---------------- single expander (adaptive_search.cuh:221-343)
-            const int cwc = deg < cbs ? deg : cbs;
-            const uint32_t parent = uni(pnode[0]);
-            const float pd0 = uni(pdist[0]);
-            const float *prow = data + static_cast<uint64_t>(parent) * g.row;
-            const uint32_t *nbrs = reinterpret_cast<const uint32_t *>(prow + g.nbr);
-            FG_COUNT(c_ids += static_cast<uint32_t>(cwc));
-            // id, factors and code issued together (one HBM round trip);
-            // unconditional loads, lanes past cwc read the last slot
-            const int nsafe = nl < cwc ? nl : cwc - 1;
-            const float *factors = prow + g.factor;
-            uint32_t ck[1] = {nbrs[nsafe]};
-            const float tx = factors[nsafe];
-            const float fdq = factors[deg + nsafe];
-            const float fvq = factors[2 * deg + nsafe];
-            uint32_t c1[1][WTR];
-            if constexpr (WT > 0)
-                load_code<WT>(reinterpret_cast<const uint32_t *>(prow + g.code) + static_cast<uint64_t>(nsafe) * WT,
-                              vec_ok, c1[0]);
-            bool fresh[1] = {nl < cwc && ck[0] < P.npoints};
-            hash_contains_n<1>(H, nbk, ck, fresh);
-            uint32_t child = fresh[0] ? ck[0] : kMaxIndex;
-            const uint32_t vmask = half_bits(ballot(child != kMaxIndex), 0);
-            const int valid_count = __popc(vmask);
-            const int keep = keep_count_for_expander(static_cast<uint32_t>(cwc), 1, ctl.rho, false, 0);
-            const bool keep_all = keep >= valid_count;
-            float dist = child == kMaxIndex ? FLT_MAX : 0.0f;
-            uint32_t admit_mask;
-            if (!keep_all) {
-                FG_COUNT(c_est += static_cast<uint32_t>(valid_count));
-                const uint32_t *codes = reinterpret_cast<const uint32_t *>(prow + g.code);
-                const bool valid = child != kMaxIndex;
-                float est = FLT_MAX;
-                int32_t r1[1] = {0};
-                if constexpr (WT > 0) {
-                    // computed on every lane, selected for the valid ones
-                    raw_batch<1, WT>(c1, planes, any_wrap, any_zero, r1);
-                    est = tx == FLT_MAX ? 0.0f : estimate_formula(r1[0], sum_q, qwidth, qlow, tx, fdq, fvq, pd0);
-                } else if (valid) {
-                    const int32_t raw = raw_words(codes + static_cast<uint64_t>(nsafe) * W, planes, W, vec_ok, any_wrap, any_zero);
-                    est = tx == FLT_MAX ? 0.0f : estimate_formula(raw, sum_q, qwidth, qlow, tx, fdq, fvq, pd0);
+          // (the lead wave's alone; a helper waits for the exact batch)
+          if (lead) {
+                // ---------------- single expander (adaptive_search.cuh:221-343)
+                const int cwc = deg < cbs ? deg : cbs;
+                const uint32_t parent = uni(pnode[0]);
+                const float pd0 = uni(pdist[0]);
+                const float *prow = data + static_cast<uint64_t>(parent) * g.row;
+                const uint32_t *nbrs = reinterpret_cast<const uint32_t *>(prow + g.nbr);
+                FG_COUNT(c_ids += static_cast<uint32_t>(cwc));
+                // id, factors and code issued together (one HBM round trip);
+                // unconditional loads, lanes past cwc read the last slot
+                const int nsafe = nl < cwc ? nl : cwc - 1;
+                const float *factors = prow + g.factor;
+                uint32_t ck[1] = {nbrs[nsafe]};
+                const float tx = factors[nsafe];
+                const float fdq = factors[deg + nsafe];
+                const float fvq = factors[2 * deg + nsafe];
+                uint32_t c1[1][WTR];
+                if constexpr (WT > 0)
+                    load_code<WT>(reinterpret_cast<const uint32_t *>(prow + g.code) + static_cast<uint64_t>(nsafe) * WT,
+                                  vec_ok, c1[0]);
+                bool fresh[1] = {nl < cwc && ck[0] < P.npoints};
+                hash_contains_n<1>(H, nbk, ck, fresh);
+                uint32_t child = fresh[0] ? ck[0] : kMaxIndex;
+                const uint32_t vmask = half_bits(ballot(child != kMaxIndex), 0);
+                const int valid_count = __popc(vmask);
+                const int keep = keep_count_for_expander(static_cast<uint32_t>(cwc), 1, ctl.rho, false, 0);
+                const bool keep_all = keep >= valid_count;
+                float dist = child == kMaxIndex ? FLT_MAX : 0.0f;
+                uint32_t admit_mask;
+                if (!keep_all) {
+                    FG_COUNT(c_est += static_cast<uint32_t>(valid_count));
+                    const uint32_t *codes = reinterpret_cast<const uint32_t *>(prow + g.code);
+                    const bool valid = child != kMaxIndex;
+                    float est = FLT_MAX;
+                    int32_t r1[1] = {0};
+                    if constexpr (WT > 0) {
+                        // computed on every lane, selected for the valid ones
+                        raw_batch<1, WT>(c1, planes, any_wrap, any_zero, r1);
+                        est = tx == FLT_MAX ? 0.0f : estimate_formula(r1[0], sum_q, qwidth, qlow, tx, fdq, fvq, pd0);
+                    } else if (valid) {
+                        const int32_t raw = raw_words(codes + static_cast<uint64_t>(nsafe) * W, planes, W, vec_ok, any_wrap, any_zero);
+                        est = tx == FLT_MAX ? 0.0f : estimate_formula(raw, sum_q, qwidth, qlow, tx, fdq, fvq, pd0);
+                    }
+                    const bool fin = isfinite(est);
+                    child = (valid && !fin) ? kMaxIndex : child;
+                    dist = valid ? (fin ? est : FLT_MAX) : dist;
+                    uint32_t near = 0;
+                    if (kth_valid)
+                        near = __popc(half_bits(ballot(child != kMaxIndex && isfinite(dist) && dist <= kth), 0));
+                    const int eff = keep_count_for_expander(static_cast<uint32_t>(cwc), 1, ctl.rho, kth_valid, near);
+                    // dispatch_candidate_bitonic_sort over the cbs-entry buffer (padding beyond it)
+                    float sk = nl < cbs ? dist : FLT_MAX;
+                    uint32_t sv = nl < cbs ? child : kMaxIndex;
+                    sort32(sk, sv);
+                    dist = sk;
+                    child = sv;
+                    if (nl >= eff) {
+                        child = kMaxIndex;
+                        dist = FLT_MAX;
+                    }
+                    admit_mask = eff >= 32 ? 0xFFFFFFFFu : ((1u << eff) - 1u);
+                } else {
+                    admit_mask = cwc >= 32 ? 0xFFFFFFFFu : ((1u << cwc) - 1u);
                 }
-                const bool fin = isfinite(est);
-                child = (valid && !fin) ? kMaxIndex : child;
-                dist = valid ? (fin ? est : FLT_MAX) : dist;
-                uint32_t near = 0;
-                if (kth_valid)
-                    near = __popc(half_bits(ballot(child != kMaxIndex && isfinite(dist) && dist <= kth), 0));
-                const int eff = keep_count_for_expander(static_cast<uint32_t>(cwc), 1, ctl.rho, kth_valid, near);
-                // dispatch_candidate_bitonic_sort over the cbs-entry buffer (padding beyond it)
-                float sk = nl < cbs ? dist : FLT_MAX;
-                uint32_t sv = nl < cbs ? child : kMaxIndex;
-                sort32(sk, sv);
-                dist = sk;
-                child = sv;
-                if (nl >= eff) {
-                    child = kMaxIndex;
-                    dist = FLT_MAX;
+                // admit in slot order: insert, drop repeats (lowest slot wins)
+                const bool want = ((admit_mask >> nl) & 1u) && child != kMaxIndex && dist < FLT_MAX;
+                const uint32_t want_mask = half_bits(ballot(want), 0);
+                bool ins = want;
+                if (!P.dup_free) ins = want && !dup_of_earlier(child, want_mask, nl, 0);
+                if (h == 0 && ins) hash_insert(H, nbk, child);
+                if (!ins) {
+                    if ((admit_mask >> nl) & 1u) {
+                        child = kMaxIndex;
+                        dist = FLT_MAX;
+                    }
                 }
-                admit_mask = eff >= 32 ? 0xFFFFFFFFu : ((1u << eff) - 1u);
-            } else {
-                admit_mask = cwc >= 32 ? 0xFFFFFFFFu : ((1u << cwc) - 1u);
-            }
-            // admit in slot order: insert, drop repeats (lowest slot wins)
-            const bool want = ((admit_mask >> nl) & 1u) && child != kMaxIndex && dist < FLT_MAX;
-            const uint32_t want_mask = half_bits(ballot(want), 0);
-            bool ins = want;
-            if (!P.dup_free) ins = want && !dup_of_earlier(child, want_mask, nl, 0);
-            if (h == 0 && ins) hash_insert(H, nbk, child);
-            if (!ins) {
-                if ((admit_mask >> nl) & 1u) {
-                    child = kMaxIndex;
-                    dist = FLT_MAX;
+                const uint32_t ins_mask = half_bits(ballot(ins), 0);
+                if (h == 0) {
+                    cd[nl] = dist;
+                    ci[nl] = child;
+                    if (ins) alist[__popc(ins_mask & ((1u << nl) - 1u))] = static_cast<uint32_t>(nl);
                 }
-            }
-            const uint32_t ins_mask = half_bits(ballot(ins), 0);
-            if (h == 0) {
-                cd[nl] = dist;
-                ci[nl] = child;
-                if (ins) alist[__popc(ins_mask & ((1u << nl) - 1u))] = static_cast<uint32_t>(nl);
-            }
-            __syncthreads();
-            const int nins = __popc(ins_mask);
-            FG_COUNT(c_exact += static_cast<uint32_t>(nins));
-            ex_n = nins;
-            ex_list = alist;
-            cand_span = 32;  // single-expander children sit at their lane's slot
-            FG_PHASE(4);
+                lead_sync<NW>();
+                const int nins = __popc(ins_mask);
+                FG_COUNT(c_exact += static_cast<uint32_t>(nins));
+                ex_n = nins;
+                ex_list = alist;
+                cand_span = 32;  // single-expander children sit at their lane's slot
+                FG_PHASE(4);
+          }
         } else {
             // ---------------- speculative expansion (adaptive_search.cuh:344-444)
             FG_COUNT(if (c_st2 == kMaxIndex) c_st2 = static_cast<uint32_t>(iter));
@@ -1890,8 +2022,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 3 
             // partial one (utils uniform over the iteration)
             const int an_full = deg < 32 ? deg : 32;
             const int an_last = deg - (tiles - 1) * 32;
-            const int lim_full = uni(keep_limit(static_cast<uint32_t>(an_full), theta, ctl.rho));
-            const int lim_last = an_last == an_full ? lim_full : uni(keep_limit(static_cast<uint32_t>(an_last), theta, ctl.rho));
+            const int lim_full = uni(keep_limit(static_cast<uint32_t>(an_full), theta, rho));
+            const int lim_last = an_last == an_full ? lim_full : uni(keep_limit(static_cast<uint32_t>(an_last), theta, rho));
             uint32_t compact = 0;
             // A task (one 32-neighbour tile of one parent: one reference warp)
             // takes G lanes: a 32-lane half, or for degree 16 a 16-lane row, so
@@ -1901,24 +2033,28 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 3 
             const int grp = lane / G, nlg = lane % G;
             for (int rbase = 0; rbase < tasks; rbase += kSearchWidth) {
                 constexpr int SR = kSearchWidth / TPW;  // sub-rounds of TPW tasks
-                uint32_t cid[SR];
-                bool val[SR];
-                int an[SR], tsk[SR], pix[SR];
-                const float *prw[SR];
-                uint32_t rof[SR];  // fixed geometry: the parents' row byte offsets
-                float tx[SR], fdq[SR], fvq[SR];
-                uint32_t code[SR][WTR];
+                // this wave's sub-rounds: all of them, or in the team form
+                // the first half (lead) or the second (helper)
+                constexpr int SRN = SR / NW;
+                const int sr0 = wv * SRN;
+                uint32_t cid[SRN];
+                bool val[SRN];
+                int an[SRN], tsk[SRN], pix[SRN];
+                const float *prw[SRN];
+                uint32_t rof[SRN];  // fixed geometry: the parents' row byte offsets
+                float tx[SRN], fdq[SRN], fvq[SRN];
+                uint32_t code[SRN][WTR];
                 // (a) neighbour ids of the round's 8 tasks, then their factors and
                 // codes: all loads issued together (one HBM round trip), ids first
                 // so the visited test can start when they arrive.  Loads are
                 // unconditional (an inactive lane reads a valid slot of parent 0
                 // or of its own parent's last neighbour); inactive lanes' ids are
                 // replaced after.
-                bool lact[SR];
-                int nsafe[SR];
+                bool lact[SRN];
+                int nsafe[SRN];
 #pragma unroll
-                for (int sr = 0; sr < SR; ++sr) {
-                    const int task = rbase + TPW * sr + grp;
+                for (int sr = 0; sr < SRN; ++sr) {
+                    const int task = rbase + TPW * (sr0 + sr) + grp;
                     const bool tact = task < tasks;
                     const int pidx = tact ? task / tiles : 0;
                     const int tile = tact ? task - pidx * tiles : 0;
@@ -1939,7 +2075,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 3 
                     FG_COUNT(c_ids += static_cast<uint32_t>(__popcll(ballot(lact[sr]))));
                 }
 #pragma unroll
-                for (int sr = 0; sr < SR; ++sr) {
+                for (int sr = 0; sr < SRN; ++sr) {
                     if constexpr (kFixedGeo) {
                         using GF = Geo<DIM_T, DEG_T>;
                         const uint32_t fo = rof[sr] + GF::kFactorB + 4u * nsafe[sr];
@@ -1970,20 +2106,20 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 3 
                     }
                 }
 #pragma unroll
-                for (int sr = 0; sr < SR; ++sr)
+                for (int sr = 0; sr < SRN; ++sr)
                     if (!lact[sr]) cid[sr] = kMaxIndex;
                 // (b) visited test against the table as it stood at the round's start
 #pragma unroll
-                for (int sr = 0; sr < SR; ++sr) val[sr] = cid[sr] != kMaxIndex && cid[sr] < P.npoints;
-                hash_contains_n<SR>(H, nbk, cid, val);
+                for (int sr = 0; sr < SRN; ++sr) val[sr] = cid[sr] != kMaxIndex && cid[sr] < P.npoints;
+                hash_contains_n<SRN>(H, nbk, cid, val);
                 // (c) which tasks need estimates.  Lane predicates from here on
                 // are masks taken straight from compares.  A task without
                 // children has no valid lane, so it never needs estimates and
                 // its keep limit is never read.
-                uint64_t valm[SR], needm[SR];
-                int keep[SR];
+                uint64_t valm[SRN], needm[SRN];
+                int keep[SRN];
 #pragma unroll
-                for (int sr = 0; sr < SR; ++sr) {
+                for (int sr = 0; sr < SRN; ++sr) {
                     valm[sr] = ballot(val[sr]);
                     const int rvc = static_cast<int>(group_popc<G>(valm[sr]));
                     keep[sr] = an[sr] == an_full ? lim_full : lim_last;
@@ -1992,11 +2128,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 3 
                 }
                 FG_PHASE(6);
                 // (d) estimates, kth-near counts, keep decisions
-                uint64_t klm[SR];
-                int32_t rawb[SR];
-                if constexpr (WT > 0) raw_batch<SR, WT>(code, planes, any_wrap, any_zero, rawb);
+                uint64_t klm[SRN];
+                int32_t rawb[SRN];
+                if constexpr (WT > 0) raw_batch<SRN, WT>(code, planes, any_wrap, any_zero, rawb);
 #pragma unroll
-                for (int sr = 0; sr < SR; ++sr) {
+                for (int sr = 0; sr < SRN; ++sr) {
                     float est = FLT_MAX;
                     const uint64_t scored = needm[sr] & valm[sr];
                     if constexpr (WT > 0) {
@@ -2044,61 +2180,125 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 3 
                     }
                     klm[sr] = kl;
                 }
-                // (e) kept children listed in (task, lane) order
-                uint32_t total = 0;
+                // the kept lanes of all sub-rounds; in the team form the
+                // helper's half reaches the lead wave through LDS
+                uint64_t klmA[SR];
+                uint32_t cidA[SR];
 #pragma unroll
-                for (int sr = 0; sr < SR; ++sr) {
-                    // the sub-round's TPW tasks sit in lane order and follow
-                    // each other in the list: a kept lane's place is the running
-                    // total plus its rank among the kept lanes of the wave
-                    if (lane_in(klm[sr])) {
-                        const uint32_t e = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(klm[sr] >> 32),
-                                                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(klm[sr]), total));
-                        if (e < 32) alist[e] = cid[sr];
+                for (int sr = 0; sr < SRN; ++sr) {
+                    klmA[sr] = klm[sr];
+                    cidA[sr] = cid[sr];
+                }
+                if constexpr (NW > 1) {
+                    if (!lead) {
+#pragma unroll
+                        for (int sr = 0; sr < SRN; ++sr) {
+                            if (lane == 0) tb->klm[sr] = klm[sr];
+                            tb->cid[sr][lane] = cid[sr];
+                        }
                     }
-                    total += static_cast<uint32_t>(__popcll(klm[sr]));
+                    __syncthreads();
+                    if (lead) {
+#pragma unroll
+                        for (int sr = 0; sr < SRN; ++sr) {
+                            const uint64_t m = tb->klm[sr];
+                            klmA[SRN + sr] = (static_cast<uint64_t>(uni(static_cast<uint32_t>(m >> 32))) << 32) |
+                                             uni(static_cast<uint32_t>(m));
+                            cidA[SRN + sr] = tb->cid[sr][lane];
+                        }
+                    }
                 }
-                __syncthreads();
-                if (total > 32) total = 32;  // <= 4 kept per task at theta = 8
-                // (f) insert in list order; a repeat of an earlier entry is dropped
-                const bool mine = lane < static_cast<int>(total);
-                const uint32_t key = mine ? alist[lane] : kMaxIndex;
-                const uint32_t got = mine ? hash_insert(H, nbk, key) : 0u;
-                // Every listed child was absent from the table when this
-                // round's visited tests ran, so an insert that finds its key
-                // present met a repeat within the list, added by another lane
-                // of this batch: of each such group the earliest lane is kept.
-                bool acc = got != 0u;
-                uint64_t lost = ballot(mine && !got);
-                while (lost != 0ull) {
-                    const uint32_t kr = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(key), __builtin_ctzll(lost)));
-                    const uint64_t same = ballot(mine && key == kr);
-                    acc = lane_in(same) ? (lane == __builtin_ctzll(same)) : acc;
-                    lost &= ~same;
+                if (lead) {
+                    // (e) kept children listed in (task, lane) order
+                    uint32_t total = 0;
+    #pragma unroll
+                    for (int sr = 0; sr < SR; ++sr) {
+                        // the sub-round's TPW tasks sit in lane order and follow
+                        // each other in the list: a kept lane's place is the running
+                        // total plus its rank among the kept lanes of the wave
+                        if (lane_in(klmA[sr])) {
+                            const uint32_t e = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(klmA[sr] >> 32),
+                                                                         __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(klmA[sr]), total));
+                            if (e < 32) alist[e] = cidA[sr];
+                        }
+                        total += static_cast<uint32_t>(__popcll(klmA[sr]));
+                    }
+                    lead_sync<NW>();
+                    if (total > 32) total = 32;  // <= 4 kept per task at theta = 8
+                    // (f) insert in list order; a repeat of an earlier entry is dropped
+                    const bool mine = lane < static_cast<int>(total);
+                    const uint32_t key = mine ? alist[lane] : kMaxIndex;
+                    const uint32_t got = mine ? hash_insert(H, nbk, key) : 0u;
+                    // Every listed child was absent from the table when this
+                    // round's visited tests ran, so an insert that finds its key
+                    // present met a repeat within the list, added by another lane
+                    // of this batch: of each such group the earliest lane is kept.
+                    bool acc = got != 0u;
+                    uint64_t lost = ballot(mine && !got);
+                    while (lost != 0ull) {
+                        const uint32_t kr = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(key), __builtin_ctzll(lost)));
+                        const uint64_t same = ballot(mine && key == kr);
+                        acc = lane_in(same) ? (lane == __builtin_ctzll(same)) : acc;
+                        lost &= ~same;
+                    }
+                    const uint32_t accm = half_bits(ballot(acc), 0);
+                    if (acc) {
+                        // (cd was reset at the iteration's start; the exact pass fills it)
+                        const uint32_t slot = __builtin_amdgcn_mbcnt_lo(accm, compact);
+                        if (slot < static_cast<uint32_t>(P.collect_cap)) ci[slot] = key;
+                    }
+                    compact += static_cast<uint32_t>(__popc(accm));
+                    lead_sync<NW>();
                 }
-                const uint32_t accm = half_bits(ballot(acc), 0);
-                if (acc) {
-                    // (cd was reset at the iteration's start; the exact pass fills it)
-                    const uint32_t slot = __builtin_amdgcn_mbcnt_lo(accm, compact);
-                    if (slot < static_cast<uint32_t>(P.collect_cap)) ci[slot] = key;
+                // in the team form the round's inserts are in the table before
+                // the helper's visited tests of the next round
+                if constexpr (NW > 1) {
+                    if (rbase + kSearchWidth < tasks) __syncthreads();
                 }
-                compact += static_cast<uint32_t>(__popc(accm));
-                __syncthreads();
             }
-            if (compact > static_cast<uint32_t>(P.collect_cap)) compact = static_cast<uint32_t>(P.collect_cap);
-            FG_COUNT(c_exact += compact);
-            ex_n = static_cast<int>(compact);
-            cand_span = ex_n;  // compacted into slots 0 .. compact - 1
+            if (lead) {
+                if (compact > static_cast<uint32_t>(P.collect_cap)) compact = static_cast<uint32_t>(P.collect_cap);
+                FG_COUNT(c_exact += compact);
+                ex_n = static_cast<int>(compact);
+                cand_span = ex_n;  // compacted into slots 0 .. compact - 1
+            }
             FG_PHASE(7);
         }
-        exact_batch<DPL>(P, g, ex_n, ex_list, cd, ci, qr, qsrc);
+        if constexpr (NW == 1) {
+            exact_batch<DPL>(P, g, ex_n, ex_list, cd, ci, qr, qsrc);
+        } else {
+            // the exact batch in two halves, one per wave
+            if (lead && lane == 0) {
+                tb->ex_n = static_cast<uint32_t>(ex_n);
+                tb->ex_alist = ex_list != nullptr ? 1u : 0u;
+            }
+            __syncthreads();
+            const int n_all = static_cast<int>(uni(tb->ex_n));
+            const uint32_t *lst = uni(tb->ex_alist) != 0u ? alist : nullptr;
+            const int mid = (n_all + 1) >> 1;
+            exact_batch_range<DPL>(P, g, lead ? 0 : mid, lead ? mid : n_all, lst, cd, ci, qr, qsrc);
+            __syncthreads();
+        }
         if (theta <= 1) FG_PHASE(5);
         else FG_PHASE(8);
+        lead_sync<NW>();
+    }
+    if constexpr (NW > 1) {
+        // the helper's work counters; from here on the lead wave is alone
+        if (!lead && lane == 0) {
+            tb->c_ids = c_ids;
+            tb->c_est = c_est;
+        }
         __syncthreads();
+        if (!lead) return;
+        if constexpr (COUNT) {
+            c_ids += uni(tb->c_ids);
+            c_est += uni(tb->c_est);
+        }
     }
     // the loop ran out at kMaxIterations: the last iteration's exact-scored
     // candidates are still in the buffer (adaptive_search.cuh:449-451)
-    if (iter == kMaxIterations) merge_beam<BIG>(P, bp, ms, cd, ci, cand_span, split_fast, lb_merge);
+    if (iter == kMaxIterations) merge_beam<BIG, NW>(P, bp, ms, cd, ci, cand_span, split_fast, lb_merge);
 
     FG_PHASE(3);
     // result writer (adaptive_search.cuh:455-464)
@@ -2428,20 +2628,51 @@ int make_params(fg_index *ix, uint32_t nq, uint32_t K, uint32_t beam, SearchPara
     P.entry = ix->entry;
     P.nq = static_cast<int>(nq);
     P.lds = lds_layout(ix->dim, ix->padded_dim, static_cast<uint32_t>(P.pbeam), static_cast<uint32_t>(P.buckets));
+    P.team = P.lds.total_team <= 65536u ? 1 : 0;
     return FG_OK;
+}
+
+// Whether a launch runs the team form: when the batch is too small to fill
+// the device with one wave per query (twice the queries fit in the
+// one-wave form's resident workgroups), a second wave per query costs no
+// query a slot and shortens every search.  FLASHGANN_TEAM=0 / 1 forces the
+// one-wave / team form (tests run both).
+inline bool use_team(const SearchParams &P, const void *one_wave_kernel) {
+    if (!P.team) return false;
+    if (const char *e = std::getenv("FLASHGANN_TEAM")) {
+        if (e[0] == '0') return false;
+        if (e[0] == '1') return true;
+    }
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return false;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return false;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, one_wave_kernel, 64, P.lds.total) != hipSuccess)
+        return false;
+    return 2ll * P.nq <= static_cast<long long>(per_cu) * cus;
 }
 
 template <int WT, int DPL, int DIM_T, int DEG_T, bool BIG>
 void launch_geo_b(const SearchParams &P, hipStream_t stream, bool count, bool prof) {
     const dim3 grid(P.nq), block(64);
+    if (!prof && use_team(P, reinterpret_cast<const void *>(
+                                 &fg_search_kernel<WT, DPL, DIM_T, DEG_T, false, false, BIG, 1>))) {
+        const dim3 team_block(128);
+        if (count)
+            hipLaunchKernelGGL((fg_search_kernel<WT, DPL, DIM_T, DEG_T, true, false, BIG, 2>), grid, team_block,
+                               P.lds.total_team, stream, P);
+        else
+            hipLaunchKernelGGL((fg_search_kernel<WT, DPL, DIM_T, DEG_T, false, false, BIG, 2>), grid, team_block,
+                               P.lds.total_team, stream, P);
+        return;
+    }
     if (prof)
-        hipLaunchKernelGGL((fg_search_kernel<WT, DPL, DIM_T, DEG_T, false, true, BIG>), grid, block,
+        hipLaunchKernelGGL((fg_search_kernel<WT, DPL, DIM_T, DEG_T, false, true, BIG, 1>), grid, block,
                            P.lds.total_prof, stream, P);
     else if (count)
-        hipLaunchKernelGGL((fg_search_kernel<WT, DPL, DIM_T, DEG_T, true, false, BIG>), grid, block, P.lds.total,
+        hipLaunchKernelGGL((fg_search_kernel<WT, DPL, DIM_T, DEG_T, true, false, BIG, 1>), grid, block, P.lds.total,
                            stream, P);
     else
-        hipLaunchKernelGGL((fg_search_kernel<WT, DPL, DIM_T, DEG_T, false, false, BIG>), grid, block, P.lds.total,
+        hipLaunchKernelGGL((fg_search_kernel<WT, DPL, DIM_T, DEG_T, false, false, BIG, 1>), grid, block, P.lds.total,
                            stream, P);
 }
 

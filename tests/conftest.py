@@ -38,6 +38,15 @@ def small_index(n=3000, nq=24, dim=128, comps=16, degree=32, kind="int", use_ip=
     return cb, q, base
 
 
+@pytest.fixture(params=["one-wave", "team"])
+def search_form(request, monkeypatch):
+    """Runs a GPU test once with each form of the search kernel: one wave
+    per query, and the team form (two waves per query) that small launches
+    use.  FLASHGANN_TEAM is read at every launch."""
+    monkeypatch.setenv("FLASHGANN_TEAM", "0" if request.param == "one-wave" else "1")
+    return request.param
+
+
 @pytest.fixture(scope="session")
 def gpu_available():
     import torch

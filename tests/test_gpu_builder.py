@@ -5,7 +5,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("search_form")]
 
 
 def test_gpu_codebook_equals_cpu_codebook_on_integer_data(gpu_available):

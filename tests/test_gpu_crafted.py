@@ -8,7 +8,7 @@ import pytest
 
 import crafted
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("search_form")]
 
 
 def _both(cb, q, K, beam):

@@ -10,7 +10,7 @@ import pytest
 
 from conftest import small_index
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("search_form")]
 
 
 def _run(cb, q, K, beam, metric=0, entry=None):

@@ -9,7 +9,7 @@ import pytest
 
 from conftest import small_index
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("search_form")]
 
 
 STAGE_CASES = [("int", 128, 1500), ("unit", 96, 1500), ("box", 960, 1500), ("aniso", 1536, 1200)]

@@ -10,7 +10,7 @@ import pytest
 
 from conftest import small_index
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("search_form")]
 
 
 def test_noalloc_equals_fg_search(gpu_available):
