@@ -1855,7 +1855,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
                 // consecutive entries); index order is k, then lane
                 uint2 e[4];
                 uint64_t m[4];
-    #pragma unroll
+#pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     const int j = base + 64 * k + lane;
                     e[k] = bp[j < pbeam ? j : pbeam];  // unconditional read; bp[pbeam] is a sentinel
@@ -1863,7 +1863,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
                 }
                 const uint64_t lt = (1ull << lane) - 1ull;
                 uint32_t before = nexp;
-    #pragma unroll
+#pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     if (lane_in(m[k])) {
                         const uint32_t r = before + static_cast<uint32_t>(__popcll(m[k] & lt));
@@ -2211,7 +2211,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
                 if (lead) {
                     // (e) kept children listed in (task, lane) order
                     uint32_t total = 0;
-    #pragma unroll
+#pragma unroll
                     for (int sr = 0; sr < SR; ++sr) {
                         // the sub-round's TPW tasks sit in lane order and follow
                         // each other in the list: a kept lane's place is the running
