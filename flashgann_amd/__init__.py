@@ -128,6 +128,13 @@ class Index:
                                      C.c_void_p(results_ptr), C.c_void_p(counters_ptr or None),
                                      C.c_void_p(stream or None)))
 
+    def search_waves(self, nq: int, K: int, beam: int) -> int:
+        """Waves per query (1, or 2 for the kernel's team form) that a search
+        of nq queries at this K and beam launches (fg_search_waves)."""
+        w = lib().fg_search_waves(self._h, nq, K, beam)
+        check(w if w < 0 else 0)
+        return w
+
     def search_stream(self, queries_ptr: int, nq: int, K: int, beam: int, results_ptr: int,
                       batch: int, nstreams: int = 2, stream: int = 0) -> None:
         """Device pointers; the nq queries searched as batches of `batch` on

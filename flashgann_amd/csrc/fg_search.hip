@@ -2652,10 +2652,15 @@ inline bool use_team(const SearchParams &P, const void *one_wave_kernel) {
 }
 
 template <int WT, int DPL, int DIM_T, int DEG_T, bool BIG>
-void launch_geo_b(const SearchParams &P, hipStream_t stream, bool count, bool prof) {
+void launch_geo_b(const SearchParams &P, hipStream_t stream, bool count, bool prof, int *waves_only) {
     const dim3 grid(P.nq), block(64);
-    if (!prof && use_team(P, reinterpret_cast<const void *>(
-                                 &fg_search_kernel<WT, DPL, DIM_T, DEG_T, false, false, BIG, 1>))) {
+    const bool team = !prof && use_team(P, reinterpret_cast<const void *>(
+                                              &fg_search_kernel<WT, DPL, DIM_T, DEG_T, false, false, BIG, 1>));
+    if (waves_only) {  // the form only, no launch
+        *waves_only = team ? 2 : 1;
+        return;
+    }
+    if (team) {
         const dim3 team_block(128);
         if (count)
             hipLaunchKernelGGL((fg_search_kernel<WT, DPL, DIM_T, DEG_T, true, false, BIG, 2>), grid, team_block,
@@ -2679,35 +2684,36 @@ void launch_geo_b(const SearchParams &P, hipStream_t stream, bool count, bool pr
 // Beams over 256 (two or more merge-path segments per lane, the pick's wide
 // scan) and smaller ones run separately compiled kernels.
 template <int WT, int DPL, int DIM_T, int DEG_T>
-void launch_geo(const SearchParams &P, hipStream_t stream, bool count, bool prof) {
-    if (P.pbeam > 256) launch_geo_b<WT, DPL, DIM_T, DEG_T, true>(P, stream, count, prof);
-    else launch_geo_b<WT, DPL, DIM_T, DEG_T, false>(P, stream, count, prof);
+void launch_geo(const SearchParams &P, hipStream_t stream, bool count, bool prof, int *waves_only) {
+    if (P.pbeam > 256) launch_geo_b<WT, DPL, DIM_T, DEG_T, true>(P, stream, count, prof, waves_only);
+    else launch_geo_b<WT, DPL, DIM_T, DEG_T, false>(P, stream, count, prof, waves_only);
 }
 
 // Shape classes: the benchmark shapes (d 128 / deg 32; d 96 / deg 32 and 16)
 // get fully compile-time geometry while the codebook is under 4 GiB; other
 // shapes and larger codebooks use runtime offsets.
 template <bool PROF>
-int launch_t(const SearchParams &P, hipStream_t stream) {
-    if (P.nq == 0) return FG_OK;
+int launch_t(const SearchParams &P, hipStream_t stream, int *waves_only = nullptr) {
+    if (P.nq == 0 && !waves_only) return FG_OK;
     const bool count = P.counters != nullptr;
     const int W = P.padded_dim / 32;
     const bool fixed = !P.runtime_geo;
     if (fixed && P.dim == 128 && P.degree == 32) {
-        launch_geo<4, 4, 128, 32>(P, stream, count, PROF);
+        launch_geo<4, 4, 128, 32>(P, stream, count, PROF, waves_only);
     } else if (fixed && P.dim == 96 && P.degree == 32) {
-        launch_geo<4, 3, 96, 32>(P, stream, count, PROF);
+        launch_geo<4, 3, 96, 32>(P, stream, count, PROF, waves_only);
     } else if (fixed && P.dim == 96 && P.degree == 16) {
-        launch_geo<4, 3, 96, 16>(P, stream, count, PROF);
+        launch_geo<4, 3, 96, 16>(P, stream, count, PROF, waves_only);
     } else if (W == 2 && P.dim <= 64) {
-        launch_geo<2, 2, 0, 0>(P, stream, count, PROF);
+        launch_geo<2, 2, 0, 0>(P, stream, count, PROF, waves_only);
     } else if (W == 4 && P.dim <= 96) {
-        launch_geo<4, 3, 0, 0>(P, stream, count, PROF);
+        launch_geo<4, 3, 0, 0>(P, stream, count, PROF, waves_only);
     } else if (W == 4) {
-        launch_geo<4, 4, 0, 0>(P, stream, count, PROF);
+        launch_geo<4, 4, 0, 0>(P, stream, count, PROF, waves_only);
     } else {
-        launch_geo<0, 0, 0, 0>(P, stream, count, PROF);
+        launch_geo<0, 0, 0, 0>(P, stream, count, PROF, waves_only);
     }
+    if (waves_only) return FG_OK;
     FG_HIP(hipGetLastError(), "search kernel launch");
     return FG_OK;
 }
@@ -2737,6 +2743,15 @@ uint32_t fg_lds_bytes(uint32_t dim, uint32_t beam, uint32_t degree) {
     uint32_t b = 1;
     while (b < dim) b <<= 1;
     return lds_layout(dim, b, effective_sort_beam(beam), visited_buckets(beam, degree)).total;
+}
+
+int fg_search_waves(fg_index *ix, uint32_t nq, uint32_t K, uint32_t beam) {
+    if (!ix) return fail(FG_EINVAL, "index is NULL");
+    SearchParams P;
+    if (int rc = make_params(ix, nq, K, beam, P)) return rc;
+    int waves = 1;
+    if (int rc = launch_t<false>(P, nullptr, &waves)) return rc;
+    return waves;
 }
 
 int fg_index_create(const float *rows, uint64_t npoints, uint32_t dim, uint32_t degree, const float *signs,

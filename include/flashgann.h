@@ -156,6 +156,14 @@ int fg_search_profile(fg_index *index, const float *d_queries, uint32_t nq, uint
  * calculate_shared_mem_size, src/adaptive_search_utils.cuh:152-176). */
 uint32_t fg_lds_bytes(uint32_t dim, uint32_t beam, uint32_t degree);
 
+/* Waves per query (1 or 2) that a search of nq queries at this K and beam
+ * launches on the current device: two, the kernel's team form, when the batch
+ * is too small to fill the device with one wave per query; FLASHGANN_TEAM=0/1
+ * in the environment forces one form.  Results are identical either way.
+ * Negative FG_E* on invalid arguments.  No counterpart in the reference (one
+ * warp-per-parent block shape). */
+int fg_search_waves(fg_index *index, uint32_t nq, uint32_t K, uint32_t beam);
+
 /* Query preparation only (utils.cuh:840-939): rotated query (padded_dim
  * float32), quantized levels (padded_dim uint8), and {low, high, width} plus
  * sum_q, for nq host queries.  Test hook for the preparation stage. */

@@ -330,3 +330,19 @@ def test_search_shape_limits(gpu_available, dim, degree):
     cb, q, _ = small_index(n=800, nq=12, dim=dim, degree=degree, comps=8)
     ids, cnt, rids, rcnt = _run(cb, q, 10, 64)
     _assert_equal(ids, cnt, rids, rcnt, f"dim={dim} degree={degree}")
+
+
+def test_search_waves_reports_the_form(gpu_available, monkeypatch):
+    """fg_search_waves: 2 (the team form) for a batch too small to fill the
+    device, 1 for one that fills it, and the environment override wins."""
+    from flashgann_amd import Index
+    cb, q, _ = small_index()
+    ix = Index.from_codebook(cb)
+    monkeypatch.delenv("FLASHGANN_TEAM", raising=False)
+    assert ix.search_waves(16, 10, 64) == 2
+    assert ix.search_waves(100000, 10, 64) == 1
+    monkeypatch.setenv("FLASHGANN_TEAM", "0")
+    assert ix.search_waves(16, 10, 64) == 1
+    monkeypatch.setenv("FLASHGANN_TEAM", "1")
+    assert ix.search_waves(100000, 10, 64) == 2
+    ix.close()
