@@ -210,9 +210,9 @@ __host__ __device__ constexpr LdsLayout lds_layout(uint32_t dim, uint32_t padded
     // phase timers of the profiling build only, past the end of the rest
     L.prof_off = L.total;
     L.total_prof = L.total + 16u * 8u;
-    // a team launch's exchange block (the profiling build has no team form)
-    L.team_off = L.total;
-    L.total_team = L.total + kTeamBytes;
+    // a team launch's exchange block, past the phase timers
+    L.team_off = L.total_prof;
+    L.total_team = L.total_prof + kTeamBytes;
     return L;
 }
 
@@ -1603,7 +1603,7 @@ __device__ __forceinline__ void hash_contains_n(const uint32_t *t, uint32_t nb, 
     do {                                                             \
         if constexpr (PROF) {                                        \
             const unsigned long long t_ = __builtin_amdgcn_s_memtime(); \
-            if (lane == 0) prof[i] += t_ - t_last;                   \
+            if (lead && lane == 0) prof[i] += t_ - t_last;           \
             t_last = t_;                                             \
         }                                                            \
     } while (0)
@@ -1627,7 +1627,7 @@ __device__ __forceinline__ void hash_contains_n(const uint32_t *t, uint32_t nb, 
 // the workgroup barriers mark the meeting points.
 template <int WT, int DPL, int DIM_T, int DEG_T, bool COUNT, bool PROF, bool BIG, int NW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 3 : 5))) void fg_search_kernel(SearchParams P) {
-    static_assert(NW == 1 || (NW == 2 && !PROF), "team form: two waves, no profiling build");
+    static_assert(NW == 1 || NW == 2, "team form: two waves");
     extern __shared__ __align__(16) unsigned char smem[];
     const int qid = blockIdx.x;
     if (qid >= P.nq) return;
@@ -2654,15 +2654,18 @@ inline bool use_team(const SearchParams &P, const void *one_wave_kernel) {
 template <int WT, int DPL, int DIM_T, int DEG_T, bool BIG>
 void launch_geo_b(const SearchParams &P, hipStream_t stream, bool count, bool prof, int *waves_only) {
     const dim3 grid(P.nq), block(64);
-    const bool team = !prof && use_team(P, reinterpret_cast<const void *>(
-                                              &fg_search_kernel<WT, DPL, DIM_T, DEG_T, false, false, BIG, 1>));
+    const bool team = use_team(P, reinterpret_cast<const void *>(
+                                      &fg_search_kernel<WT, DPL, DIM_T, DEG_T, false, false, BIG, 1>));
     if (waves_only) {  // the form only, no launch
         *waves_only = team ? 2 : 1;
         return;
     }
     if (team) {
         const dim3 team_block(128);
-        if (count)
+        if (prof)
+            hipLaunchKernelGGL((fg_search_kernel<WT, DPL, DIM_T, DEG_T, false, true, BIG, 2>), grid, team_block,
+                               P.lds.total_team, stream, P);
+        else if (count)
             hipLaunchKernelGGL((fg_search_kernel<WT, DPL, DIM_T, DEG_T, true, false, BIG, 2>), grid, team_block,
                                P.lds.total_team, stream, P);
         else
