@@ -1922,8 +1922,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
         int ex_n = 0;
         const uint32_t *ex_list = nullptr;
         if (theta <= 1) {
-          // (the lead wave's alone; a helper waits for the exact batch)
-          if (lead) {
+            // (the lead wave's alone; a helper waits for the exact batch)
+            if (lead) {
                 // ---------------- single expander (adaptive_search.cuh:221-343)
                 const int cwc = deg < cbs ? deg : cbs;
                 const uint32_t parent = uni(pnode[0]);
@@ -2012,7 +2012,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
                 ex_list = alist;
                 cand_span = 32;  // single-expander children sit at their lane's slot
                 FG_PHASE(4);
-          }
+            }
         } else {
             // ---------------- speculative expansion (adaptive_search.cuh:344-444)
             FG_COUNT(if (c_st2 == kMaxIndex) c_st2 = static_cast<uint32_t>(iter));
