@@ -5,13 +5,17 @@
 // around one 64-lane wavefront per query:
 //   * one workgroup = one wave = one query; the reference's 256-thread block
 //     barriers become wave-ordered LDS traffic, so the beam, candidate buffer,
-//     visited table and controller state never leave the CU's LDS/registers;
+//     visited table and controller state never leave the CU's LDS/registers
+//     (a launch too small to fill the device runs the team form instead: a
+//     second wave per query takes half of the expansion rounds and of the
+//     exact distances);
 //   * the reference's 32-lane sorting networks are data-oblivious, so the
 //     same compare-exchange sequence is replayed on the wave (two 32-lane
 //     halves, or 1-2 positions per lane) and ties resolve identically;
-//   * RaBitQ scores come from 7 popcount bit-planes of the quantized query
-//     held in LDS (raw = sum_p 2^p popcount(code & plane_p)), corrected for the
-//     reference's uint8 LUT wrap, instead of per-nibble LUT gathers;
+//   * RaBitQ scores come from 6 popcount bit-planes of the quantized query
+//     minus one, held in LDS (raw = popcount(code) + sum_p 2^p
+//     popcount(code & plane_p)), corrected for the reference's uint8 LUT wrap,
+//     instead of per-nibble LUT gathers;
 //   * exact distances keep the reference's per-lane accumulation order and
 //     reduction tree, so results are bitwise equal to the 32-lane original.
 // Determinism: where the reference races (concurrent inserts of one child by
