@@ -117,28 +117,38 @@ __host__ __device__ inline int keep_count_for_expander(uint32_t active, int thet
     return clamp_i(max_keep, 1, active_count);
 }
 
-// Visited-table size, in 4-slot buckets.  Between two resets the table
-// receives at most beam + 16 * 32 * tiles + 1 distinct keys (restore + one
-// reset interval of inserts, <= 32 per 8-task round, + the entry point).  A
-// table with more slots than that never fills, so it answers every
+// Visited-table size bounds, in 4-slot buckets.  Between two resets the
+// table receives at most beam + 16 * 32 * tiles + 1 distinct keys (restore +
+// one reset interval of inserts, <= 32 per 8-task round, + the entry point).
+// A table with more slots than that never fills, so it answers every
 // membership query exactly like the reference's 2^11-entry table
-// (utils.cuh:137-151), which never fills either.  The bucket count keeps that
-// worst case at <= 90% load.
-__host__ __device__ inline uint32_t visited_buckets(uint32_t beam, uint32_t degree) {
-    const uint32_t tiles = (degree + 31) / 32;
-    const uint32_t need = beam + 16u * 32u * tiles + 1u;
-    const uint32_t slots = (need * 10u + 8u) / 9u;
+// (utils.cuh:137-151), which never fills either.  The smallest table keeps
+// that worst case at <= 99% load with at least one slot to spare (an insert
+// always finds a free slot, a lookup's walk always meets one); the roomiest
+// at <= 90% (fewer lookups that walk on).  visited_buckets() picks between
+// them.
+__host__ __device__ inline uint32_t visited_keys_max(uint32_t beam, uint32_t degree) {
+    return beam + 16u * 32u * ((degree + 31) / 32) + 1u;
+}
+__host__ __device__ inline uint32_t visited_buckets_min(uint32_t beam, uint32_t degree) {
+    const uint32_t slots = (visited_keys_max(beam, degree) * 100u + 98u) / 99u + 1u;
+    return (slots + 3u) / 4u;
+}
+__host__ __device__ inline uint32_t visited_buckets_roomy(uint32_t beam, uint32_t degree) {
+    const uint32_t slots = (visited_keys_max(beam, degree) * 10u + 8u) / 9u;
     return (slots + 3u) / 4u;
 }
 
 struct LdsLayout {
-    uint32_t hash_off, beam_off, cand_off, msort_off, query_off, plane_off, scratch_off, prof_off, total,
-        total_prof, team_off, total_team;
+    uint32_t hash_off, beam_off, msort_off, plane_off, scratch_off, prof_off, total, total_prof, team_off,
+        total_team;
 };
 
-// Sorted-candidate staging for the beam merge: (distance, id) pairs at
-// indices -1 .. kMsortHi, the 32 sorted candidates at 0..31 between a
-// -FLT_MAX sentinel (index -1) and FLT_MAX sentinels (32 and up).
+// Candidate buffer and sorted-candidate staging of the beam merge, one array
+// of (distance, id) pairs at indices -1 .. kMsortHi: the 32 candidates at
+// 0..31 between a -FLT_MAX sentinel (index -1) and FLT_MAX sentinels (32 and
+// up).  The stages fill slots 0..31 in any order; the merge reads them into
+// registers, sorts them and writes them back sorted before it merges.
 constexpr int kMsortHi = 35;
 constexpr uint32_t kMsortPairs = 38;
 // Beam: (distance, id) pairs at indices -1 .. pbeam + kBeamPad - 1: a
@@ -179,22 +189,18 @@ __device__ __forceinline__ void team_stop(TeamBlock *tb, int lane) {
 
 
 // Per-query LDS: visited table and beam (aliased by the rotated query during
-// preparation), the 32-entry candidate buffer, the sorted-candidate
-// staging area (which, for d <= 128, also holds the raw query during set-up:
-// the loop keeps it in registers; a larger query is read from global memory,
-// where it stays cached), 8 x B/32 plane words and a small scratch area
-// (32-entry child list + parent ids and distances).
+// preparation), the candidate pairs, 8 x B/32 plane words and a small
+// scratch area (32-entry child list + parent ids and distances).  The raw
+// query is read from global memory, where it stays cached (the fixed
+// geometries keep it in registers through the loop).
 __host__ __device__ constexpr LdsLayout lds_layout(uint32_t dim, uint32_t padded_dim, uint32_t pbeam,
                                                    uint32_t buckets) {
     // fixed-size regions first (compile-time offsets for a fixed geometry),
     // then the beam-dependent visited table and beam
     LdsLayout L{};
     uint32_t off = 0;
-    L.cand_off = off;
-    off += 32u * 8u;
     L.msort_off = off;
     off += kMsortPairs * 8u;
-    L.query_off = 0;  // set-up only: d <= 128 floats fit in the 560 bytes above
     (void)dim;
     L.plane_off = off;
     off += 8u * (padded_dim / 32u) * 4u;
@@ -218,6 +224,25 @@ __host__ __device__ constexpr LdsLayout lds_layout(uint32_t dim, uint32_t padded
     L.team_off = L.total_prof;
     L.total_team = L.total_prof + kTeamBytes;
     return L;
+}
+
+// LDS is allocated to a workgroup in units of 1,280 bytes on gfx950
+// (measured: 7,632-byte workgroups fit 21 to a CU, 7,760-byte ones 18).
+constexpr uint32_t kLdsGranule = 1280;
+
+// The visited table a search uses: the roomiest table (at most 90% worst-case
+// load) that fits in as many LDS granules as the smallest one needs, so the
+// table never costs a workgroup per CU (beam 384: 21 instead of 18 per CU,
+// beam 512: 18 instead of 16, beam 1024: 10 instead of 9) and keeps its
+// slack where that is free (beam 256).
+__host__ __device__ inline uint32_t visited_buckets(uint32_t dim, uint32_t padded_dim, uint32_t pbeam, uint32_t beam,
+                                                    uint32_t degree) {
+    const uint32_t lo = visited_buckets_min(beam, degree);
+    const uint32_t total = lds_layout(dim, padded_dim, pbeam, lo).total;
+    const uint32_t cap = (total + kLdsGranule - 1u) / kLdsGranule * kLdsGranule;
+    uint32_t b = visited_buckets_roomy(beam, degree);
+    while (b > lo && lds_layout(dim, padded_dim, pbeam, b).total > cap) --b;
+    return b;
 }
 
 struct SearchParams {
@@ -770,7 +795,7 @@ __device__ __forceinline__ void exact_generic_pass(const SearchParams &P, uint64
     for (int j = 0; j < PB; ++j) {
         const int e = e0 + 2 * j + h;
         const int slot = e < n ? static_cast<int>(slot_list ? slot_list[e] : static_cast<uint32_t>(e)) : 0;
-        const uint32_t child = e < n ? ci[slot] : 0u;
+        const uint32_t child = e < n ? ci[2 * slot] : 0u;
         rows[j] = P.data + static_cast<uint64_t>(child) * row_floats;
     }
     float acc[PB];
@@ -796,7 +821,7 @@ __device__ __forceinline__ void exact_generic_pass(const SearchParams &P, uint64
         const int e = e0 + 2 * j + h;
         if (e < n && nl == 0) {
             const int slot = static_cast<int>(slot_list ? slot_list[e] : static_cast<uint32_t>(e));
-            cd[slot] = beam_key(ip ? -r : r);
+            cd[2 * slot] = beam_key(ip ? -r : r);
         }
     }
 }
@@ -1074,8 +1099,9 @@ __device__ __forceinline__ void merge_path(const SearchParams &P, uint2 *bp, con
 }
 
 // Beam merge (utils.cuh:1369-1399 dispatch for a <= 32-entry buffer): the
-// candidates are sorted (warp_sort<1>), staged in `ms`, and merged into the
-// beam in place.  `span`: slots at or past it hold (FLT_MAX, MAX_INDEX), so a
+// candidates (slot s: distance cd[2 s], id ci[2 s], the pairs of `ms`) are
+// read into registers, sorted (warp_sort<1>), written back to `ms` in sorted
+// order, and merged into the beam in place.  `span`: slots at or past it hold (FLT_MAX, MAX_INDEX), so a
 // candidate buffer filled only in its first 8 or 16 slots is sorted with the
 // stages that reach that block size (sort32<TOP>).  `fast_ok` stays true while
 // every pair merged into this beam has a key in (-FLT_MAX, FLT_MAX) or is the
@@ -1089,8 +1115,8 @@ __device__ __forceinline__ void merge_beam(const SearchParams &P, uint2 *bp, uin
     lb_out = 0;
     const int nl = lane & 31, h = lane >> 5;
     const int cbs = P.cbs, pbeam = P.pbeam;
-    float ck = nl < cbs ? cd[nl] : FLT_MAX;
-    uint32_t cv = nl < cbs ? ci[nl] : kMaxIndex;
+    float ck = nl < cbs ? cd[2 * nl] : FLT_MAX;
+    uint32_t cv = nl < cbs ? ci[2 * nl] : kMaxIndex;
     fast_ok = fast_ok && !any_lane(!((ck > -FLT_MAX && ck < FLT_MAX) || (ck == FLT_MAX && cv == kMaxIndex)));
     // every key of the span at most FLT_MAX (never inf or NaN)
     const bool short_ok = !any_lane(nl < span && !(ck <= FLT_MAX));
@@ -1391,7 +1417,7 @@ __device__ __forceinline__ void exact_pass(const SearchParams &P, const G &g, in
     }
     uint32_t cid[PB];
 #pragma unroll
-    for (int j = 0; j < PB; ++j) cid[j] = ci[sl[j]];
+    for (int j = 0; j < PB; ++j) cid[j] = ci[2 * sl[j]];
     float v[PB][DPL];
     if constexpr (G::kFixed) {
         const uint32_t lo = static_cast<uint32_t>(nl) * 4u;  // this lane's first dimension
@@ -1483,11 +1509,12 @@ __device__ __forceinline__ void exact_pass(const SearchParams &P, const G &g, in
     const int e = e0 + 2 * c + h;
     if (e < n && (nl & (kGroup - 1)) == 0) {
         const int sl = slot_list ? static_cast<int>(slot_list[e] & 31u) : e;
-        cd[sl] = beam_key(ip ? -r4 : r4);
+        cd[2 * sl] = beam_key(ip ? -r4 : r4);
     }
 }
 
-// Exact distances for children lo .. n-1 held in cd/ci at slots
+// Exact distances for children lo .. n-1 held in the candidate pairs (id at
+// ci[2 s], distance written to cd[2 s]) at slots
 // slot_list[lo..n) (or lo..n when slot_list is null): passes of 16
 // children, the last one sized to what is left (DPL > 0: dims per lane known
 // at compile time; DPL == 0: generic geometry, exact_generic_pass).
@@ -1619,7 +1646,7 @@ __device__ __forceinline__ void hash_contains_n(const uint32_t *t, uint32_t nb, 
 
 // One wave per workgroup; the register budget targets 5 waves per SIMD
 // (<= 96 VGPRs; the fixed-geometry kernels use 77-79, which leaves room for
-// a sixth), which LDS also allows for beams up to 256 (6,400 bytes a
+// a sixth), which LDS also allows for beams up to 256 (6,144 bytes a
 // workgroup at beam 256).  The generic-geometry instantiation (padded dimension
 // >= 256) gets 3 (<= 168 VGPRs) for its wide code batches and the plane reads
 // it keeps in flight: at padded dimension 2048 its LDS (raw query, planes,
@@ -1652,19 +1679,17 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
     // (the same layout function the host sizes the launch with)
     constexpr bool kFixedGeo = Geo<DIM_T, DEG_T>::kFixed;
     constexpr LdsLayout kL = lds_layout(DIM_T, Geo<DIM_T, DEG_T>::kB, 0, 0);
-    const uint32_t query_off = kFixedGeo ? kL.query_off : P.lds.query_off;
     const uint32_t plane_off = kFixedGeo ? kL.plane_off : P.lds.plane_off;
     const uint32_t scratch_off = kFixedGeo ? kL.scratch_off : P.lds.scratch_off;
     const uint32_t prof_off = P.lds.prof_off;
-    static_assert(kL.cand_off == 0 && kL.msort_off == 256u, "fixed LDS regions");
-    static_assert(32u * 8u + kMsortPairs * 8u >= 128u * 4u, "an aliased query fits the candidate and staging area");
+    static_assert(kL.msort_off == 0u, "fixed LDS regions");
     uint32_t *H = reinterpret_cast<uint32_t *>(smem + P.lds.hash_off);
     // beam pairs: bp[-1] and bp[pbeam] are sentinels
     uint2 *bp = reinterpret_cast<uint2 *>(smem + P.lds.beam_off) + 1;
     uint2 *ms = reinterpret_cast<uint2 *>(smem + kL.msort_off) + 1;
-    float *cd = reinterpret_cast<float *>(smem);
-    uint32_t *ci = reinterpret_cast<uint32_t *>(cd + 32);
-    float *qv = reinterpret_cast<float *>(smem + query_off);
+    // candidate slot s: distance at cd[2 s], id at ci[2 s] (the pair ms[s])
+    float *cd = reinterpret_cast<float *>(ms);
+    uint32_t *ci = reinterpret_cast<uint32_t *>(ms) + 1;
     uint32_t *planes = reinterpret_cast<uint32_t *>(smem + plane_off);
     uint32_t *alist = reinterpret_cast<uint32_t *>(smem + scratch_off);
     uint32_t *pnode = alist + 32;
@@ -1682,11 +1707,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
     int sum_q = 0;
     if (lead)
         prepare_query<NW>(P.queries + static_cast<uint64_t>(qid) * g.dim, P.signs, g.dim, B,
-                          reinterpret_cast<float *>(H), WT == 0 ? nullptr : qv, planes, qlow, qhigh, qwidth, sum_q,
-                          nullptr);
-    // the generic geometry reads the query from global memory (it stays
-    // cached), the others keep it in registers (qr below)
-    const float *qsrc = WT == 0 ? P.queries + static_cast<uint64_t>(qid) * g.dim : qv;
+                          reinterpret_cast<float *>(H), nullptr, planes, qlow, qhigh, qwidth, sum_q, nullptr);
+    // the query is read from global memory, where it stays cached (the
+    // generic geometry's exact distances read it there; the others keep it in
+    // registers, qr below)
+    const float *qsrc = P.queries + static_cast<uint64_t>(qid) * g.dim;
     constexpr int WTR = WT > 0 ? WT : 1;
     // whether any chunk of the quantized query wraps the reference's uint8
     // LUT entry (then the estimates subtract the wrapped chunks)
@@ -1713,13 +1738,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
     }
     constexpr int DPLR = DPL > 0 ? DPL : 1;
     float qr[DPLR];
-    // (the helper wave reads the query from global memory: the LDS copy is
-    // overwritten once the lead wave initialises the candidate area)
-    const float *qraw = lead ? qv : P.queries + static_cast<uint64_t>(qid) * g.dim;
 #pragma unroll
     for (int k = 0; k < DPLR; ++k) {
         const int i = nl + 32 * k;
-        qr[k] = (DPL > 0 && i < g.dim) ? qraw[i] : 0.0f;
+        qr[k] = (DPL > 0 && i < g.dim) ? qsrc[i] : 0.0f;
     }
 
     const uint2 kEmpty = make_uint2(__float_as_uint(FLT_MAX), kMaxIndex);
@@ -1728,22 +1750,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
     if (lead) {
         entry_d = uni(beam_key(half_distance(P.data + static_cast<uint64_t>(P.entry) * g.row, qsrc, g.dim, nl,
                                              P.use_ip != 0, true)));
-        // the query's LDS copy may share the candidate and staging area: every
-        // lane is done reading it before that area is initialised
-        lead_sync<NW>();
 
         // ---- state (adaptive_search.cuh:67-107)
         hash_reset(H, nbk);
         for (int i = lane - 1; i < P.pbeam + static_cast<int>(kBeamPad); i += 64) bp[i] = i < 0 ? kLowSentinel : kEmpty;
-        if (lane <= kMsortHi + 1) ms[lane - 1] = lane == 0 ? kLowSentinel : kEmpty;
-        if (lane < 32) {
-            cd[lane] = FLT_MAX;
-            ci[lane] = kMaxIndex;
-        }
+        if (lane <= kMsortHi + 1) ms[lane - 1] = lane == 0 ? kLowSentinel : kEmpty;  // candidates empty
         lead_sync<NW>();
         if (lane == 0) {
-            cd[0] = entry_d;
-            ci[0] = P.entry;
+            ms[0] = make_uint2(__float_as_uint(entry_d), P.entry);
             hash_insert(H, nbk, P.entry);
         }
         lead_sync<NW>();
@@ -1815,8 +1829,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
                 break;
             }
             for (int i = beam_sz + lane; i < pbeam; i += 64) bp[i] = kEmpty;
-            cd[nl] = FLT_MAX;  // both halves store the same values: no branch
-            ci[nl] = kMaxIndex;
+            ms[nl] = kEmpty;  // both halves store the same pair: no branch
             lead_sync<NW>();
             kth = FLT_MAX;  // adaptive_search_utils.cuh:25-30
             if (bp[beam_sz - 1].y != kMaxIndex) kth = __uint_as_float(bp[(P.K < beam_sz ? P.K : beam_sz) - 1].x);
@@ -2005,8 +2018,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
                 }
                 const uint32_t ins_mask = half_bits(ballot(ins), 0);
                 if (h == 0) {
-                    cd[nl] = dist;
-                    ci[nl] = child;
+                    ms[nl] = make_uint2(__float_as_uint(dist), child);
                     if (ins) alist[__popc(ins_mask & ((1u << nl) - 1u))] = static_cast<uint32_t>(nl);
                 }
                 lead_sync<NW>();
@@ -2247,9 +2259,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
                     }
                     const uint32_t accm = half_bits(ballot(acc), 0);
                     if (acc) {
-                        // (cd was reset at the iteration's start; the exact pass fills it)
+                        // (the distance was reset at the iteration's start; the exact pass fills it)
                         const uint32_t slot = __builtin_amdgcn_mbcnt_lo(accm, compact);
-                        if (slot < static_cast<uint32_t>(P.collect_cap)) ci[slot] = key;
+                        if (slot < static_cast<uint32_t>(P.collect_cap)) ci[2 * slot] = key;
                     }
                     compact += static_cast<uint32_t>(__popc(accm));
                     lead_sync<NW>();
@@ -2592,7 +2604,8 @@ int make_params(fg_index *ix, uint32_t nq, uint32_t K, uint32_t beam, SearchPara
     if (cap > static_cast<uint32_t>(kBufferBound)) cap = kBufferBound;
     P.cbs = static_cast<int>(round_up_pow2(cap));
     P.collect_cap = P.cbs < kBufferBound ? P.cbs : kBufferBound;
-    P.buckets = static_cast<int>(visited_buckets(beam, ix->degree));
+    P.buckets = static_cast<int>(
+        visited_buckets(ix->dim, ix->padded_dim, static_cast<uint32_t>(P.pbeam), beam, ix->degree));
     // The reference's visited table has 2^bitlen slots with bitlen sized for
     // 32 inserts per iteration (utils.cuh:137-151): 2048 at every beam up to
     // 1024.  Between two resets it receives at most beam + 16 * 32 * tiles
@@ -2749,7 +2762,8 @@ const char *fg_version(void) { return "flashgann-amd 0.1 (gfx950, wave64)"; }
 uint32_t fg_lds_bytes(uint32_t dim, uint32_t beam, uint32_t degree) {
     uint32_t b = 1;
     while (b < dim) b <<= 1;
-    return lds_layout(dim, b, effective_sort_beam(beam), visited_buckets(beam, degree)).total;
+    const uint32_t pb = effective_sort_beam(beam);
+    return lds_layout(dim, b, pb, visited_buckets(dim, b, pb, beam, degree)).total;
 }
 
 int fg_search_waves(fg_index *ix, uint32_t nq, uint32_t K, uint32_t beam) {
