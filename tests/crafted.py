@@ -203,3 +203,34 @@ def line_index(n: int = 20000, dim: int = 64, degree: int = 32):
     q[:, 0] = [n + 10, n + 500, n + 3000, 2 * n]
     q[:, 1] = [0, 1, 2, 3]
     return cb, q, base
+
+
+@functools.lru_cache(maxsize=None)
+def random_graph_index(n: int = 20000, dim: int = 128, degree: int = 32, nq: int = 4, seed: int = 7):
+    """Integer points in [0, 16)^dim, each linked to `degree` uniformly random
+    other points; entry point 0, queries from the same distribution.  Nearly
+    every child is fresh, so with K = beam each stage-II iteration inserts
+    close to 32 keys into the visited table: between two resets the table
+    comes within a few keys of its worst case (beam + 16 x 32 + 1 keys), which
+    the kernel's table is sized to hold with one slot to spare."""
+    from flashgann_amd import builder, datasets
+    rng = np.random.default_rng(seed)
+    base = rng.integers(0, 16, size=(n, dim)).astype(np.float32)
+    q = rng.integers(0, 16, size=(nq, dim)).astype(np.float32)
+    nb = rng.integers(0, n - 1, size=(n, degree))
+    nb = nb + (nb >= np.arange(n)[:, None])  # no self links
+    cb = builder.codebook_from_graph(base, nb, datasets.signs_for(128, 1), entry=0)
+    return cb, q, base
+
+
+def visited_peak(trace, beam: int) -> int:
+    """Most distinct keys the visited set holds between two resets of one
+    traced search: the restored beam (every merged candidate enters the beam
+    until it is full, and none repeats an entry still in it) plus the
+    candidates inserted over the next 16 iterations and the entry point."""
+    valid = np.array([sum(1 for c in r.cand_idx if c != 0xFFFFFFFF) for r in trace])
+    merged = 1 + np.cumsum(valid)
+    peak = 0
+    for t0 in range(15, len(trace), 16):
+        peak = max(peak, min(beam, int(merged[t0 - 1])) + int(valid[t0:t0 + 16].sum()) + 1)
+    return peak

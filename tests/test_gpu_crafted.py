@@ -63,3 +63,14 @@ def test_complete_graph_brute_force(gpu_available):
     ids, cnt, rids, rcnt = _both(cb, q, 10, 64)
     assert np.array_equal(ids, gt)
     assert np.array_equal(ids, rids) and np.array_equal(cnt, rcnt)
+
+
+@pytest.mark.parametrize("beam", [256, 512, 1024])
+def test_random_graph_nearly_full_visited_set(gpu_available, beam):
+    """Random links and K = beam: the visited set comes within a few keys of
+    the worst case the table is sized for (test_oracle_search checks the fill
+    on the oracle's traces); ids and work counters equal the oracle's."""
+    cb, q, _ = crafted.random_graph_index()
+    ids, cnt, rids, rcnt = _both(cb, q, beam, beam)
+    assert np.array_equal(cnt, rcnt)
+    assert np.array_equal(ids, rids)

@@ -88,3 +88,22 @@ def test_trace_records_theta_switch():
         assert all(t == 8 for t in thetas[k:]) and all(t == 1 for t in thetas[:k])
     rhos = [t.rho for t in tr if t.theta == 1]
     assert rhos[0] >= 0.25 and all(b >= a for a, b in zip(rhos, rhos[1:]))   # stage-I rho never decreases
+
+
+@pytest.mark.parametrize("beam,floor", [(256, 0.95), (512, 0.96), (1024, 0.99)])
+def test_random_graph_fills_the_visited_set(beam, floor):
+    """The random-graph input of the GPU parity test drives the visited set to
+    within a few keys of its worst case between two resets (beam + 16 x 32 +
+    1 keys), the bound the kernel's table is sized for: the GPU test on it
+    exercises a nearly full table."""
+    import crafted
+    cb, q, _ = crafted.random_graph_index()
+    ix = O.OracleIndex.from_codebook(cb)
+    worst = beam + 16 * 32 + 1
+    peaks = []
+    for i in range(len(q)):
+        _, cnt, tr = ix.search_one(q[i], beam, beam, trace_cap=1100)
+        assert len(tr) == cnt.iterations
+        peaks.append(crafted.visited_peak(tr, beam))
+    assert max(peaks) <= worst
+    assert max(peaks) >= floor * worst, (peaks, worst)
