@@ -267,8 +267,31 @@ struct SearchParams {
     int team;         // host only: the team form (two waves per query) may run
     uint32_t entry;
     int nq;
+    // Two-launch search (one-wave form, beams up to 256): slice 1 runs every
+    // query to the top of iteration slice_stop and keeps an unfinished
+    // query's state in slice_state; slice 2 resumes the queries slice_order
+    // lists (longest expected first), the first slice_state[0] of them.
+    int slice = 0;  // 0: one launch; 1: first slice; 2: second slice
+    int slice_stop = 0;
+    uint32_t *slice_state = nullptr;        // kSliceHeader words, then slice_words(pbeam) per query
+    uint32_t *slice_keys = nullptr;         // per query: ordering key, or kSliceDone
+    const uint32_t *slice_order = nullptr;  // second slice: query of each workgroup
     LdsLayout lds;
 };
+
+// Per-query state of a suspended search, in 32-bit words after a header of
+// kSliceHeader words (word 0: the number of suspended queries, set by the
+// order kernel).  Per query: a mark (1), the ordering key, the controller (9
+// words), the work counters (6), the candidate span and the split flag, then
+// the pbeam beam pairs and the 32 candidate pairs.  slice_keys holds the
+// key (bits of a non-negative distance) of each suspended query and
+// kSliceDone for a query the first slice finished.
+constexpr uint32_t kSliceHeader = 64;
+constexpr uint32_t kSliceFixed = 20;  // 2 + 9 + 6 + 2, padded to keep the pairs 8-byte aligned
+__host__ __device__ inline uint32_t slice_words(uint32_t pbeam) { return kSliceFixed + 2u * (pbeam + 32u); }
+constexpr uint32_t kSliceDone = 0xFFFFFFFFu;
+constexpr int kSliceMaxQueries = 16384;  // the order kernel holds every query's bin in LDS
+constexpr int kSliceBins = 4096;
 
 
 // Row geometry (include/qg.hpp:66-73), compile-time for the specialised
@@ -1660,8 +1683,20 @@ template <int WT, int DPL, int DIM_T, int DEG_T, bool COUNT, bool PROF, bool BIG
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0 ? 3 : 5))) void fg_search_kernel(SearchParams P) {
     static_assert(NW == 1 || NW == 2, "team form: two waves");
     extern __shared__ __align__(16) unsigned char smem[];
-    const int qid = blockIdx.x;
+    int qid = blockIdx.x;
     if (qid >= P.nq) return;
+    // the two-launch search runs in the one-wave form at beams up to 256
+    constexpr bool kSliceable = NW == 1 && !BIG && !PROF;
+    if constexpr (kSliceable) {
+        if (P.slice == 2) {
+            // workgroup w resumes the w-th query of the order, if there is one
+            const uint32_t n = __builtin_amdgcn_readfirstlane(P.slice_state[0]);
+            if (static_cast<uint32_t>(qid) >= n) return;
+            const uint32_t o = __builtin_amdgcn_readfirstlane(P.slice_order[qid]);
+            if (o >= static_cast<uint32_t>(P.nq)) return;
+            qid = static_cast<int>(o);
+        }
+    }
     const int lane = lane_id();
     // wave index within the team (0 for the one-wave form)
     const int wv = NW > 1 ? (__builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x)) >> 6) : 0;
@@ -1794,9 +1829,54 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
     int scan_from = 0, lb_merge = 0;
     const float *data = P.data;
 
-    FG_PHASE(0);
     int iter = 0;
+    bool suspended = false;
+    if constexpr (kSliceable) {
+        if (P.slice == 2) {
+            // resume at the top of iteration slice_stop (before its visited-table
+            // rebuild, which derives the table from the beam): the beam, the
+            // unmerged candidates, the controller and the counters as the first
+            // slice left them.  Ids are checked so that no later row read can
+            // leave the codebook, whatever the buffer holds.
+            const uint32_t *st = P.slice_state + kSliceHeader + static_cast<uint64_t>(qid) * slice_words(pbeam);
+            const uint2 *sb = reinterpret_cast<const uint2 *>(st + kSliceFixed);
+            const uint2 kEmptyPair = make_uint2(__float_as_uint(FLT_MAX), kMaxIndex);
+            for (int i = lane; i < pbeam + 32; i += 64) {
+                const uint2 e = sb[i];
+                const bool ok = e.y == kMaxIndex || static_cast<uint64_t>(e.y & 0x7FFFFFFFu) < P.npoints;
+                if (i < pbeam) bp[i] = ok ? e : kEmptyPair;
+                else ms[i - pbeam] = ok ? e : kEmptyPair;
+            }
+            ctl.spec = clamp_i(static_cast<int>(uni(st[2])), 1, kSearchWidth);
+            ctl.rho = __uint_as_float(uni(st[3]));
+            ctl.policy_iters = static_cast<int>(uni(st[4]));
+            ctl.top1 = uni(st[5]);
+            ctl.stall = static_cast<int>(uni(st[6]));
+            ctl.warm = uni(st[7]) != 0u;
+            ctl.entry_d = __uint_as_float(uni(st[8]));
+            ctl.last_e = __uint_as_float(uni(st[9]));
+            ctl.cur_e = __uint_as_float(uni(st[10]));
+            c_iters = uni(st[11]);
+            c_exp = uni(st[12]);
+            c_ids = uni(st[13]);
+            c_est = uni(st[14]);
+            c_exact = uni(st[15]);
+            c_st2 = uni(st[16]);
+            cand_span = clamp_i(static_cast<int>(uni(st[17])), 0, kBufferBound);
+            split_fast = uni(st[18]) != 0u;
+            iter = P.slice_stop;
+            lead_sync<NW>();
+        }
+    }
+
+    FG_PHASE(0);
     for (; iter < kMaxIterations; ++iter) {
+        if constexpr (kSliceable) {
+            if (P.slice == 1 && iter == P.slice_stop) {
+                suspended = true;
+                break;
+            }
+        }
         // lane-derived values are recomputed in each iteration, not held
         const int lane = lane_id_opaque();
         const int h = lane >> 5, nl = lane & 31;
@@ -2312,6 +2392,43 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
             c_est += uni(tb->c_est);
         }
     }
+    if constexpr (kSliceable) {
+        if (P.slice == 1) {
+            uint32_t *st = P.slice_state + kSliceHeader + static_cast<uint64_t>(qid) * slice_words(pbeam);
+            if (suspended) {
+                // the state the second slice resumes from; the ordering key is
+                // the best distance found so far (the larger, the longer the
+                // rest of the search tends to run)
+                uint2 *sb = reinterpret_cast<uint2 *>(st + kSliceFixed);
+                for (int i = lane; i < pbeam + 32; i += 64) sb[i] = i < pbeam ? bp[i] : ms[i - pbeam];
+                if (lane == 0) {
+                    const uint32_t key = __float_as_uint(fmaxf(pair_key(bp[0]), 0.0f));
+                    P.slice_keys[qid] = key;
+                    st[0] = 1u;
+                    st[1] = key;
+                    st[2] = static_cast<uint32_t>(ctl.spec);
+                    st[3] = __float_as_uint(ctl.rho);
+                    st[4] = static_cast<uint32_t>(ctl.policy_iters);
+                    st[5] = ctl.top1;
+                    st[6] = static_cast<uint32_t>(ctl.stall);
+                    st[7] = ctl.warm ? 1u : 0u;
+                    st[8] = __float_as_uint(ctl.entry_d);
+                    st[9] = __float_as_uint(ctl.last_e);
+                    st[10] = __float_as_uint(ctl.cur_e);
+                    st[11] = c_iters;
+                    st[12] = c_exp;
+                    st[13] = c_ids;
+                    st[14] = c_est;
+                    st[15] = c_exact;
+                    st[16] = c_st2;
+                    st[17] = static_cast<uint32_t>(cand_span);
+                    st[18] = split_fast ? 1u : 0u;
+                }
+                return;
+            }
+            if (lane == 0) P.slice_keys[qid] = kSliceDone;  // finished within the first slice
+        }
+    }
     // the loop ran out at kMaxIterations: the last iteration's exact-scored
     // candidates are still in the buffer (adaptive_search.cuh:449-451)
     if (iter == kMaxIterations) merge_beam<BIG, NW>(P, bp, ms, cd, ci, cand_span, split_fast, lb_merge);
@@ -2338,6 +2455,65 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
         c[3] = c_est;
         c[4] = c_exact;
         c[5] = c_st2;
+    }
+}
+
+// Order of the second slice: the suspended queries sorted by key, largest
+// first (a counting sort over kSliceBins bins of [0, largest key]; within a
+// bin the order is arbitrary).  One workgroup; writes the count to
+// slice_state[0] and the queries to order[0 .. count).
+__global__ __launch_bounds__(1024) void fg_slice_order_kernel(uint32_t *state, const uint32_t *keys, int nq,
+                                                             uint32_t *order) {
+    __shared__ uint16_t qb[kSliceMaxQueries];  // each query's bin (0xFFFF: finished)
+    __shared__ uint32_t hist[kSliceBins];
+    __shared__ uint32_t part[1024];
+    __shared__ uint32_t kmax;
+    const int t = static_cast<int>(threadIdx.x);
+    for (int b = t; b < kSliceBins; b += 1024) hist[b] = 0u;
+    if (t == 0) kmax = 0u;
+    __syncthreads();
+    uint32_t m = 0u;
+    for (int q = t; q < nq; q += 1024) {
+        const uint32_t v = keys[q];
+        if (v != kSliceDone) m = max(m, v);
+    }
+    atomicMax(&kmax, m);
+    __syncthreads();
+    const float top = __uint_as_float(kmax);
+    const float scale = top > 0.0f ? static_cast<float>(kSliceBins - 1) / top : 0.0f;
+    for (int q = t; q < nq; q += 1024) {
+        const uint32_t v = keys[q];
+        uint32_t b = 0xFFFFu;
+        if (v != kSliceDone) {
+            const int x = static_cast<int>(__uint_as_float(v) * scale);
+            b = static_cast<uint32_t>(kSliceBins - 1 - min(max(x, 0), kSliceBins - 1));  // largest key first
+            atomicAdd(&hist[b], 1u);
+        }
+        qb[q] = static_cast<uint16_t>(b);
+    }
+    __syncthreads();
+    // exclusive scan: four bins per thread, then the 1024 partial sums
+    constexpr int kPer = kSliceBins / 1024;
+    uint32_t loc[kPer], sum = 0u;
+    for (int j = 0; j < kPer; ++j) {
+        loc[j] = sum;
+        sum += hist[t * kPer + j];
+    }
+    part[t] = sum;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {
+        const uint32_t v = t >= off ? part[t - off] : 0u;
+        __syncthreads();
+        part[t] += v;
+        __syncthreads();
+    }
+    const uint32_t base = part[t] - sum;
+    for (int j = 0; j < kPer; ++j) hist[t * kPer + j] = base + loc[j];
+    if (t == 1023) state[0] = part[1023];
+    __syncthreads();
+    for (int q = t; q < nq; q += 1024) {
+        const uint32_t b = qb[q];
+        if (b != 0xFFFFu) order[atomicAdd(&hist[b], 1u)] = static_cast<uint32_t>(q);
     }
 }
 
@@ -2468,6 +2644,12 @@ struct fg_index {
     size_t res_cap = 0;
     uint32_t *d_cnt = nullptr;
     size_t cnt_cap = 0;
+    // two-launch search: suspended queries' state, keys and order; the event
+    // after the last sliced search, which the next one waits for
+    uint32_t *d_slice = nullptr;
+    size_t slice_cap = 0;
+    hipEvent_t slice_done = nullptr;
+    bool slice_pending = false;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     // this device's staging area of fg_search_noalloc (device address)
     unsigned char *noalloc = nullptr;
@@ -2644,6 +2826,11 @@ int make_params(fg_index *ix, uint32_t nq, uint32_t K, uint32_t beam, SearchPara
     P.runtime_geo = ix->runtime_geo || ix->npoints * ix->row_offset * 4ull > 0xFFFFFFFFull ? 1 : 0;
     P.entry = ix->entry;
     P.nq = static_cast<int>(nq);
+    P.slice = 0;
+    P.slice_stop = 0;
+    P.slice_state = nullptr;
+    P.slice_keys = nullptr;
+    P.slice_order = nullptr;
     P.lds = lds_layout(ix->dim, ix->padded_dim, static_cast<uint32_t>(P.pbeam), static_cast<uint32_t>(P.buckets));
     P.team = P.lds.total_team <= 65536u ? 1 : 0;
     return FG_OK;
@@ -2738,7 +2925,54 @@ int launch_t(const SearchParams &P, hipStream_t stream, int *waves_only = nullpt
     return FG_OK;
 }
 
-int launch(fg_index *, const SearchParams &P, hipStream_t stream) { return launch_t<false>(P, stream); }
+// Whether a search runs as two launches (first slice, order, second slice):
+// the one-wave form at beams up to 256 with the L2 metric, a batch that
+// fills the device (the last queries to start are the ones that make a
+// launch's tail) and fits the order kernel.  FLASHGANN_SLICE=0 / 1 forces
+// one launch / two launches wherever the form allows them (tests run both).
+constexpr int kSliceStop = 15;  // the top of the first iteration that rebuilds the visited table
+bool slice_wanted(const SearchParams &P) {
+    if (P.nq < 1 || P.nq > kSliceMaxQueries || P.pbeam > 256 || P.max_iter <= kSliceStop || P.use_ip) return false;
+    if (const char *e = std::getenv("FLASHGANN_SLICE")) {
+        if (e[0] == '0') return false;
+        if (e[0] == '1') return true;
+    }
+    return P.nq >= 4096;
+}
+
+int launch(fg_index *ix, const SearchParams &P0, hipStream_t stream, bool may_slice) {
+    if (may_slice && slice_wanted(P0)) {
+        int waves = 0;
+        if (int rc = launch_t<false>(P0, stream, &waves)) return rc;
+        if (waves == 1) {
+            // one buffer: header (word 0: the count of suspended queries), the
+            // per-query states, the keys, the order
+            const uint64_t nq = static_cast<uint64_t>(P0.nq), pad = (nq + 63u) & ~63ull;
+            const uint64_t states = nq * slice_words(static_cast<uint32_t>(P0.pbeam));
+            const uint64_t words = kSliceHeader + states + 2u * pad;
+            if (int rc = ensure(reinterpret_cast<void **>(&ix->d_slice), &ix->slice_cap, words * 4u)) return rc;
+            if (!ix->slice_done) FG_HIP(hipEventCreateWithFlags(&ix->slice_done, hipEventDisableTiming), "event");
+            // a sliced search on another stream may still use the buffer
+            if (ix->slice_pending) FG_HIP(hipStreamWaitEvent(stream, ix->slice_done, 0), "stream wait");
+            uint32_t *state = ix->d_slice, *keys = state + kSliceHeader + states, *order = keys + pad;
+            SearchParams P = P0;
+            P.slice_stop = kSliceStop;
+            P.slice_state = state;
+            P.slice_keys = keys;
+            P.slice_order = order;
+            P.slice = 1;
+            if (int rc = launch_t<false>(P, stream)) return rc;
+            hipLaunchKernelGGL(fg_slice_order_kernel, dim3(1), dim3(1024), 0, stream, state, keys, P0.nq, order);
+            FG_HIP(hipGetLastError(), "order kernel launch");
+            P.slice = 2;
+            if (int rc = launch_t<false>(P, stream)) return rc;
+            FG_HIP(hipEventRecord(ix->slice_done, stream), "event record");
+            ix->slice_pending = true;
+            return FG_OK;
+        }
+    }
+    return launch_t<false>(P0, stream);
+}
 
 bool rows_dup_free(const float *rows, uint64_t n, uint32_t degree, uint64_t nbr_off, uint64_t row_off) {
     std::vector<uint32_t> tmp(degree);
@@ -2862,6 +3096,11 @@ void fg_index_destroy(fg_index *ix) {
     if (ix->d_q) (void)hipFree(ix->d_q);
     if (ix->d_res) (void)hipFree(ix->d_res);
     if (ix->d_cnt) (void)hipFree(ix->d_cnt);
+    if (ix->slice_done) {
+        (void)hipEventSynchronize(ix->slice_done);
+        (void)hipEventDestroy(ix->slice_done);
+    }
+    if (ix->d_slice) (void)hipFree(ix->d_slice);
     if (ix->ev0) (void)hipEventDestroy(ix->ev0);
     if (ix->ev1) (void)hipEventDestroy(ix->ev1);
     for (int i = 0; i < ix->serve_count; ++i) {
@@ -2898,7 +3137,7 @@ int fg_search_device(fg_index *ix, const float *d_queries, uint32_t nq, uint32_t
     P.results = d_results;
     P.counters = d_counters;
     P.phase = nullptr;
-    return launch(ix, P, reinterpret_cast<hipStream_t>(stream));
+    return launch(ix, P, reinterpret_cast<hipStream_t>(stream), true);
 }
 
 int fg_search_stream(fg_index *ix, const float *d_queries, uint32_t nq, uint32_t K, uint32_t beam,
@@ -2936,7 +3175,7 @@ int fg_search_stream(fg_index *ix, const float *d_queries, uint32_t nq, uint32_t
         Pb.results = d_results + q0 * K;
         Pb.counters = nullptr;
         Pb.phase = nullptr;
-        if (int rc = launch(ix, Pb, ix->serve[b % nstreams])) return rc;
+        if (int rc = launch(ix, Pb, ix->serve[b % nstreams], false)) return rc;
     }
     // and the caller's later work runs after every batch
     for (uint32_t i = 0; i < used; ++i) {
@@ -2967,7 +3206,7 @@ namespace {
 // into `dq`, the kernel runs on the null stream, and the ids (and counters)
 // are copied back from `dres` (`dcnt`).
 int search_host(fg_index *ix, SearchParams &P, const float *queries, uint32_t nq, uint32_t K, uint32_t *result_ids,
-                uint32_t *counters, fg_stats *stats, float *dq, uint32_t *dres, uint32_t *dcnt) {
+                uint32_t *counters, fg_stats *stats, float *dq, uint32_t *dres, uint32_t *dcnt, bool may_slice) {
     const size_t qb = static_cast<size_t>(nq) * ix->dim * sizeof(float);
     const size_t rb = static_cast<size_t>(nq) * K * sizeof(uint32_t);
     const size_t cb = static_cast<size_t>(nq) * FG_COUNTERS_PER_QUERY * sizeof(uint32_t);
@@ -2979,7 +3218,7 @@ int search_host(fg_index *ix, SearchParams &P, const float *queries, uint32_t nq
     P.phase = nullptr;
     const auto t0 = std::chrono::high_resolution_clock::now();
     FG_HIP(hipEventRecord(ix->ev0, nullptr), "event record");
-    if (int rc = launch(ix, P, nullptr)) return rc;
+    if (int rc = launch(ix, P, nullptr, may_slice)) return rc;
     FG_HIP(hipEventRecord(ix->ev1, nullptr), "event record");
     FG_HIP(hipDeviceSynchronize(), "search kernel");
     const auto t1 = std::chrono::high_resolution_clock::now();
@@ -3023,7 +3262,7 @@ int fg_search(fg_index *ix, const float *queries, uint32_t nq, uint32_t K, uint3
     if (int rc = ensure(reinterpret_cast<void **>(&ix->d_res), &ix->res_cap, rb)) return rc;
     if (counters)
         if (int rc = ensure(reinterpret_cast<void **>(&ix->d_cnt), &ix->cnt_cap, cb)) return rc;
-    return search_host(ix, P, queries, nq, K, result_ids, counters, stats, ix->d_q, ix->d_res, ix->d_cnt);
+    return search_host(ix, P, queries, nq, K, result_ids, counters, stats, ix->d_q, ix->d_res, ix->d_cnt, true);
 }
 
 int fg_search_noalloc(fg_index *ix, const float *queries, uint32_t nq, uint32_t K, uint32_t beam,
@@ -3041,8 +3280,9 @@ int fg_search_noalloc(fg_index *ix, const float *queries, uint32_t nq, uint32_t 
                                    std::to_string(FG_NOALLOC_STAGING_BYTES) + " (use fewer queries per call)");
     if (!ix->noalloc) return fail(FG_EDEVICE, "fg_search_noalloc: staging area not set up");
     unsigned char *base = ix->noalloc;
+    // (one launch: the two-launch search keeps its state in memory the index allocates)
     return search_host(ix, P, queries, nq, K, result_ids, counters, stats, reinterpret_cast<float *>(base),
-                       reinterpret_cast<uint32_t *>(base + qb), reinterpret_cast<uint32_t *>(base + qb + rb));
+                       reinterpret_cast<uint32_t *>(base + qb), reinterpret_cast<uint32_t *>(base + qb + rb), false);
 }
 
 int fg_query_prepare(fg_index *ix, const float *queries, uint32_t nq, float *rotated, uint8_t *quantized,

@@ -346,3 +346,54 @@ def test_search_waves_reports_the_form(gpu_available, monkeypatch):
     monkeypatch.setenv("FLASHGANN_TEAM", "1")
     assert ix.search_waves(100000, 10, 64) == 2
     ix.close()
+
+
+@pytest.mark.parametrize("dim,degree,kind,K,beam", [(128, 32, "int", 100, 256), (128, 32, "int", 10, 64),
+                                                    (96, 16, "unit", 100, 200), (96, 32, "unit", 10, 32),
+                                                    (40, 8, "int", 10, 128)])
+def test_two_launch_search_equals_one_launch(gpu_available, monkeypatch, dim, degree, kind, K, beam):
+    """The two-launch search (every query suspended at the top of iteration
+    15 with its beam, candidates, controller and counters kept in HBM, then
+    resumed in an order of its own) returns the ids and work counters of the
+    one-launch search and of the oracle, with and without counters."""
+    from flashgann_amd import Index
+    from oracle import oracle as O
+    cb, q, _ = small_index(n=3000, nq=300, dim=dim, degree=degree, kind=kind, comps=16)
+    ix = Index.from_codebook(cb)
+    monkeypatch.setenv("FLASHGANN_TEAM", "0")
+    monkeypatch.setenv("FLASHGANN_SLICE", "0")
+    ids1, _, cnt1 = ix.search(q, K, beam, counters=True)
+    monkeypatch.setenv("FLASHGANN_SLICE", "1")
+    ids2, _, cnt2 = ix.search(q, K, beam, counters=True)
+    ids3, _, _ = ix.search(q, K, beam)
+    ix.close()
+    assert (cnt1[:, 0] > 15).any()  # some queries are suspended and resumed
+    assert np.array_equal(ids2, ids1) and np.array_equal(cnt2, cnt1)
+    assert np.array_equal(ids3, ids1)
+    rids, rcnt = O.OracleIndex.from_codebook(cb).search(q, K, beam)
+    assert np.array_equal(ids2, rids)
+    assert np.array_equal(cnt2, rcnt.view(np.uint32).reshape(-1, 6))
+
+
+def test_two_launch_search_device_back_to_back(gpu_available, monkeypatch):
+    """Sliced device searches on one stream reuse the index's state buffer one
+    after another; a second index is independent; results equal fg_search's."""
+    import torch
+    from flashgann_amd import Index
+    cb, q, _ = small_index(n=3000, nq=300)
+    monkeypatch.setenv("FLASHGANN_TEAM", "0")
+    monkeypatch.setenv("FLASHGANN_SLICE", "0")
+    a = Index.from_codebook(cb)
+    ref = {b: a.search(q, 100, b)[0] for b in (128, 256)}
+    monkeypatch.setenv("FLASHGANN_SLICE", "1")
+    dq = torch.as_tensor(q, device="cuda")
+    s = torch.cuda.current_stream()
+    outs = []
+    for b in (256, 128, 256):
+        out = torch.full((q.shape[0], 100), -1, dtype=torch.int32, device="cuda")
+        a.search_device(dq.data_ptr(), q.shape[0], 100, b, out.data_ptr(), 0, s.cuda_stream)
+        outs.append((b, out))
+    torch.cuda.synchronize()
+    for b, out in outs:
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), ref[b]), b
+    a.close()
