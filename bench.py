@@ -469,7 +469,8 @@ def main() -> int:
                    "beam": chosen, "recall": round(float(recall), 5), "beam_sweep": sweep,
                    "host_buffers_qps": round(host_qps, 1), "work_per_query": work, "serving": serving,
                    "lds_bytes": fg.lds_bytes(dim, chosen, args.degree),
-                   "waves_per_query": index.search_waves(args.nq, args.K, chosen), "graph": graph_desc,
+                   "waves_per_query": index.search_waves(args.nq, args.K, chosen),
+                   "launches_per_search": index.search_launches(args.nq, args.K, chosen), "graph": graph_desc,
                    "rng_graph": rng_graph},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,

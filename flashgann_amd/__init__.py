@@ -135,6 +135,15 @@ class Index:
         check(w if w < 0 else 0)
         return w
 
+    def search_launches(self, nq: int, K: int, beam: int) -> int:
+        """Kernel launches (1, or 2 for the two-launch schedule: every query
+        to iteration 15, then the unfinished ones resumed longest-expected
+        first) that a search of nq queries at this K and beam makes
+        (fg_search_launches)."""
+        n = lib().fg_search_launches(self._h, nq, K, beam)
+        check(n if n < 0 else 0)
+        return n
+
     def search_stream(self, queries_ptr: int, nq: int, K: int, beam: int, results_ptr: int,
                       batch: int, nstreams: int = 2, stream: int = 0) -> None:
         """Device pointers; the nq queries searched as batches of `batch` on

@@ -3009,6 +3009,16 @@ int fg_search_waves(fg_index *ix, uint32_t nq, uint32_t K, uint32_t beam) {
     return waves;
 }
 
+int fg_search_launches(fg_index *ix, uint32_t nq, uint32_t K, uint32_t beam) {
+    if (!ix) return fail(FG_EINVAL, "index is NULL");
+    SearchParams P;
+    if (int rc = make_params(ix, nq, K, beam, P)) return rc;
+    if (!slice_wanted(P)) return 1;
+    int waves = 1;
+    if (int rc = launch_t<false>(P, nullptr, &waves)) return rc;
+    return waves == 1 ? 2 : 1;
+}
+
 int fg_index_create(const float *rows, uint64_t npoints, uint32_t dim, uint32_t degree, const float *signs,
                     uint32_t entry, int metric, fg_index **out) {
     if (!out) return fail(FG_EINVAL, "out is NULL");

@@ -164,6 +164,21 @@ uint32_t fg_lds_bytes(uint32_t dim, uint32_t beam, uint32_t degree);
  * warp-per-parent block shape). */
 int fg_search_waves(fg_index *index, uint32_t nq, uint32_t K, uint32_t beam);
 
+/* Kernel launches (1 or 2) that fg_search / fg_search_device make for a
+ * search of nq queries at this K and beam.  Two when the batch fills the
+ * device in the one-wave form (at least 4,096 and at most 16,384 queries,
+ * beam up to 256, L2 metric): every query first runs to iteration 15 and an
+ * unfinished one keeps its state in memory the index holds, then the
+ * unfinished queries resume in a second launch, those with the largest best
+ * distance so far first, so the longest searches start early.  Results are
+ * identical either way; FLASHGANN_SLICE=0/1 in the environment forces one
+ * launch / two wherever the form allows.  Device searches on one index that
+ * overlap on different streams run one after another when they take two
+ * launches.  fg_search_stream and fg_search_noalloc always make one.
+ * Negative FG_E* on invalid arguments.  No counterpart in the reference (one
+ * launch per call, gpu_search_adaptive.cu:99-103). */
+int fg_search_launches(fg_index *index, uint32_t nq, uint32_t K, uint32_t beam);
+
 /* Query preparation only (utils.cuh:840-939): rotated query (padded_dim
  * float32), quantized levels (padded_dim uint8), and {low, high, width} plus
  * sum_q, for nq host queries.  Test hook for the preparation stage. */
