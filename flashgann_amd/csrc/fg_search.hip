@@ -2464,32 +2464,35 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
 // slice_state[0] and the queries to order[0 .. count).
 __global__ __launch_bounds__(1024) void fg_slice_order_kernel(uint32_t *state, const uint32_t *keys, int nq,
                                                              uint32_t *order) {
-    __shared__ uint16_t qb[kSliceMaxQueries];  // each query's bin (0xFFFF: finished)
+    constexpr int kPerThread = kSliceMaxQueries / 1024;
     __shared__ uint32_t hist[kSliceBins];
     __shared__ uint32_t part[1024];
     __shared__ uint32_t kmax;
     const int t = static_cast<int>(threadIdx.x);
     for (int b = t; b < kSliceBins; b += 1024) hist[b] = 0u;
     if (t == 0) kmax = 0u;
-    __syncthreads();
-    uint32_t m = 0u;
-    for (int q = t; q < nq; q += 1024) {
-        const uint32_t v = keys[q];
-        if (v != kSliceDone) m = max(m, v);
+    // every key this thread handles, loaded at once (query t + 1024 j)
+    uint32_t v[kPerThread];
+#pragma unroll
+    for (int j = 0; j < kPerThread; ++j) {
+        const int q = t + 1024 * j;
+        v[j] = q < nq ? keys[q] : kSliceDone;
     }
+    uint32_t m = 0u;
+#pragma unroll
+    for (int j = 0; j < kPerThread; ++j) m = v[j] != kSliceDone ? max(m, v[j]) : m;
+    __syncthreads();
     atomicMax(&kmax, m);
     __syncthreads();
     const float top = __uint_as_float(kmax);
     const float scale = top > 0.0f ? static_cast<float>(kSliceBins - 1) / top : 0.0f;
-    for (int q = t; q < nq; q += 1024) {
-        const uint32_t v = keys[q];
-        uint32_t b = 0xFFFFu;
-        if (v != kSliceDone) {
-            const int x = static_cast<int>(__uint_as_float(v) * scale);
-            b = static_cast<uint32_t>(kSliceBins - 1 - min(max(x, 0), kSliceBins - 1));  // largest key first
-            atomicAdd(&hist[b], 1u);
+#pragma unroll
+    for (int j = 0; j < kPerThread; ++j) {
+        if (v[j] != kSliceDone) {
+            const int x = static_cast<int>(__uint_as_float(v[j]) * scale);
+            v[j] = static_cast<uint32_t>(kSliceBins - 1 - min(max(x, 0), kSliceBins - 1));  // largest key first
+            atomicAdd(&hist[v[j]], 1u);
         }
-        qb[q] = static_cast<uint16_t>(b);
     }
     __syncthreads();
     // exclusive scan: four bins per thread, then the 1024 partial sums
@@ -2502,19 +2505,18 @@ __global__ __launch_bounds__(1024) void fg_slice_order_kernel(uint32_t *state, c
     part[t] = sum;
     __syncthreads();
     for (int off = 1; off < 1024; off <<= 1) {
-        const uint32_t v = t >= off ? part[t - off] : 0u;
+        const uint32_t x = t >= off ? part[t - off] : 0u;
         __syncthreads();
-        part[t] += v;
+        part[t] += x;
         __syncthreads();
     }
     const uint32_t base = part[t] - sum;
     for (int j = 0; j < kPer; ++j) hist[t * kPer + j] = base + loc[j];
     if (t == 1023) state[0] = part[1023];
     __syncthreads();
-    for (int q = t; q < nq; q += 1024) {
-        const uint32_t b = qb[q];
-        if (b != 0xFFFFu) order[atomicAdd(&hist[b], 1u)] = static_cast<uint32_t>(q);
-    }
+#pragma unroll
+    for (int j = 0; j < kPerThread; ++j)
+        if (v[j] != kSliceDone) order[atomicAdd(&hist[v[j]], 1u)] = static_cast<uint32_t>(t + 1024 * j);
 }
 
 // ------------------------------------------------------------ test-hook kernels
