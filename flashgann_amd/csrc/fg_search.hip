@@ -267,12 +267,13 @@ struct SearchParams {
     int team;         // host only: the team form (two waves per query) may run
     uint32_t entry;
     int nq;
-    // Two-launch search (one-wave form, beams up to 256): slice 1 runs every
-    // query to the top of iteration slice_stop and keeps an unfinished
-    // query's state in slice_state; slice 2 resumes the queries slice_order
-    // lists (longest expected first), the first slice_state[0] of them.
-    int slice = 0;  // 0: one launch; 1: first slice; 2: second slice
-    int slice_stop = 0;
+    // Sliced search (one-wave form, beams up to 256): a slice that suspends
+    // runs its queries to the top of iteration slice_suspend and keeps an
+    // unfinished query's state in slice_state; a slice that resumes runs the
+    // queries slice_order lists (longest expected first), the first
+    // slice_state[0] of them, from iteration slice_resume.
+    int slice_suspend = 0;  // > 0: an unfinished query stops at the top of this iteration and keeps its state
+    int slice_resume = 0;   // > 0: resume the ordered queries at this iteration
     uint32_t *slice_state = nullptr;        // kSliceHeader words, then slice_words(pbeam) per query
     uint32_t *slice_keys = nullptr;         // per query: ordering key, or kSliceDone
     const uint32_t *slice_order = nullptr;  // second slice: query of each workgroup
@@ -1688,7 +1689,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
     // the two-launch search runs in the one-wave form at beams up to 256
     constexpr bool kSliceable = NW == 1 && !BIG && !PROF;
     if constexpr (kSliceable) {
-        if (P.slice == 2) {
+        if (P.slice_resume > 0) {
             // workgroup w resumes the w-th query of the order, if there is one
             const uint32_t n = __builtin_amdgcn_readfirstlane(P.slice_state[0]);
             if (static_cast<uint32_t>(qid) >= n) return;
@@ -1832,8 +1833,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
     int iter = 0;
     bool suspended = false;
     if constexpr (kSliceable) {
-        if (P.slice == 2) {
-            // resume at the top of iteration slice_stop (before its visited-table
+        if (P.slice_resume > 0) {
+            // resume at the top of iteration slice_resume (before its visited-table
             // rebuild, which derives the table from the beam): the beam, the
             // unmerged candidates, the controller and the counters as the first
             // slice left them.  Ids are checked so that no later row read can
@@ -1864,7 +1865,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
             c_st2 = uni(st[16]);
             cand_span = clamp_i(static_cast<int>(uni(st[17])), 0, kBufferBound);
             split_fast = uni(st[18]) != 0u;
-            iter = P.slice_stop;
+            iter = P.slice_resume;
             lead_sync<NW>();
         }
     }
@@ -1872,7 +1873,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
     FG_PHASE(0);
     for (; iter < kMaxIterations; ++iter) {
         if constexpr (kSliceable) {
-            if (P.slice == 1 && iter == P.slice_stop) {
+            if (P.slice_suspend > 0 && iter == P.slice_suspend) {
                 suspended = true;
                 break;
             }
@@ -2393,16 +2394,17 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
         }
     }
     if constexpr (kSliceable) {
-        if (P.slice == 1) {
+        if (P.slice_suspend > 0) {
             uint32_t *st = P.slice_state + kSliceHeader + static_cast<uint64_t>(qid) * slice_words(pbeam);
             if (suspended) {
-                // the state the second slice resumes from; the ordering key is
-                // the best distance found so far (the larger, the longer the
-                // rest of the search tends to run)
+                // the state the next slice resumes from; the ordering key is the
+                // best distance found so far (the larger, the longer the rest of
+                // the search tends to run)
                 uint2 *sb = reinterpret_cast<uint2 *>(st + kSliceFixed);
+                const float kd = pair_key(bp[0]);
                 for (int i = lane; i < pbeam + 32; i += 64) sb[i] = i < pbeam ? bp[i] : ms[i - pbeam];
                 if (lane == 0) {
-                    const uint32_t key = __float_as_uint(fmaxf(pair_key(bp[0]), 0.0f));
+                    const uint32_t key = __float_as_uint(fminf(fmaxf(kd, 0.0f), FLT_MAX));
                     P.slice_keys[qid] = key;
                     st[0] = 1u;
                     st[1] = key;
@@ -2426,7 +2428,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
                 }
                 return;
             }
-            if (lane == 0) P.slice_keys[qid] = kSliceDone;  // finished within the first slice
+            if (lane == 0) P.slice_keys[qid] = kSliceDone;  // finished within this slice
         }
     }
     // the loop ran out at kMaxIterations: the last iteration's exact-scored
@@ -2828,8 +2830,8 @@ int make_params(fg_index *ix, uint32_t nq, uint32_t K, uint32_t beam, SearchPara
     P.runtime_geo = ix->runtime_geo || ix->npoints * ix->row_offset * 4ull > 0xFFFFFFFFull ? 1 : 0;
     P.entry = ix->entry;
     P.nq = static_cast<int>(nq);
-    P.slice = 0;
-    P.slice_stop = 0;
+    P.slice_suspend = 0;
+    P.slice_resume = 0;
     P.slice_state = nullptr;
     P.slice_keys = nullptr;
     P.slice_order = nullptr;
@@ -2958,15 +2960,18 @@ int launch(fg_index *ix, const SearchParams &P0, hipStream_t stream, bool may_sl
             if (ix->slice_pending) FG_HIP(hipStreamWaitEvent(stream, ix->slice_done, 0), "stream wait");
             uint32_t *state = ix->d_slice, *keys = state + kSliceHeader + states, *order = keys + pad;
             SearchParams P = P0;
-            P.slice_stop = kSliceStop;
             P.slice_state = state;
             P.slice_keys = keys;
             P.slice_order = order;
-            P.slice = 1;
+            // (a third slice, suspending again at iteration 31 and reordering by
+            // the K-th cutoff, measured 4-10% slower than two)
+            P.slice_suspend = kSliceStop;
+            P.slice_resume = 0;
             if (int rc = launch_t<false>(P, stream)) return rc;
             hipLaunchKernelGGL(fg_slice_order_kernel, dim3(1), dim3(1024), 0, stream, state, keys, P0.nq, order);
             FG_HIP(hipGetLastError(), "order kernel launch");
-            P.slice = 2;
+            P.slice_resume = kSliceStop;
+            P.slice_suspend = 0;
             if (int rc = launch_t<false>(P, stream)) return rc;
             FG_HIP(hipEventRecord(ix->slice_done, stream), "event record");
             ix->slice_pending = true;
