@@ -267,7 +267,7 @@ struct SearchParams {
     int team;         // host only: the team form (two waves per query) may run
     uint32_t entry;
     int nq;
-    // Sliced search (one-wave form, beams up to 256): a slice that suspends
+    // Sliced search (one-wave form): a slice that suspends
     // runs its queries to the top of iteration slice_suspend and keeps an
     // unfinished query's state in slice_state; a slice that resumes runs the
     // queries slice_order lists (longest expected first), the first
@@ -283,12 +283,13 @@ struct SearchParams {
 // Per-query state of a suspended search, in 32-bit words after a header of
 // kSliceHeader words (word 0: the number of suspended queries, set by the
 // order kernel).  Per query: a mark (1), the ordering key, the controller (9
-// words), the work counters (6), the candidate span and the split flag, then
+// words), the work counters (6), the candidate span, the split flag and the
+// pick's start (beams over 256), then
 // the pbeam beam pairs and the 32 candidate pairs.  slice_keys holds the
 // key (bits of a non-negative distance) of each suspended query and
 // kSliceDone for a query the first slice finished.
 constexpr uint32_t kSliceHeader = 64;
-constexpr uint32_t kSliceFixed = 20;  // 2 + 9 + 6 + 2, padded to keep the pairs 8-byte aligned
+constexpr uint32_t kSliceFixed = 20;  // 2 + 9 + 6 + 2 + 1 (the pick's start, beams over 256)
 __host__ __device__ inline uint32_t slice_words(uint32_t pbeam) { return kSliceFixed + 2u * (pbeam + 32u); }
 constexpr uint32_t kSliceDone = 0xFFFFFFFFu;
 constexpr int kSliceMaxQueries = 16384;  // the order kernel holds every query's bin in LDS
@@ -1686,8 +1687,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
     extern __shared__ __align__(16) unsigned char smem[];
     int qid = blockIdx.x;
     if (qid >= P.nq) return;
-    // the two-launch search runs in the one-wave form at beams up to 256
-    constexpr bool kSliceable = NW == 1 && !BIG && !PROF;
+    // the two-launch search runs in the one-wave form
+    constexpr bool kSliceable = NW == 1 && !PROF;
     if constexpr (kSliceable) {
         if (P.slice_resume > 0) {
             // workgroup w resumes the w-th query of the order, if there is one
@@ -1865,6 +1866,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
             c_st2 = uni(st[16]);
             cand_span = clamp_i(static_cast<int>(uni(st[17])), 0, kBufferBound);
             split_fast = uni(st[18]) != 0u;
+            scan_from = clamp_i(static_cast<int>(uni(st[19])), 0, beam_sz);
             iter = P.slice_resume;
             lead_sync<NW>();
         }
@@ -2425,6 +2427,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
                     st[16] = c_st2;
                     st[17] = static_cast<uint32_t>(cand_span);
                     st[18] = split_fast ? 1u : 0u;
+                    st[19] = static_cast<uint32_t>(scan_from);
                 }
                 return;
             }
@@ -2930,13 +2933,13 @@ int launch_t(const SearchParams &P, hipStream_t stream, int *waves_only = nullpt
 }
 
 // Whether a search runs as two launches (first slice, order, second slice):
-// the one-wave form at beams up to 256 with the L2 metric, a batch that
+// the one-wave form with the L2 metric, a batch that
 // fills the device (the last queries to start are the ones that make a
 // launch's tail) and fits the order kernel.  FLASHGANN_SLICE=0 / 1 forces
 // one launch / two launches wherever the form allows them (tests run both).
 constexpr int kSliceStop = 15;  // the top of the first iteration that rebuilds the visited table
 bool slice_wanted(const SearchParams &P) {
-    if (P.nq < 1 || P.nq > kSliceMaxQueries || P.pbeam > 256 || P.max_iter <= kSliceStop || P.use_ip) return false;
+    if (P.nq < 1 || P.nq > kSliceMaxQueries || P.max_iter <= kSliceStop || P.use_ip) return false;
     if (const char *e = std::getenv("FLASHGANN_SLICE")) {
         if (e[0] == '0') return false;
         if (e[0] == '1') return true;

@@ -167,7 +167,7 @@ int fg_search_waves(fg_index *index, uint32_t nq, uint32_t K, uint32_t beam);
 /* Kernel launches (1 or 2) that fg_search / fg_search_device make for a
  * search of nq queries at this K and beam.  Two when the batch fills the
  * device in the one-wave form (at least 4,096 and at most 16,384 queries,
- * beam up to 256, L2 metric): every query first runs to iteration 15 and an
+ * L2 metric): every query first runs to iteration 15 and an
  * unfinished one keeps its state in memory the index holds, then the
  * unfinished queries resume in a second launch, those with the largest best
  * distance so far first, so the longest searches start early.  Results are

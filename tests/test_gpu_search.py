@@ -350,7 +350,9 @@ def test_search_waves_reports_the_form(gpu_available, monkeypatch):
 
 @pytest.mark.parametrize("dim,degree,kind,K,beam", [(128, 32, "int", 100, 256), (128, 32, "int", 10, 64),
                                                     (96, 16, "unit", 100, 200), (96, 32, "unit", 10, 32),
-                                                    (40, 8, "int", 10, 128)])
+                                                    (40, 8, "int", 10, 128), (128, 32, "int", 100, 512),
+                                                    (96, 16, "unit", 100, 384), (128, 32, "int", 100, 1000),
+                                                    (960, 32, "box", 100, 384)])
 def test_two_launch_search_equals_one_launch(gpu_available, monkeypatch, dim, degree, kind, K, beam):
     """The two-launch search (every query suspended at the top of iteration
     15 with its beam, candidates, controller and counters kept in HBM, then
