@@ -2948,6 +2948,11 @@ bool slice_wanted(const SearchParams &P) {
 }
 
 int launch(fg_index *ix, const SearchParams &P0, hipStream_t stream, bool may_slice) {
+    // a stream being captured into a graph gets one launch: the two-launch
+    // search may allocate its state buffer and orders itself with an event
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    if (may_slice && hipStreamIsCapturing(stream, &capture) == hipSuccess && capture != hipStreamCaptureStatusNone)
+        may_slice = false;
     if (may_slice && slice_wanted(P0)) {
         int waves = 0;
         if (int rc = launch_t<false>(P0, stream, &waves)) return rc;

@@ -174,7 +174,8 @@ int fg_search_waves(fg_index *index, uint32_t nq, uint32_t K, uint32_t beam);
  * identical either way; FLASHGANN_SLICE=0/1 in the environment forces one
  * launch / two wherever the form allows.  Device searches on one index that
  * overlap on different streams run one after another when they take two
- * launches.  fg_search_stream and fg_search_noalloc always make one.
+ * launches.  fg_search_stream, fg_search_noalloc and a device search on a
+ * stream that is being captured into a graph always make one.
  * Negative FG_E* on invalid arguments.  No counterpart in the reference (one
  * launch per call, gpu_search_adaptive.cu:99-103). */
 int fg_search_launches(fg_index *index, uint32_t nq, uint32_t K, uint32_t beam);

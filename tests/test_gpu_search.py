@@ -399,3 +399,30 @@ def test_two_launch_search_device_back_to_back(gpu_available, monkeypatch):
     for b, out in outs:
         assert np.array_equal(out.cpu().numpy().view(np.uint32), ref[b]), b
     a.close()
+
+
+def test_device_search_captured_in_a_graph(gpu_available, monkeypatch):
+    """A device search on a stream that is being captured makes one launch
+    (the two-launch search would allocate and order itself with an event);
+    every replay, with eager work between replays, returns the eager ids."""
+    import torch
+    from flashgann_amd import Index
+    cb, q, _ = small_index(n=3000, nq=300)
+    monkeypatch.setenv("FLASHGANN_TEAM", "0")
+    monkeypatch.setenv("FLASHGANN_SLICE", "1")
+    ix = Index.from_codebook(cb)
+    ref, _, _ = ix.search(q, 100, 256)
+    dq = torch.as_tensor(q, device="cuda")
+    out = torch.full((q.shape[0], 100), -1, dtype=torch.int32, device="cuda")
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        ix.search_device(dq.data_ptr(), q.shape[0], 100, 256, out.data_ptr(), 0, s.cuda_stream)
+    for _ in range(3):
+        out.fill_(-1)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), ref)
+    del g
+    ix.close()
