@@ -2657,6 +2657,7 @@ struct fg_index {
     size_t slice_cap = 0;
     hipEvent_t slice_done = nullptr;
     bool slice_pending = false;
+    hipStream_t slice_stream = nullptr;  // the stream of the last sliced search
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     // this device's staging area of fg_search_noalloc (device address)
     unsigned char *noalloc = nullptr;
@@ -2863,10 +2864,10 @@ inline bool use_team(const SearchParams &P, const void *one_wave_kernel) {
 }
 
 template <int WT, int DPL, int DIM_T, int DEG_T, bool BIG>
-void launch_geo_b(const SearchParams &P, hipStream_t stream, bool count, bool prof, int *waves_only) {
+void launch_geo_b(const SearchParams &P, hipStream_t stream, bool count, bool prof, int *waves_only, bool one_wave) {
     const dim3 grid(P.nq), block(64);
-    const bool team = use_team(P, reinterpret_cast<const void *>(
-                                      &fg_search_kernel<WT, DPL, DIM_T, DEG_T, false, false, BIG, 1>));
+    const bool team = !one_wave && use_team(P, reinterpret_cast<const void *>(
+                                                   &fg_search_kernel<WT, DPL, DIM_T, DEG_T, false, false, BIG, 1>));
     if (waves_only) {  // the form only, no launch
         *waves_only = team ? 2 : 1;
         return;
@@ -2898,34 +2899,36 @@ void launch_geo_b(const SearchParams &P, hipStream_t stream, bool count, bool pr
 // Beams over 256 (two or more merge-path segments per lane, the pick's wide
 // scan) and smaller ones run separately compiled kernels.
 template <int WT, int DPL, int DIM_T, int DEG_T>
-void launch_geo(const SearchParams &P, hipStream_t stream, bool count, bool prof, int *waves_only) {
-    if (P.pbeam > 256) launch_geo_b<WT, DPL, DIM_T, DEG_T, true>(P, stream, count, prof, waves_only);
-    else launch_geo_b<WT, DPL, DIM_T, DEG_T, false>(P, stream, count, prof, waves_only);
+void launch_geo(const SearchParams &P, hipStream_t stream, bool count, bool prof, int *waves_only, bool one_wave) {
+    if (P.pbeam > 256) launch_geo_b<WT, DPL, DIM_T, DEG_T, true>(P, stream, count, prof, waves_only, one_wave);
+    else launch_geo_b<WT, DPL, DIM_T, DEG_T, false>(P, stream, count, prof, waves_only, one_wave);
 }
 
 // Shape classes: the benchmark shapes (d 128 / deg 32; d 96 / deg 32 and 16)
 // get fully compile-time geometry while the codebook is under 4 GiB; other
 // shapes and larger codebooks use runtime offsets.
+// one_wave: the one-wave form without asking the occupancy rule again (the
+// slices of a search whose form is already known)
 template <bool PROF>
-int launch_t(const SearchParams &P, hipStream_t stream, int *waves_only = nullptr) {
+int launch_t(const SearchParams &P, hipStream_t stream, int *waves_only = nullptr, bool one_wave = false) {
     if (P.nq == 0 && !waves_only) return FG_OK;
     const bool count = P.counters != nullptr;
     const int W = P.padded_dim / 32;
     const bool fixed = !P.runtime_geo;
     if (fixed && P.dim == 128 && P.degree == 32) {
-        launch_geo<4, 4, 128, 32>(P, stream, count, PROF, waves_only);
+        launch_geo<4, 4, 128, 32>(P, stream, count, PROF, waves_only, one_wave);
     } else if (fixed && P.dim == 96 && P.degree == 32) {
-        launch_geo<4, 3, 96, 32>(P, stream, count, PROF, waves_only);
+        launch_geo<4, 3, 96, 32>(P, stream, count, PROF, waves_only, one_wave);
     } else if (fixed && P.dim == 96 && P.degree == 16) {
-        launch_geo<4, 3, 96, 16>(P, stream, count, PROF, waves_only);
+        launch_geo<4, 3, 96, 16>(P, stream, count, PROF, waves_only, one_wave);
     } else if (W == 2 && P.dim <= 64) {
-        launch_geo<2, 2, 0, 0>(P, stream, count, PROF, waves_only);
+        launch_geo<2, 2, 0, 0>(P, stream, count, PROF, waves_only, one_wave);
     } else if (W == 4 && P.dim <= 96) {
-        launch_geo<4, 3, 0, 0>(P, stream, count, PROF, waves_only);
+        launch_geo<4, 3, 0, 0>(P, stream, count, PROF, waves_only, one_wave);
     } else if (W == 4) {
-        launch_geo<4, 4, 0, 0>(P, stream, count, PROF, waves_only);
+        launch_geo<4, 4, 0, 0>(P, stream, count, PROF, waves_only, one_wave);
     } else {
-        launch_geo<0, 0, 0, 0>(P, stream, count, PROF, waves_only);
+        launch_geo<0, 0, 0, 0>(P, stream, count, PROF, waves_only, one_wave);
     }
     if (waves_only) return FG_OK;
     FG_HIP(hipGetLastError(), "search kernel launch");
@@ -2965,7 +2968,8 @@ int launch(fg_index *ix, const SearchParams &P0, hipStream_t stream, bool may_sl
             if (int rc = ensure(reinterpret_cast<void **>(&ix->d_slice), &ix->slice_cap, words * 4u)) return rc;
             if (!ix->slice_done) FG_HIP(hipEventCreateWithFlags(&ix->slice_done, hipEventDisableTiming), "event");
             // a sliced search on another stream may still use the buffer
-            if (ix->slice_pending) FG_HIP(hipStreamWaitEvent(stream, ix->slice_done, 0), "stream wait");
+            if (ix->slice_pending && ix->slice_stream != stream)
+                FG_HIP(hipStreamWaitEvent(stream, ix->slice_done, 0), "stream wait");
             uint32_t *state = ix->d_slice, *keys = state + kSliceHeader + states, *order = keys + pad;
             SearchParams P = P0;
             P.slice_state = state;
@@ -2975,14 +2979,15 @@ int launch(fg_index *ix, const SearchParams &P0, hipStream_t stream, bool may_sl
             // the K-th cutoff, measured 4-10% slower than two)
             P.slice_suspend = kSliceStop;
             P.slice_resume = 0;
-            if (int rc = launch_t<false>(P, stream)) return rc;
+            if (int rc = launch_t<false>(P, stream, nullptr, true)) return rc;
             hipLaunchKernelGGL(fg_slice_order_kernel, dim3(1), dim3(1024), 0, stream, state, keys, P0.nq, order);
             FG_HIP(hipGetLastError(), "order kernel launch");
             P.slice_resume = kSliceStop;
             P.slice_suspend = 0;
-            if (int rc = launch_t<false>(P, stream)) return rc;
+            if (int rc = launch_t<false>(P, stream, nullptr, true)) return rc;
             FG_HIP(hipEventRecord(ix->slice_done, stream), "event record");
             ix->slice_pending = true;
+            ix->slice_stream = stream;
             return FG_OK;
         }
     }
