@@ -2849,6 +2849,15 @@ int make_params(fg_index *ix, uint32_t nq, uint32_t K, uint32_t beam, SearchPara
 // one-wave form's resident workgroups), a second wave per query costs no
 // query a slot and shortens every search.  FLASHGANN_TEAM=0 / 1 forces the
 // one-wave / team form (tests run both).
+// Workgroups of the one-wave kernel the device holds at once (0 if unknown).
+inline long long resident_one_wave(const SearchParams &P, const void *one_wave_kernel) {
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, one_wave_kernel, 64, P.lds.total) != hipSuccess) return 0;
+    return static_cast<long long>(per_cu) * cus;
+}
+
 inline bool use_team(const SearchParams &P, const void *one_wave_kernel) {
     if (!P.team) return false;
     if (const char *e = std::getenv("FLASHGANN_TEAM")) {
@@ -2864,12 +2873,14 @@ inline bool use_team(const SearchParams &P, const void *one_wave_kernel) {
 }
 
 template <int WT, int DPL, int DIM_T, int DEG_T, bool BIG>
-void launch_geo_b(const SearchParams &P, hipStream_t stream, bool count, bool prof, int *waves_only, bool one_wave) {
+void launch_geo_b(const SearchParams &P, hipStream_t stream, bool count, bool prof, int *waves_only, bool one_wave,
+                  long long *resident) {
     const dim3 grid(P.nq), block(64);
-    const bool team = !one_wave && use_team(P, reinterpret_cast<const void *>(
-                                                   &fg_search_kernel<WT, DPL, DIM_T, DEG_T, false, false, BIG, 1>));
+    const void *one = reinterpret_cast<const void *>(&fg_search_kernel<WT, DPL, DIM_T, DEG_T, false, false, BIG, 1>);
+    const bool team = !one_wave && use_team(P, one);
     if (waves_only) {  // the form only, no launch
         *waves_only = team ? 2 : 1;
+        if (resident) *resident = resident_one_wave(P, one);
         return;
     }
     if (team) {
@@ -2899,9 +2910,10 @@ void launch_geo_b(const SearchParams &P, hipStream_t stream, bool count, bool pr
 // Beams over 256 (two or more merge-path segments per lane, the pick's wide
 // scan) and smaller ones run separately compiled kernels.
 template <int WT, int DPL, int DIM_T, int DEG_T>
-void launch_geo(const SearchParams &P, hipStream_t stream, bool count, bool prof, int *waves_only, bool one_wave) {
-    if (P.pbeam > 256) launch_geo_b<WT, DPL, DIM_T, DEG_T, true>(P, stream, count, prof, waves_only, one_wave);
-    else launch_geo_b<WT, DPL, DIM_T, DEG_T, false>(P, stream, count, prof, waves_only, one_wave);
+void launch_geo(const SearchParams &P, hipStream_t stream, bool count, bool prof, int *waves_only, bool one_wave,
+                long long *resident) {
+    if (P.pbeam > 256) launch_geo_b<WT, DPL, DIM_T, DEG_T, true>(P, stream, count, prof, waves_only, one_wave, resident);
+    else launch_geo_b<WT, DPL, DIM_T, DEG_T, false>(P, stream, count, prof, waves_only, one_wave, resident);
 }
 
 // Shape classes: the benchmark shapes (d 128 / deg 32; d 96 / deg 32 and 16)
@@ -2909,45 +2921,56 @@ void launch_geo(const SearchParams &P, hipStream_t stream, bool count, bool prof
 // shapes and larger codebooks use runtime offsets.
 // one_wave: the one-wave form without asking the occupancy rule again (the
 // slices of a search whose form is already known)
+// resident (with waves_only): the one-wave kernel's workgroups the device holds at once
 template <bool PROF>
-int launch_t(const SearchParams &P, hipStream_t stream, int *waves_only = nullptr, bool one_wave = false) {
+int launch_t(const SearchParams &P, hipStream_t stream, int *waves_only = nullptr, bool one_wave = false,
+             long long *resident = nullptr) {
     if (P.nq == 0 && !waves_only) return FG_OK;
     const bool count = P.counters != nullptr;
     const int W = P.padded_dim / 32;
     const bool fixed = !P.runtime_geo;
     if (fixed && P.dim == 128 && P.degree == 32) {
-        launch_geo<4, 4, 128, 32>(P, stream, count, PROF, waves_only, one_wave);
+        launch_geo<4, 4, 128, 32>(P, stream, count, PROF, waves_only, one_wave, resident);
     } else if (fixed && P.dim == 96 && P.degree == 32) {
-        launch_geo<4, 3, 96, 32>(P, stream, count, PROF, waves_only, one_wave);
+        launch_geo<4, 3, 96, 32>(P, stream, count, PROF, waves_only, one_wave, resident);
     } else if (fixed && P.dim == 96 && P.degree == 16) {
-        launch_geo<4, 3, 96, 16>(P, stream, count, PROF, waves_only, one_wave);
+        launch_geo<4, 3, 96, 16>(P, stream, count, PROF, waves_only, one_wave, resident);
     } else if (W == 2 && P.dim <= 64) {
-        launch_geo<2, 2, 0, 0>(P, stream, count, PROF, waves_only, one_wave);
+        launch_geo<2, 2, 0, 0>(P, stream, count, PROF, waves_only, one_wave, resident);
     } else if (W == 4 && P.dim <= 96) {
-        launch_geo<4, 3, 0, 0>(P, stream, count, PROF, waves_only, one_wave);
+        launch_geo<4, 3, 0, 0>(P, stream, count, PROF, waves_only, one_wave, resident);
     } else if (W == 4) {
-        launch_geo<4, 4, 0, 0>(P, stream, count, PROF, waves_only, one_wave);
+        launch_geo<4, 4, 0, 0>(P, stream, count, PROF, waves_only, one_wave, resident);
     } else {
-        launch_geo<0, 0, 0, 0>(P, stream, count, PROF, waves_only, one_wave);
+        launch_geo<0, 0, 0, 0>(P, stream, count, PROF, waves_only, one_wave, resident);
     }
     if (waves_only) return FG_OK;
     FG_HIP(hipGetLastError(), "search kernel launch");
     return FG_OK;
 }
 
-// Whether a search runs as two launches (first slice, order, second slice):
-// the one-wave form with the L2 metric, a batch that
-// fills the device (the last queries to start are the ones that make a
-// launch's tail) and fits the order kernel.  FLASHGANN_SLICE=0 / 1 forces
-// one launch / two launches wherever the form allows them (tests run both).
+// Whether a search may run as two launches (first slice, order, second
+// slice): the L2 metric, a batch the order kernel holds, and searches that
+// reach the suspension point.  slice_fits then asks for the one-wave form and
+// a batch larger than the device holds at once (the last queries to start
+// are the ones that make a launch's tail).  FLASHGANN_SLICE=0 / 1 forces one
+// launch / two launches wherever the form allows them (tests run both).
 constexpr int kSliceStop = 15;  // the top of the first iteration that rebuilds the visited table
 bool slice_wanted(const SearchParams &P) {
     if (P.nq < 1 || P.nq > kSliceMaxQueries || P.max_iter <= kSliceStop || P.use_ip) return false;
+    return true;
+}
+
+// slice_wanted's answer for a batch whose form is known: the one-wave form,
+// and more queries than the device holds at once (when every query starts
+// at once, there is no order to improve), or FLASHGANN_SLICE's answer.
+bool slice_fits(const SearchParams &P, int waves, long long resident) {
+    if (waves != 1) return false;
     if (const char *e = std::getenv("FLASHGANN_SLICE")) {
         if (e[0] == '0') return false;
         if (e[0] == '1') return true;
     }
-    return P.nq >= 4096;
+    return resident > 0 && static_cast<long long>(P.nq) > resident;
 }
 
 int launch(fg_index *ix, const SearchParams &P0, hipStream_t stream, bool may_slice) {
@@ -2958,8 +2981,9 @@ int launch(fg_index *ix, const SearchParams &P0, hipStream_t stream, bool may_sl
         may_slice = false;
     if (may_slice && slice_wanted(P0)) {
         int waves = 0;
-        if (int rc = launch_t<false>(P0, stream, &waves)) return rc;
-        if (waves == 1) {
+        long long resident = 0;
+        if (int rc = launch_t<false>(P0, stream, &waves, false, &resident)) return rc;
+        if (slice_fits(P0, waves, resident)) {
             // one buffer: header (word 0: the count of suspended queries), the
             // per-query states, the keys, the order
             const uint64_t nq = static_cast<uint64_t>(P0.nq), pad = (nq + 63u) & ~63ull;
@@ -3035,8 +3059,9 @@ int fg_search_launches(fg_index *ix, uint32_t nq, uint32_t K, uint32_t beam) {
     if (int rc = make_params(ix, nq, K, beam, P)) return rc;
     if (!slice_wanted(P)) return 1;
     int waves = 1;
-    if (int rc = launch_t<false>(P, nullptr, &waves)) return rc;
-    return waves == 1 ? 2 : 1;
+    long long resident = 0;
+    if (int rc = launch_t<false>(P, nullptr, &waves, false, &resident)) return rc;
+    return slice_fits(P, waves, resident) ? 2 : 1;
 }
 
 int fg_index_create(const float *rows, uint64_t npoints, uint32_t dim, uint32_t degree, const float *signs,

@@ -165,9 +165,10 @@ uint32_t fg_lds_bytes(uint32_t dim, uint32_t beam, uint32_t degree);
 int fg_search_waves(fg_index *index, uint32_t nq, uint32_t K, uint32_t beam);
 
 /* Kernel launches (1 or 2) that fg_search / fg_search_device make for a
- * search of nq queries at this K and beam.  Two when the batch fills the
- * device in the one-wave form (at least 4,096 and at most 16,384 queries,
- * L2 metric): every query first runs to iteration 15 and an
+ * search of nq queries at this K and beam.  Two when the batch, in the
+ * one-wave form, holds more queries than the device runs at once (6,144 at
+ * d 128, degree 32, beam 256) and at most 16,384, with the L2 metric: every
+ * query first runs to iteration 15 and an
  * unfinished one keeps its state in memory the index holds, then the
  * unfinished queries resume in a second launch, those with the largest best
  * distance so far first, so the longest searches start early.  Results are

@@ -426,3 +426,23 @@ def test_device_search_captured_in_a_graph(gpu_available, monkeypatch):
         assert np.array_equal(out.cpu().numpy().view(np.uint32), ref)
     del g
     ix.close()
+
+
+def test_search_launches_reports_the_schedule(gpu_available, monkeypatch):
+    """fg_search_launches: two launches for a one-wave batch larger than the
+    device holds at once (and at most 16,384 queries), one otherwise, and
+    the environment override wins where the form allows two."""
+    from flashgann_amd import Index
+    cb, q, _ = small_index()
+    ix = Index.from_codebook(cb)
+    monkeypatch.delenv("FLASHGANN_TEAM", raising=False)
+    monkeypatch.delenv("FLASHGANN_SLICE", raising=False)
+    assert ix.search_launches(10000, 100, 256) == 2   # 24 queries per CU x 256 CUs = 6,144 at once
+    assert ix.search_launches(5000, 100, 256) == 1    # every query starts at once
+    assert ix.search_launches(16, 10, 64) == 1        # the team form
+    assert ix.search_launches(20000, 100, 256) == 1   # above the order kernel's 16,384
+    monkeypatch.setenv("FLASHGANN_SLICE", "0")
+    assert ix.search_launches(10000, 100, 256) == 1
+    monkeypatch.setenv("FLASHGANN_SLICE", "1")
+    assert ix.search_launches(5000, 100, 256) == 2
+    ix.close()
