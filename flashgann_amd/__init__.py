@@ -144,6 +144,14 @@ class Index:
         check(n if n < 0 else 0)
         return n
 
+    def search_geometry(self) -> int:
+        """0 when the kernels specialised for this shape (32-bit row offsets)
+        serve searches on this index, 1 for the general kernels (runtime
+        offsets, 64-bit row addresses) (fg_search_geometry)."""
+        g = lib().fg_search_geometry(self._h)
+        check(g if g < 0 else 0)
+        return g
+
     def search_stream(self, queries_ptr: int, nq: int, K: int, beam: int, results_ptr: int,
                       batch: int, nstreams: int = 2, stream: int = 0) -> None:
         """Device pointers; the nq queries searched as batches of `batch` on

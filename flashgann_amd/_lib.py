@@ -24,7 +24,7 @@ FG_NOALLOC_STAGING_BYTES = 16 << 20
 
 EXPORTED = (
     "fg_index_create", "fg_index_load", "fg_index_destroy", "fg_index_get_info", "fg_search", "fg_search_noalloc",
-    "fg_search_device", "fg_search_stream", "fg_search_profile", "fg_lds_bytes", "fg_search_waves", "fg_search_launches", "fg_query_prepare", "fg_score_edges", "fg_last_error",
+    "fg_search_device", "fg_search_stream", "fg_search_profile", "fg_lds_bytes", "fg_search_waves", "fg_search_launches", "fg_search_geometry", "fg_query_prepare", "fg_score_edges", "fg_last_error",
     "fg_version",
 )
 
@@ -80,6 +80,8 @@ def lib():
         L.fg_search_waves.restype = C.c_int
         L.fg_search_launches.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32]
         L.fg_search_launches.restype = C.c_int
+        L.fg_search_geometry.argtypes = [C.c_void_p]
+        L.fg_search_geometry.restype = C.c_int
         L.fg_query_prepare.argtypes = [vp, f32p, C.c_uint32, f32p, u8p, f32p, i32p]
         L.fg_score_edges.argtypes = [vp, f32p, C.c_uint32, u32p, u32p, u32p, C.c_uint32, f32p,
                                      f32p, f32p]

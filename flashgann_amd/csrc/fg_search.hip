@@ -2767,6 +2767,20 @@ int ensure(void **p, size_t *cap, size_t need) {
     return FG_OK;
 }
 
+// Whether an index must use the general kernels: the fixed-geometry kernels
+// address rows with 32-bit byte offsets, so a codebook of 4 GiB or more (or
+// an index created with FG_FORCE_RUNTIME_GEOMETRY=1) takes runtime offsets
+// and 64-bit row addresses.
+inline bool index_runtime_geo(const fg_index *ix) {
+    return ix->runtime_geo || ix->npoints * ix->row_offset * 4ull > 0xFFFFFFFFull;
+}
+
+// The benchmark shapes that get compile-time geometry (d 128 / degree 32;
+// d 96 / degree 32 and 16) while 32-bit row offsets reach every row.
+inline bool fixed_geometry(int runtime_geo, int dim, int degree) {
+    return !runtime_geo && ((dim == 128 && degree == 32) || (dim == 96 && (degree == 32 || degree == 16)));
+}
+
 int make_params(fg_index *ix, uint32_t nq, uint32_t K, uint32_t beam, SearchParams &P) {
     if (K < 1) return fail(FG_EINVAL, "K must be >= 1");
     if (beam < 1 || beam > static_cast<uint32_t>(kMaxBeam))
@@ -2830,8 +2844,7 @@ int make_params(fg_index *ix, uint32_t nq, uint32_t K, uint32_t beam, SearchPara
     P.use_ip = ix->metric == FG_METRIC_IP ? 1 : 0;
     P.dup_free = ix->dup_free;
     P.vec_ok = (ix->row_offset % 4 == 0 && ix->code_offset % 4 == 0) ? 1 : 0;
-    // the fixed-geometry kernels address rows with 32-bit byte offsets
-    P.runtime_geo = ix->runtime_geo || ix->npoints * ix->row_offset * 4ull > 0xFFFFFFFFull ? 1 : 0;
+    P.runtime_geo = index_runtime_geo(ix) ? 1 : 0;
     P.entry = ix->entry;
     P.nq = static_cast<int>(nq);
     P.slice_suspend = 0;
@@ -2928,12 +2941,12 @@ int launch_t(const SearchParams &P, hipStream_t stream, int *waves_only = nullpt
     if (P.nq == 0 && !waves_only) return FG_OK;
     const bool count = P.counters != nullptr;
     const int W = P.padded_dim / 32;
-    const bool fixed = !P.runtime_geo;
-    if (fixed && P.dim == 128 && P.degree == 32) {
+    const bool fixed = fixed_geometry(P.runtime_geo, P.dim, P.degree);
+    if (fixed && P.dim == 128) {
         launch_geo<4, 4, 128, 32>(P, stream, count, PROF, waves_only, one_wave, resident);
-    } else if (fixed && P.dim == 96 && P.degree == 32) {
+    } else if (fixed && P.degree == 32) {
         launch_geo<4, 3, 96, 32>(P, stream, count, PROF, waves_only, one_wave, resident);
-    } else if (fixed && P.dim == 96 && P.degree == 16) {
+    } else if (fixed) {
         launch_geo<4, 3, 96, 16>(P, stream, count, PROF, waves_only, one_wave, resident);
     } else if (W == 2 && P.dim <= 64) {
         launch_geo<2, 2, 0, 0>(P, stream, count, PROF, waves_only, one_wave, resident);
@@ -3062,6 +3075,13 @@ int fg_search_launches(fg_index *ix, uint32_t nq, uint32_t K, uint32_t beam) {
     long long resident = 0;
     if (int rc = launch_t<false>(P, nullptr, &waves, false, &resident)) return rc;
     return slice_fits(P, waves, resident) ? 2 : 1;
+}
+
+int fg_search_geometry(const fg_index *ix) {
+    if (!ix) return fail(FG_EINVAL, "index is NULL");
+    const bool rt = index_runtime_geo(ix);
+    return fixed_geometry(rt ? 1 : 0, static_cast<int>(ix->dim), static_cast<int>(ix->degree)) ? FG_GEOMETRY_FIXED
+                                                                                                : FG_GEOMETRY_GENERAL;
 }
 
 int fg_index_create(const float *rows, uint64_t npoints, uint32_t dim, uint32_t degree, const float *signs,

@@ -181,6 +181,19 @@ int fg_search_waves(fg_index *index, uint32_t nq, uint32_t K, uint32_t beam);
  * launch per call, gpu_search_adaptive.cu:99-103). */
 int fg_search_launches(fg_index *index, uint32_t nq, uint32_t K, uint32_t beam);
 
+/* Which kernels serve searches on this index: FG_GEOMETRY_FIXED, the
+ * kernels specialised for d 128 / degree 32 and d 96 / degree 32 or 16,
+ * whose row offsets are compile-time constants and whose row addresses are
+ * 32-bit byte offsets (codebooks under 4 GiB), or FG_GEOMETRY_GENERAL, the
+ * kernels with runtime offsets and 64-bit row addresses (other shapes,
+ * codebooks of 4 GiB or more, FG_FORCE_RUNTIME_GEOMETRY=1).  Results are
+ * identical either way; negative FG_E* for a NULL index.  Diagnostic, no
+ * counterpart in the reference (which addresses rows as
+ * size_t(node) * row_offset, src/adaptive_search.cuh:225, 366, 438). */
+#define FG_GEOMETRY_FIXED 0
+#define FG_GEOMETRY_GENERAL 1
+int fg_search_geometry(const fg_index *index);
+
 /* Query preparation only (utils.cuh:840-939): rotated query (padded_dim
  * float32), quantized levels (padded_dim uint8), and {low, high, width} plus
  * sum_q, for nq host queries.  Test hook for the preparation stage. */

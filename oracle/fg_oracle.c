@@ -24,9 +24,12 @@
  *   bitonic network              sortedness + permutation vs sorted() on
  *                                distinct keys; tie behaviour by brute force
  *                                of compare-exchange on tiny inputs
- *   merges                       vs heapq.merge / sorted() on distinct keys
+ *   merges                       vs heapq.merge / sorted() on distinct keys;
+ *                                merge-path ties between beam and candidates
+ *                                inside a segment: the stable merge, beam first
  *   hash                         set semantics vs a Python set
- *   pick / keep counts           hand-computed cases
+ *   pick / keep counts           hand-computed cases; the stage-II rank keeps
+ *                                the lower lane of a tie (keep 1 over a tie)
  *   controller, K-th cutoff      hand-computed trajectories of the exported
  *                                fgo_controller_step / fgo_record_expander /
  *                                fgo_kth_cutoff (test_oracle_traces.py)
@@ -37,7 +40,14 @@
  *                                set's rebuild at iteration 15 (a pending
  *                                sibling admitted twice), max_iter and the
  *                                final merge (a line graph whose searches run
- *                                to the iteration limit)
+ *                                to the iteration limit); stage-II estimates
+ *                                from each parent's own distance, the keep-all
+ *                                shortcut at equality in both stages, the
+ *                                8-slot second tile of a degree-40 parent, and
+ *                                the result writer's empty slots (0x7FFFFFFF
+ *                                inside the beam, the last id past it)
+ *   mutations                    each rule above planted wrong in a copy of
+ *                                this file fails a pin (test_oracle_mutations)
  *   entry point / recall / I/O   the reference's own host headers compiled
  *                                from /root/reference (oracle/_ref)
  *   whole search                 recall vs brute-force ground truth; a
@@ -48,7 +58,9 @@
  * Parity unpinned -- these cannot be pinned without running the reference
  * (no CUDA toolchain here), so they are the oracle's stated choices:
  *   - the fp-contraction sites (fmaf exactly where nvcc's default --fmad=true
- *     would contract; every other operation unfused);
+ *     would contract; every other operation unfused).  Bounded instead:
+ *     test_oracle_fma rebuilds this file with all six sites unfused and
+ *     requires the same ids on >= 98% of queries and recall within 0.2 pp;
  *   - the speculative round's visibility rule (every task of a round sees the
  *     visited set as it stood at the round's start; inserts resolve in
  *     (task, lane) order) and theta = 1 duplicates resolving by slot order;

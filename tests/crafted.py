@@ -234,3 +234,95 @@ def visited_peak(trace, beam: int) -> int:
     for t0 in range(15, len(trace), 16):
         peak = max(peak, min(beam, int(merged[t0 - 1])) + int(valid[t0:t0 + 16].sum()) + 1)
     return peak
+
+
+def scenario_short_graph():
+    """Three nodes, degree 2: the entry 0 (100) links to 1 (36) and 2 (49),
+    which link back to 0.  Every search reaches three nodes, fewer than the
+    beam or K asks for, so the result writer's empty slots show
+    (adaptive_search.cuh:455-464): a beam slot that never held an id is
+    written as 0x7FFFFFFF (its MSB masked before the MAX_INDEX test), and
+    only positions past the beam repeat the last id."""
+    dist = {0: 100, 1: 36, 2: 49}
+    adj = {0: [1, 2], 1: [0], 2: [0]}
+    return make(dist, adj, {}, degree=2)
+
+
+def scenario_stage2_parents():
+    """Degree 8, beam 8, K 8: one stage-II round whose outcome depends on
+    three rules of adaptive_search.cuh:377-404 that the other scenarios leave
+    open.  The prelude is scenario_stage2_cutoff's (1 .. 6 scored from the
+    entry, 9 (500) and 10 (510) from node 1, 2 and 3 dead ends), so the
+    round runs over parents 4 (40), 5 (50), 6 (60) and 9 (500) with the
+    K-th cutoff 500 and a keep of 4 per parent:
+      - parent 5 (not the first parent) has 8 fresh children estimated at
+        420, 490, 505, 600 .. 1000 from ITS distance 50: two are within the
+        cutoff.  Estimated from the first parent's distance (40) instead,
+        three would be;
+      - parent 6 has 8 fresh children all above the cutoff, the best two
+        tied at 650 in lanes 1 and 3: the keep falls to 1 and the lower lane
+        wins the tie;
+      - parent 9 has exactly 4 fresh children (the keep): all are admitted
+        without estimates, although their estimates (600 .. 900) lie above
+        the cutoff."""
+    cb_dist = {0: 1}
+    adj = {0: [1, 2, 3, 4, 5, 6, 7, 8]}
+    for i in range(1, 9):
+        cb_dist[i] = 10 * i
+        adj[i] = [0]
+    adj[1] = [9, 10, 0]
+    cb_dist[9], cb_dist[10] = 500, 510
+    adj[10] = [1]
+    est = {}
+    # parent 5: estimates and true distances
+    kids5 = list(range(30, 38))
+    adj[5] = kids5
+    for k, e in zip(kids5, (420, 490, 505, 600, 700, 800, 900, 1000)):
+        cb_dist[k] = e
+        est[(5, k)] = e
+        adj[k] = [5]
+    cb_dist[31], cb_dist[32] = 15, 16
+    # parent 6: all above the cutoff, a tie at the minimum in lanes 1 and 3
+    kids6 = list(range(40, 48))
+    adj[6] = kids6
+    for k, e in zip(kids6, (700, 650, 900, 650, 800, 750, 1000, 950)):
+        cb_dist[k] = e
+        est[(6, k)] = e
+        adj[k] = [6]
+    cb_dist[41], cb_dist[43] = 25, 26
+    # parent 9: four fresh children between four visited ones
+    adj[9] = [50, 51, 52, 53, 0, 1, 2, 3]
+    for k, d, e in zip((50, 51, 52, 53), (35, 36, 37, 38), (600, 700, 800, 900)):
+        cb_dist[k] = d
+        est[(9, k)] = e
+        adj[k] = [0]
+    adj[31] = adj[41] = [0]
+    for i in list(range(11, 30)) + list(range(38, 40)) + list(range(48, 50)):  # unused ids
+        cb_dist[i] = 5000
+        adj[i] = [0]
+    return make(cb_dist, adj, est, degree=8)
+
+
+def scenario_wide_degree():
+    """Degree 40 (two 32-neighbour tiles per parent), beam 64, K 12.  With
+    one expander the search reads only the first min(degree, 32) slots of a
+    list (adaptive_search.cuh:222): node 9 (distance 5) sits in slot 35 of
+    the entry's list and is never found.  In stage II the second tile of a
+    parent holds 8 slots, so its keep is min(ceil(8 (1 - 0.9)), 32 / 8) = 1
+    (adaptive_search.cuh:380-382 with rate 1 - 4/40): of parent 4's three
+    fresh children in slots 32 .. 34 only the best estimate (21, 150) is
+    kept.  Five parents of two tiles each make 10 tasks: two rounds."""
+    dist = {0: 1, 9: 5}
+    adj = {0: [1, 2, 3, 4, 5, 6, 7, 8] + [None] * 27 + [9]}
+    for i in range(1, 9):
+        dist[i] = 10 * i
+        adj[i] = [0]
+    adj[9] = [0]
+    adj[4] = [0] + [None] * 31 + [20, 21, 22]
+    for k, d in zip((20, 21, 22), (200, 150, 300)):
+        dist[k] = d
+        adj[k] = [4]
+    for i in range(10, 20):  # unused ids
+        dist[i] = 5000
+        adj[i] = [0]
+    return make(dist, adj, {}, degree=40)

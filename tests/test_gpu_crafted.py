@@ -48,6 +48,10 @@ def test_line_search_at_max_iter(gpu_available, beam):
     ("scenario_stage2", 10, 64, [0, 1, 2, 3, 4, 5, 6, 10, 12, 14]),
     ("scenario_stage2_cutoff", 8, 8, [0, 1, 2, 3, 4, 5, 6, 30]),
     ("scenario_reset", 16, 16, [36, 35, 34, 33, 32, 31, 30, 29, 29, 28, 27, 26, 25, 24, 23, 22]),
+    ("scenario_short_graph", 8, 8, [1, 2, 0] + [0x7FFFFFFF] * 5),
+    ("scenario_short_graph", 4, 2, [1, 2, 2, 2]),
+    ("scenario_stage2_parents", 8, 8, [0, 1, 31, 2, 41, 3, 50, 51]),
+    ("scenario_wide_degree", 12, 64, [0, 1, 2, 3, 4, 5, 6, 7, 8, 21, 0x7FFFFFFF, 0x7FFFFFFF]),
 ])
 def test_hand_traced_scenarios(gpu_available, name, K, beam, want):
     cb, q = getattr(crafted, name)()

@@ -1,8 +1,10 @@
-"""The pins in test_oracle_traces.py are strong enough to catch plausible
-mistakes in the oracle's controller and loop sequencing: each mutation below
-is planted in a temporary copy of oracle/fg_oracle.c (compiled on the CPU,
-loaded through FG_ORACLE_LIB in a separate pytest process), and the pin tests
-must fail against it.  The unmutated copy must pass them."""
+"""The oracle's pins are strong enough to catch plausible mistakes in its
+controller, loop sequencing, merge, stage-II selection and result writer:
+each mutation below is planted in a temporary copy of oracle/fg_oracle.c
+(compiled on the CPU, loaded through FG_ORACLE_LIB in a separate pytest
+process), and the pin tests (hand-traced searches, hand-computed primitives
+and the merge-path tie case) must fail against it.  The unmutated copy must
+pass them."""
 from __future__ import annotations
 
 import os
@@ -33,6 +35,26 @@ MUTATIONS = {
     "stage-II keep + 1": (
         "eff = fgo_keep_count_for_expander(an, st.spec_degree, st.rho, kth_valid, near);",
         "eff = fgo_keep_count_for_expander(an, st.spec_degree, st.rho, kth_valid, near) + 1;"),
+    "merge-path ties go to the candidate": (
+        "beam_d[ti] <= cand_d[ci]", "beam_d[ti] < cand_d[ci]"),
+    "result writer tests MAX_INDEX before masking": (
+        """        const uint32_t r = i < beam_sz ? (bi[i] & 0x7fffffffu) : FGO_MAX_INDEX;
+        if (r != FGO_MAX_INDEX) last = r;
+        out[i] = r == FGO_MAX_INDEX ? last : r;""",
+        """        const uint32_t r = i < beam_sz ? bi[i] : FGO_MAX_INDEX;
+        if (r != FGO_MAX_INDEX) last = r & 0x7fffffffu;
+        out[i] = r == FGO_MAX_INDEX ? last : (r & 0x7fffffffu);"""),
+    "stage-II estimates from the first parent's distance": (
+        "fvq[l], pdist[pidx], B);", "fvq[l], pdist[0], B);"),
+    "stage-II rank ties go to the higher lane": (
+        "(other == mine && s < l)", "(other == mine && s > l)"),
+    "stage-II keep-all >= -> >": (
+        "const int keep_all = keep >= (int)raw_valid;", "const int keep_all = keep > (int)raw_valid;"),
+    "stage-I keep-all >= -> >": (
+        "const int keep_all = keep >= (int)valid;", "const int keep_all = keep > (int)valid;"),
+    "partial tile counted as a full one": (
+        "uint32_t an = active ? deg - (uint32_t)tile * 32u : 0u;",
+        "uint32_t an = active ? (deg < 32u ? deg : 32u) : 0u;"),
     "no final merge after the loop": (
         "fgo_merge_candidates(bd, bi, cd, ci, cbs, pbeam, 0, ws->scratch_d, ws->scratch_i);  /* :449-451 */",
         "/* final merge dropped */"),
@@ -54,10 +76,14 @@ def _build(tmp_path, name, mutation):
     return str(so)
 
 
+PIN_TESTS = ["test_oracle_traces.py", "test_oracle_primitives.py",
+             "test_oracle_networks.py::test_merge_path_ties_inside_segments_keep_beam_first"]
+
+
 def _pins_pass(lib):
     env = dict(os.environ, FG_ORACLE_LIB=lib)
-    r = subprocess.run([sys.executable, "-m", "pytest", "-x", "-q", "-p", "no:cacheprovider",
-                        os.path.join(ROOT, "tests", "test_oracle_traces.py")],
+    r = subprocess.run([sys.executable, "-m", "pytest", "-x", "-q", "-p", "no:cacheprovider"] +
+                       [os.path.join(ROOT, "tests", t) for t in PIN_TESTS],
                        cwd=ROOT, env=env, capture_output=True, text=True, timeout=600)
     return r.returncode == 0, r.stdout[-400:]
 

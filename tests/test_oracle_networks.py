@@ -259,6 +259,65 @@ def test_merge_path_distinct_keys_is_sorted_union():
         assert all(key_of[int(i)] == float(k) for i, k in zip(b2, b1))
 
 
+@pytest.mark.parametrize("pbeam", [256, 384, 512, 1024])
+def test_merge_path_ties_inside_segments_keep_beam_first(pbeam):
+    """Keys tied between the beam and the candidates: the output loop takes
+    the beam entry on `<=` (utils.cuh:656-661), so the result is the stable
+    merge with beam entries before candidates of equal key.  At these beams
+    the reference's segmentation gives every thread 4 outputs (ceil(pbeam/4)
+    threads, at most 256), so each tie is placed strictly inside one group
+    of 4 outputs with distinct keys on either side of every group boundary:
+    the partitions at the boundaries are unique and only the `<=` decides.
+    Group g of the output holds keys 10g, 10g+1, 10g+1, 10g+2; in 32 groups
+    the tied pair is (beam, candidate), in the others (beam, beam), and in 8
+    of the candidate groups a second beam entry shares the key (beam, beam,
+    candidate over positions 1-3).  The 32 leftover beam entries sort after
+    everything and drop out."""
+    L = O.lib()
+    groups = pbeam // 4
+    cand_groups = set(range(1, groups, groups // 32))
+    assert len(cand_groups) == 32
+    triple = set(sorted(cand_groups)[::4])
+    beam_k, cand_k, want = [], [], []  # want: (key, source) in output order
+    for g in range(groups):
+        k0, k1, k3 = 10 * g, 10 * g + 1, 10 * g + 2
+        if g in triple:
+            slots = [(k0, "b"), (k1, "b"), (k1, "b"), (k1, "c")]
+        elif g in cand_groups:
+            slots = [(k0, "b"), (k1, "b"), (k1, "c"), (k3, "b")]
+        else:
+            slots = [(k0, "b"), (k1, "b"), (k1, "b"), (k3, "b")]
+        for k, src in slots:
+            (beam_k if src == "b" else cand_k).append(k)
+        want += slots
+    beam_k += [100000 + i for i in range(pbeam - len(beam_k))]
+    assert len(beam_k) == pbeam and len(cand_k) == 32
+    for b in range(4, pbeam, 4):  # distinct keys across every group boundary
+        assert want[b - 1][0] < want[b][0]
+    bd = np.asarray(beam_k, np.float32)
+    bi = np.arange(pbeam, dtype=np.uint32)
+    rng = np.random.default_rng(pbeam)
+    perm = rng.permutation(32)  # the candidate buffer arrives unsorted
+    cd = np.asarray(cand_k, np.float32)[perm].copy()
+    ci = (5000 + perm).astype(np.uint32)
+    # expected ids: beam entries in beam order, candidates in key order
+    nb = nc = 0
+    want_ids = []
+    for k, src in want:
+        if src == "b":
+            want_ids.append(nb)
+            nb += 1
+        else:
+            want_ids.append(5000 + nc)
+            nc += 1
+    sd = np.zeros(1024, np.float32)
+    si = np.zeros(1024, np.uint32)
+    L.fgo_merge_candidates(O.ptr(bd, C.c_float), O.ptr(bi, C.c_uint32), O.ptr(cd, C.c_float),
+                           O.ptr(ci, C.c_uint32), 32, pbeam, 0, O.ptr(sd, C.c_float), O.ptr(si, C.c_uint32))
+    assert bd.tolist() == [float(k) for k, _ in want]
+    assert bi.tolist() == want_ids
+
+
 def _ref_partition(a, b, diag):
     """Brute force: the binary search of utils.cuh:588-616, unrolled."""
     na, nb = len(a), len(b)

@@ -259,6 +259,24 @@ def test_pick_expanders():
     assert n == 3 and list(out[:3]) == [40, 41, 42]
 
 
+def test_keep_topk_single_keep_over_a_tie_takes_the_lower_lane():
+    """warp_keep_topk_smallest_f32 (utils.cuh:251-267) ranks a lane by the
+    valid lanes with a smaller value or an equal value in a lower lane: with
+    keep 1 over equal minima in lanes 5 and 17 (lane 9, also at the minimum,
+    is invalid), only lane 5 is kept; with keep 2 lanes 5 and 17."""
+    vals = np.full(32, 50.0, np.float32)
+    vals[[5, 9, 17]] = 7.0
+    vals[30] = 8.0
+    valid = np.ones(32, np.int32)
+    valid[9] = 0
+    keep = np.zeros(32, np.int32)
+    call = lambda k: L().fgo_warp_keep_topk(O.ptr(vals, C.c_float), valid.ctypes.data_as(C.POINTER(C.c_int)), k,
+                                            keep.ctypes.data_as(C.POINTER(C.c_int)))
+    assert call(1) == 1 and list(np.nonzero(keep)[0]) == [5]
+    assert call(2) == 2 and list(np.nonzero(keep)[0]) == [5, 17]
+    assert call(3) == 3 and list(np.nonzero(keep)[0]) == [5, 17, 30]
+
+
 def test_keep_topk_rank_ties_by_lane():
     vals = np.array([3, 1, 1, 2] + [9] * 28, np.float32)
     valid = np.array([1, 1, 1, 1] + [0] * 28, np.int32)

@@ -122,8 +122,8 @@ def _trace(cb, q, K, beam):
     c = tuple(getattr(cnt, f) for f, _ in O.Counters._fields_)
     recs = []
     for t in tr:
-        ids = [t.cand_idx[i] for i in range(32) if t.cand_idx[i] != 0xFFFFFFFF]
-        ds = [t.cand_dist[i] for i in range(32) if t.cand_idx[i] != 0xFFFFFFFF]
+        ids = [t.cand_idx[i] for i in range(t.n_cand) if t.cand_idx[i] != 0xFFFFFFFF]
+        ds = [t.cand_dist[i] for i in range(t.n_cand) if t.cand_idx[i] != 0xFFFFFFFF]
         recs.append(dict(theta=t.theta, rho=t.rho, parents=list(t.parents)[: t.n_parents],
                          top1=t.top1 & ~MSB, kth=t.kth_cutoff, cand=ids, cdist=ds, stall=t.stall,
                          last=t.last_expander_distance, cur=t.current_expander_distance,
@@ -277,3 +277,85 @@ def test_line_iterations_and_final_merge(beam):
             seen += [t.cand_dist[i] for i in range(32) if t.cand_idx[i] != 0xFFFFFFFF]
         got = np.sort(((base[out.astype(np.int64)] - q[qi]) ** 2).sum(-1))
         assert np.array_equal(got, np.sort(np.asarray(seen, np.float32))[:K]), (beam, qi)
+
+
+def test_trace_result_writer_empty_slots():
+    """adaptive_search.cuh:455-464 masks the expanded flag off a beam slot
+    BEFORE testing it against MAX_INDEX, so a slot that never held an id
+    (0xFFFFFFFF) is written as 0x7FFFFFFF; only positions at or past the beam
+    repeat the last id written.  Degree 2: cbs = 16, keep ceil(2 * 0.75) = 2
+    takes both of the entry's children without estimates.
+      beam 8, K 8: it 0 expands 0 and scores 1 (36), 2 (49); it 1 and 2
+            expand 1 and 2 (children visited); it 3 has nothing to expand.
+            The beam holds 1, 2, 0 and five empty slots.
+      beam 2, K 4: the same three iterations (max_iter (22 + 9)/10 = 3); the
+            beam keeps 1, 2 and positions 2, 3 repeat 2.
+    Counters: 3 iterations, 3 expansions, 3 x 2 ids, no estimates, 1 + 2
+    exact distances."""
+    cb, q = crafted.scenario_short_graph()
+    out, cnt, tr = _trace(cb, q, 8, 8)
+    assert out == [1, 2, 0] + [0x7FFFFFFF] * 5
+    assert cnt == (3, 3, 6, 0, 3, 0xFFFFFFFF)
+    assert [t["parents"] for t in tr] == [[0], [1], [2]]
+    out, cnt, tr = _trace(cb, q, 4, 2)
+    assert out == [1, 2, 2, 2]
+    assert cnt == (3, 3, 6, 0, 3, 0xFFFFFFFF)
+    assert [t["kth"] for t in tr] == [FLT_MAX, 49.0, 49.0]
+
+
+def test_trace_stage2_parent_distance_lane_tie_and_keep_all():
+    """Degree 8, beam 8, K 8 (crafted.scenario_stage2_parents).
+      it 0-3: as in scenario_stage2_cutoff: 1 .. 6 scored, then 9 (500) and
+            10 (510); 2 and 3 are dead ends; the cutoff is 500 from it 2.
+      it 4: fourth stall: stage II over 4 (40), 5 (50), 6 (60), 9 (500), keep
+            min(ceil(8 * 0.5), 32 / 8) = 4 per parent.
+            parent 4: no fresh child (keep-all, nothing estimated);
+            parent 5: estimates from ITS distance (adaptive_search.cuh:394):
+              420, 490, 505, 600 .. 1000; near count (<= 500) 2: keep 30, 31;
+            parent 6: all 8 estimated above 500 (near count 0, keep
+              clamp(0, 1, 4) = 1); the minimum 650 is tied between lanes 1
+              (41) and 3 (43): the lower lane wins (utils.cuh:261);
+            parent 9: 4 fresh children = the keep, so all four are admitted
+              unestimated (`keep >= valid`, adaptive_search.cuh:387).
+            Compacted in (task, lane) order: 30 31 41 50 51 52 53, scored at
+            420, 15, 25, 35, 36, 37, 38.
+      it 5: beam [0, 1, 31, 2, 41, 3, 50, 51], cutoff 36; the four new
+            entries are dead ends.  it 6 finds nothing to expand.
+    Counters: 6 iterations, 1+1+1+1+4+4 = 12 expansions, 4 x 8 + 8 x 8 = 96
+    ids, 8 + 8 + 8 estimates, 1 + 6 + 2 + 7 exact distances, stage II from
+    iteration 4."""
+    cb, q = crafted.scenario_stage2_parents()
+    out, cnt, tr = _trace(cb, q, 8, 8)
+    assert out == [0, 1, 31, 2, 41, 3, 50, 51]
+    assert cnt == (6, 12, 96, 24, 16, 4)
+    assert [t["parents"] for t in tr] == [[0], [1], [2], [3], [4, 5, 6, 9], [31, 41, 50, 51]]
+    assert [t["kth"] for t in tr] == [FLT_MAX, FLT_MAX, 500.0, 500.0, 500.0, 36.0]
+    assert tr[4]["cand"] == [30, 31, 41, 50, 51, 52, 53]
+    assert tr[4]["cdist"] == [420, 15, 25, 35, 36, 37, 38]
+    assert tr[5]["cand"] == []
+
+
+def test_trace_wide_degree_tiles():
+    """Degree 40, beam 64 (never full: no cutoff), K 12
+    (crafted.scenario_wide_degree).
+      it 0: one expander reads min(40, cbs 32) = 32 slots
+            (adaptive_search.cuh:222): 1 .. 8 are found (keep ceil(32 * 0.75)
+            = 24 >= 8: all scored); node 9 in slot 35 is never read.
+      it 1-3: 1, 2, 3 are dead ends; top-1 0 stalls 1, 2, 3 times.
+      it 4: stage II, rate 1 - 4/40 = 0.9, parents 4 .. 8, two tiles each: 10
+            tasks in two rounds.  A full tile keeps min(ceil(32 * 0.1), 4) =
+            4, the 8-slot second tile min(ceil(8 * 0.1), 4) = 1
+            (adaptive_search.cuh:380-382): of parent 4's fresh 20, 21, 22
+            (slots 32-34, estimated 200, 150, 300) only 21 is kept.
+      it 5: expand 21 (a dead end); it 6 finds nothing.
+    The beam holds 10 ids: positions 10 and 11 are empty slots (0x7FFFFFFF).
+    Counters: 6 iterations, 1+1+1+1+5+1 = 10 expansions, 4 x 32 + 6 x 40 =
+    368 ids, 3 estimates, 1 + 8 + 1 exact distances."""
+    cb, q = crafted.scenario_wide_degree()
+    out, cnt, tr = _trace(cb, q, 12, 64)
+    assert out == [0, 1, 2, 3, 4, 5, 6, 7, 8, 21, 0x7FFFFFFF, 0x7FFFFFFF]
+    assert cnt == (6, 10, 368, 3, 10, 4)
+    assert [t["parents"] for t in tr] == [[0], [1], [2], [3], [4, 5, 6, 7, 8], [21]]
+    assert tr[0]["cand"] == [1, 2, 3, 4, 5, 6, 7, 8]
+    assert tr[4]["cand"] == [21] and tr[4]["cdist"] == [150]
+    assert np.allclose([t["rho"] for t in tr[4:]], [0.9, 0.9])
