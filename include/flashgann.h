@@ -113,8 +113,10 @@ int fg_search(fg_index *index, const float *queries, uint32_t nq, uint32_t K, ui
  * align256(nq*dim*4) + align256(nq*K*4) [+ align256(nq*24) with counters]
  * bytes of it and is rejected with FG_EINVAL above the maximum (about 17,900
  * queries at dim 128, K 100, with counters).  Every call on one device
- * shares that area: calls that overlap on one device race, so issue them from
- * one host thread at a time per device. */
+ * shares that area: calls on one device from several host threads take a
+ * per-device host lock for their whole duration and run one after another
+ * (the lock is host memory; nothing is allocated on the device).  Calls on
+ * one index still come from one host thread at a time, as for fg_search. */
 #define FG_NOALLOC_STAGING_BYTES (16u << 20)
 int fg_search_noalloc(fg_index *index, const float *queries, uint32_t nq, uint32_t K, uint32_t beam,
                       uint32_t *result_ids, uint32_t *counters, fg_stats *stats);

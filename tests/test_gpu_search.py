@@ -429,20 +429,61 @@ def test_device_search_captured_in_a_graph(gpu_available, monkeypatch):
 
 
 def test_search_launches_reports_the_schedule(gpu_available, monkeypatch):
-    """fg_search_launches: two launches for a one-wave batch larger than the
-    device holds at once (and at most 16,384 queries), one otherwise, and
-    the environment override wins where the form allows two."""
+    """fg_search_launches: one launch while every query of a one-wave batch
+    starts at once, two for a larger batch (up to 16,384 queries), one above
+    that and for the team form; the environment override wins where the form
+    allows two.  The residency threshold is found by bisection and must be a
+    whole number of workgroups per CU (it depends on the device's CU count
+    and the kernel's occupancy, so no number is hard-coded)."""
+    import torch
     from flashgann_amd import Index
     cb, q, _ = small_index()
     ix = Index.from_codebook(cb)
     monkeypatch.delenv("FLASHGANN_TEAM", raising=False)
     monkeypatch.delenv("FLASHGANN_SLICE", raising=False)
-    assert ix.search_launches(10000, 100, 256) == 2   # 24 queries per CU x 256 CUs = 6,144 at once
-    assert ix.search_launches(5000, 100, 256) == 1    # every query starts at once
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    lo, hi = 2 * cus, 16384  # (2 x CUs: the team form, one launch)
+    assert ix.search_launches(lo, 100, 256) == 1
+    assert ix.search_launches(hi, 100, 256) == 2
+    while hi - lo > 1:  # the largest one-launch batch
+        mid = (lo + hi) // 2
+        if ix.search_launches(mid, 100, 256) == 1:
+            lo = mid
+        else:
+            hi = mid
+    assert lo % cus == 0 and 2 <= lo // cus <= 64, (lo, cus)
+    assert all(ix.search_launches(n, 100, 256) == 2 for n in (lo + 1, lo + 1000, 16384))
     assert ix.search_launches(16, 10, 64) == 1        # the team form
-    assert ix.search_launches(20000, 100, 256) == 1   # above the order kernel's 16,384
+    assert ix.search_launches(16385, 100, 256) == 1   # above the order kernel's 16,384
     monkeypatch.setenv("FLASHGANN_SLICE", "0")
-    assert ix.search_launches(10000, 100, 256) == 1
+    assert ix.search_launches(16384, 100, 256) == 1
     monkeypatch.setenv("FLASHGANN_SLICE", "1")
-    assert ix.search_launches(5000, 100, 256) == 2
+    assert ix.search_launches(lo, 100, 256) == 2
     ix.close()
+
+
+@pytest.mark.parametrize("nq,beam", [(4000, 256), (4000, 384), (16384, 256), (16384, 512)])
+def test_two_launch_search_large_batches(gpu_available, monkeypatch, nq, beam):
+    """Forced two-launch searches over batches that use every part of the
+    order kernel (queries past its first 1,024 slots, and its 16,384-query
+    maximum): ids and counters equal the one-launch search's, and on the
+    distinct queries the oracle's.  The batch repeats 300 queries, so each
+    distinct query is checked at many positions of the order."""
+    from flashgann_amd import Index
+    from oracle import oracle as O
+    cb, q, _ = small_index(n=3000, nq=300)
+    qq = np.ascontiguousarray(np.resize(q, (nq, q.shape[1])))
+    ix = Index.from_codebook(cb)
+    monkeypatch.setenv("FLASHGANN_TEAM", "0")
+    monkeypatch.setenv("FLASHGANN_SLICE", "0")
+    ids1, _, cnt1 = ix.search(qq, 100, beam, counters=True)
+    monkeypatch.setenv("FLASHGANN_SLICE", "1")
+    assert ix.search_launches(nq, 100, beam) == 2
+    ids2, _, cnt2 = ix.search(qq, 100, beam, counters=True)
+    ix.close()
+    assert (cnt1[:, 0] > 15).any()
+    assert np.array_equal(ids2, ids1) and np.array_equal(cnt2, cnt1)
+    rids, rcnt = O.OracleIndex.from_codebook(cb).search(q, 100, beam)
+    rep = np.arange(nq) % q.shape[0]
+    assert np.array_equal(ids2, rids[rep])
+    assert np.array_equal(cnt2, rcnt.view(np.uint32).reshape(-1, 6)[rep])

@@ -3,9 +3,9 @@
 With promotion of private arrays to registers turned off (a flag the build
 needs for speed), a private array indexed by a run-time value is kept in
 scratch memory, where an index outside the array is an out-of-bounds memory
-access on the device rather than a wrong value.  This compiles the kernel
-source to device assembly with the product flags and checks every kernel's
-ScratchSize."""
+access on the device rather than a wrong value.  This compiles every kernel
+source (the host side's and each shape class's object) to device assembly
+with the product flags and checks every kernel's ScratchSize."""
 from __future__ import annotations
 
 import os
@@ -29,14 +29,25 @@ def _flags():
 
 @pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not installed")
 def test_no_kernel_uses_scratch(tmp_path):
-    out = tmp_path / "fg_search.s"
-    src = os.path.join(ROOT, "flashgann_amd", "csrc", "fg_search.hip")
-    cmd = [HIPCC, *_flags(), "--cuda-device-only", "-S", "-o", str(out), src]
-    r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
-    assert r.returncode == 0, r.stderr[-2000:]
-    asm = out.read_text()
-    names = re.findall(r"^(_Z\w+):\s*;\s*@", asm, re.M)
-    sizes = [int(x) for x in re.findall(r"; ScratchSize: (\d+)", asm)]
-    assert len(sizes) == len(names) and len(names) >= 20, (len(names), len(sizes))
+    csrc = os.path.join(ROOT, "flashgann_amd", "csrc")
+    # the host side's kernels and each shape class's object, compiled in parallel
+    units = [("fg_search", os.path.join(csrc, "fg_search.hip"), [])]
+    units += [(f"fg_shape{i}", os.path.join(csrc, "fg_shapes.hip"), [f"-DFG_SHAPE={i}"]) for i in range(7)]
+    procs = []
+    for name, src, extra in units:
+        out = tmp_path / f"{name}.s"
+        cmd = [HIPCC, *_flags(), *extra, "--cuda-device-only", "-S", "-o", str(out), src]
+        procs.append((name, out, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
+    names, sizes = [], []
+    for name, out, p in procs:
+        _, err = p.communicate(timeout=900)
+        assert p.returncode == 0, (name, err[-2000:])
+        asm = out.read_text()
+        n = re.findall(r"^(_Z\w+):\s*;\s*@", asm, re.M)
+        z = [int(x) for x in re.findall(r"; ScratchSize: (\d+)", asm)]
+        assert len(z) == len(n), (name, len(n), len(z))
+        names += n
+        sizes += z
+    assert len(names) >= 80, len(names)
     bad = [(n, s) for n, s in zip(names, sizes) if s != 0]
     assert not bad, bad

@@ -2,7 +2,8 @@
 fg_search itself: ids and work counters identical on two calls in a row (the
 second with fewer queries, so stale staging from the first would show), with
 and without counters; a call whose staging exceeds the fixed area is rejected
-before any device work."""
+before any device work; the first search of a fresh index allocates no
+device memory; calls from two host threads on one device take turns."""
 from __future__ import annotations
 
 import numpy as np
@@ -63,3 +64,70 @@ def test_noalloc_rejects_staging_above_maximum(gpu_available):
         assert np.array_equal(ix.search(q[:8], 100, 64, noalloc=True)[0], ids)
     finally:
         ix.close()
+
+
+def test_noalloc_first_search_on_a_fresh_index_allocates_nothing(gpu_available):
+    """On an index that has never searched (so fg_search's own staging
+    buffers do not exist), the first call is fg_search_noalloc: the device's
+    free memory is the same before and after it, and a second call returns
+    the same ids.  A search on another index first loads the kernels, whose
+    code objects take device memory once per process."""
+    import torch
+
+    from flashgann_amd import Index
+    cb, q, _ = small_index(nq=400)
+    warm = Index.from_codebook(cb)
+    warm.search(q[:64], 100, 256, counters=True, noalloc=True)
+    warm.close()
+    ix = Index.from_codebook(cb)
+    try:
+        torch.cuda.synchronize()
+        free0 = torch.cuda.mem_get_info()[0]
+        ids, _, cnt = ix.search(q[:64], 100, 256, counters=True, noalloc=True)
+        torch.cuda.synchronize()
+        assert torch.cuda.mem_get_info()[0] == free0
+        ids2, _, cnt2 = ix.search(q[:64], 100, 256, counters=True, noalloc=True)
+        assert np.array_equal(ids2, ids) and np.array_equal(cnt2, cnt)
+        assert torch.cuda.mem_get_info()[0] == free0
+    finally:
+        ix.close()
+
+
+def test_noalloc_calls_from_two_threads_take_turns(gpu_available):
+    """Two host threads search two indices on one device through
+    fg_search_noalloc at the same time (ctypes releases the interpreter lock
+    during the call), each with its own queries: every call returns the ids
+    its own serial call does, because the per-device lock keeps one call at a
+    time in the shared staging area."""
+    import threading
+
+    from flashgann_amd import Index
+    cb, q, _ = small_index(nq=400)
+    cb96, q96, _ = small_index(n=2000, nq=24, dim=96, degree=16, kind="unit")
+    a, b = Index.from_codebook(cb), Index.from_codebook(cb96)
+    try:
+        want_a = [a.search(q[i * 50:(i + 1) * 50], 10, 128)[0] for i in range(8)]
+        want_b = b.search(q96, 10, 128)[0]
+        errors = []
+
+        def run_a():
+            for rep in range(6):
+                for i in range(8):
+                    if not np.array_equal(a.search(q[i * 50:(i + 1) * 50], 10, 128, noalloc=True)[0], want_a[i]):
+                        errors.append(("a", rep, i))
+
+        def run_b():
+            for rep in range(48):
+                if not np.array_equal(b.search(q96, 10, 128, noalloc=True)[0], want_b):
+                    errors.append(("b", rep))
+
+        ts = [threading.Thread(target=run_a), threading.Thread(target=run_b)]
+        for t in ts:
+            t.start()
+        for t in ts:
+            t.join(timeout=60)
+        assert not any(t.is_alive() for t in ts)
+        assert not errors, errors[:5]
+    finally:
+        a.close()
+        b.close()
