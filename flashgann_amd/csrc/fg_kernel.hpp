@@ -266,18 +266,39 @@ struct SearchParams {
 
 // Per-query state of a suspended search, in 32-bit words after a header of
 // kSliceHeader words (word 0: the number of suspended queries, set by the
-// order kernel).  Per query: a mark (1), the ordering key, the controller (9
+// order step).  Per query: a mark (1), the ordering key, the controller (9
 // words), the work counters (6), the candidate span, the split flag and the
-// pick's start (beams over 256), then
-// the pbeam beam pairs and the 32 candidate pairs.  slice_keys holds the
-// key (bits of a non-negative distance) of each suspended query and
-// kSliceDone for a query the first slice finished.
+// pick's start (beams over 256), then the pbeam beam pairs and the 32
+// candidate pairs, then the prepared query: low, width, sum_q, a pad word and
+// the 8 planes of W = padded_dim / 32 words (so the second slice does not
+// rotate and quantise the query again, nor read the entry point's row).
+// slice_keys holds the key (bits of a finite float: the best distance so far)
+// of each suspended query and kSliceDone (a NaN pattern, never a key) for a
+// query the first slice finished.
 constexpr uint32_t kSliceHeader = 64;
 constexpr uint32_t kSliceFixed = 20;  // 2 + 9 + 6 + 2 + 1 (the pick's start, beams over 256)
-__host__ __device__ inline uint32_t slice_words(uint32_t pbeam) { return kSliceFixed + 2u * (pbeam + 32u); }
+__host__ __device__ inline uint32_t slice_prep_offset(uint32_t pbeam) { return kSliceFixed + 2u * (pbeam + 32u); }
+__host__ __device__ inline uint32_t slice_words(uint32_t pbeam, uint32_t padded_dim) {
+    return slice_prep_offset(pbeam) + 4u + 8u * (padded_dim / 32u);
+}
 constexpr uint32_t kSliceDone = 0xFFFFFFFFu;
-constexpr int kSliceMaxQueries = 16384;  // the order kernel holds every query's bin in LDS
+constexpr int kSliceMaxQueries = 16384;  // the one-workgroup order kernel holds every query's bin in LDS
 constexpr int kSliceBins = 4096;
+
+// The ordering key of a suspended query: the best distance so far, made
+// finite (+inf -> FLT_MAX, -inf and NaN -> -FLT_MAX) so that it orders as a
+// float for either metric (inner-product distances are negative).
+__device__ __forceinline__ uint32_t slice_key(float d) {
+    const float k = isnan(d) ? -FLT_MAX : fminf(fmaxf(d, -FLT_MAX), FLT_MAX);
+    return __float_as_uint(k);
+}
+// Order-preserving unsigned image of a finite float key (larger key, larger image).
+__host__ __device__ inline uint32_t key_order_bits(uint32_t bits) {
+    return (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
+}
+__host__ __device__ inline uint32_t key_from_order_bits(uint32_t o) {
+    return (o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o;
+}
 
 
 // Row geometry (include/qg.hpp:66-73), compile-time for the specialised
@@ -1723,12 +1744,27 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
         t_last = __builtin_amdgcn_s_memtime();
     }
 
-    // ---- query preparation (the visited table's LDS holds the rotation)
+    // ---- query preparation (the visited table's LDS holds the rotation); a
+    // query resumed by the second slice reads back the planes and constants
+    // the first slice kept instead
     float qlow = 0.0f, qhigh = 0.0f, qwidth = 0.0f;
     int sum_q = 0;
-    if (lead)
-        prepare_query<NW>(P.queries + static_cast<uint64_t>(qid) * g.dim, P.signs, g.dim, B,
-                          reinterpret_cast<float *>(H), nullptr, planes, qlow, qhigh, qwidth, sum_q, nullptr);
+    const bool resuming = kSliceable && P.slice_resume > 0;
+    if (lead) {
+        if (resuming) {
+            const uint32_t *sp = P.slice_state + kSliceHeader +
+                                 static_cast<uint64_t>(qid) * slice_words(static_cast<uint32_t>(P.pbeam), B) +
+                                 slice_prep_offset(static_cast<uint32_t>(P.pbeam));
+            for (int i = lane; i < 8 * W; i += 64) planes[i] = sp[4 + i];
+            qlow = __uint_as_float(uni(sp[0]));
+            qwidth = __uint_as_float(uni(sp[1]));
+            sum_q = static_cast<int>(uni(sp[2]));
+            lead_sync<NW>();
+        } else {
+            prepare_query<NW>(P.queries + static_cast<uint64_t>(qid) * g.dim, P.signs, g.dim, B,
+                              reinterpret_cast<float *>(H), nullptr, planes, qlow, qhigh, qwidth, sum_q, nullptr);
+        }
+    }
     // the query is read from global memory, where it stays cached (the
     // generic geometry's exact distances read it there; the others keep it in
     // registers, qr below)
@@ -1769,8 +1805,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
     const uint2 kLowSentinel = make_uint2(__float_as_uint(-FLT_MAX), kMaxIndex);
     float entry_d = 0.0f;
     if (lead) {
-        entry_d = uni(beam_key(half_distance(P.data + static_cast<uint64_t>(P.entry) * g.row, qsrc, g.dim, nl,
-                                             P.use_ip != 0, true)));
+        // (a resumed query's entry distance comes back with its controller)
+        if (!resuming)
+            entry_d = uni(beam_key(half_distance(P.data + static_cast<uint64_t>(P.entry) * g.row, qsrc, g.dim, nl,
+                                                 P.use_ip != 0, true)));
 
         // ---- state (adaptive_search.cuh:67-107)
         hash_reset(H, nbk);
@@ -1824,7 +1862,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
             // unmerged candidates, the controller and the counters as the first
             // slice left them.  Ids are checked so that no later row read can
             // leave the codebook, whatever the buffer holds.
-            const uint32_t *st = P.slice_state + kSliceHeader + static_cast<uint64_t>(qid) * slice_words(pbeam);
+            const uint32_t *st = P.slice_state + kSliceHeader + static_cast<uint64_t>(qid) * slice_words(pbeam, B);
             const uint2 *sb = reinterpret_cast<const uint2 *>(st + kSliceFixed);
             const uint2 kEmptyPair = make_uint2(__float_as_uint(FLT_MAX), kMaxIndex);
             for (int i = lane; i < pbeam + 32; i += 64) {
@@ -2381,7 +2419,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
     }
     if constexpr (kSliceable) {
         if (P.slice_suspend > 0) {
-            uint32_t *st = P.slice_state + kSliceHeader + static_cast<uint64_t>(qid) * slice_words(pbeam);
+            uint32_t *st = P.slice_state + kSliceHeader + static_cast<uint64_t>(qid) * slice_words(pbeam, B);
             if (suspended) {
                 // the state the next slice resumes from; the ordering key is the
                 // best distance found so far (the larger, the longer the rest of
@@ -2389,8 +2427,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
                 uint2 *sb = reinterpret_cast<uint2 *>(st + kSliceFixed);
                 const float kd = pair_key(bp[0]);
                 for (int i = lane; i < pbeam + 32; i += 64) sb[i] = i < pbeam ? bp[i] : ms[i - pbeam];
+                uint32_t *sp = st + slice_prep_offset(pbeam);
+                for (int i = lane; i < 8 * W; i += 64) sp[4 + i] = planes[i];
                 if (lane == 0) {
-                    const uint32_t key = __float_as_uint(fminf(fmaxf(kd, 0.0f), FLT_MAX));
+                    sp[0] = __float_as_uint(qlow);
+                    sp[1] = __float_as_uint(qwidth);
+                    sp[2] = static_cast<uint32_t>(sum_q);
+                    sp[3] = 0u;
+                    const uint32_t key = slice_key(kd);
                     P.slice_keys[qid] = key;
                     st[0] = 1u;
                     st[1] = key;

@@ -46,18 +46,36 @@ using namespace fgk;
 namespace {
 
 // Order of the second slice: the suspended queries sorted by key, largest
-// first (a counting sort over kSliceBins bins of [0, largest key]; within a
-// bin the order is arbitrary).  One workgroup; writes the count to
+// first: a counting sort over kSliceBins bins spread linearly over [smallest
+// key, largest key] (keys are finite floats of either sign; within a bin the
+// order is arbitrary).  Writes the count of suspended queries to
 // slice_state[0] and the queries to order[0 .. count).
+//
+// Up to kSliceMaxQueries queries: one workgroup does it all.
+__device__ __forceinline__ uint32_t slice_bin(uint32_t key_bits, float kmin, double scale) {
+    const double x = (static_cast<double>(__uint_as_float(key_bits)) - static_cast<double>(kmin)) * scale;
+    const int b = x >= static_cast<double>(kSliceBins - 1) ? kSliceBins - 1 : (x > 0.0 ? static_cast<int>(x) : 0);
+    return static_cast<uint32_t>(kSliceBins - 1 - b);  // largest key first
+}
+
+__device__ __forceinline__ double slice_scale(uint32_t omin, uint32_t omax) {
+    const float kmin = __uint_as_float(key_from_order_bits(omin)), kmax = __uint_as_float(key_from_order_bits(omax));
+    const double range = static_cast<double>(kmax) - static_cast<double>(kmin);
+    return range > 0.0 ? static_cast<double>(kSliceBins - 1) / range : 0.0;
+}
+
 __global__ __launch_bounds__(1024) void fg_slice_order_kernel(uint32_t *state, const uint32_t *keys, int nq,
                                                              uint32_t *order) {
     constexpr int kPerThread = kSliceMaxQueries / 1024;
     __shared__ uint32_t hist[kSliceBins];
     __shared__ uint32_t part[1024];
-    __shared__ uint32_t kmax;
+    __shared__ uint32_t omin, omax;
     const int t = static_cast<int>(threadIdx.x);
     for (int b = t; b < kSliceBins; b += 1024) hist[b] = 0u;
-    if (t == 0) kmax = 0u;
+    if (t == 0) {
+        omin = 0xFFFFFFFFu;
+        omax = 0u;
+    }
     // every key this thread handles, loaded at once (query t + 1024 j)
     uint32_t v[kPerThread];
 #pragma unroll
@@ -65,19 +83,26 @@ __global__ __launch_bounds__(1024) void fg_slice_order_kernel(uint32_t *state, c
         const int q = t + 1024 * j;
         v[j] = q < nq ? keys[q] : kSliceDone;
     }
-    uint32_t m = 0u;
+    uint32_t lo = 0xFFFFFFFFu, hi = 0u;
 #pragma unroll
-    for (int j = 0; j < kPerThread; ++j) m = v[j] != kSliceDone ? max(m, v[j]) : m;
+    for (int j = 0; j < kPerThread; ++j)
+        if (v[j] != kSliceDone) {
+            const uint32_t o = key_order_bits(v[j]);
+            lo = min(lo, o);
+            hi = max(hi, o);
+        }
     __syncthreads();
-    atomicMax(&kmax, m);
+    if (hi >= lo) {
+        atomicMin(&omin, lo);
+        atomicMax(&omax, hi);
+    }
     __syncthreads();
-    const float top = __uint_as_float(kmax);
-    const float scale = top > 0.0f ? static_cast<float>(kSliceBins - 1) / top : 0.0f;
+    const float kmin = __uint_as_float(key_from_order_bits(omin));
+    const double scale = slice_scale(omin, omax);
 #pragma unroll
     for (int j = 0; j < kPerThread; ++j) {
         if (v[j] != kSliceDone) {
-            const int x = static_cast<int>(__uint_as_float(v[j]) * scale);
-            v[j] = static_cast<uint32_t>(kSliceBins - 1 - min(max(x, 0), kSliceBins - 1));  // largest key first
+            v[j] = slice_bin(v[j], kmin, scale);
             atomicAdd(&hist[v[j]], 1u);
         }
     }
@@ -104,6 +129,114 @@ __global__ __launch_bounds__(1024) void fg_slice_order_kernel(uint32_t *state, c
 #pragma unroll
     for (int j = 0; j < kPerThread; ++j)
         if (v[j] != kSliceDone) order[atomicAdd(&hist[v[j]], 1u)] = static_cast<uint32_t>(t + 1024 * j);
+}
+
+// More queries: four steps over chunks of kSliceChunk queries, one workgroup
+// of 256 threads per chunk, through a work area of (2 + kSliceBins) words plus
+// two words per chunk and one per query:
+//   minmax  each chunk's smallest and largest key (order-preserving bits);
+//           the workgroups also clear the global histogram
+//   hist    every workgroup reduces the chunks' extremes, bins its keys
+//           (kept per query) and adds its chunk's histogram to the global one
+//   scan    one workgroup: exclusive scan of the global histogram, the count
+//   scatter each suspended query takes the next place of its bin
+constexpr int kSliceChunk = 4096;
+
+__global__ __launch_bounds__(256) void fg_slice_minmax_kernel(const uint32_t *keys, int nq, uint32_t *ext,
+                                                              uint32_t *ghist, int nchunks) {
+    __shared__ uint32_t lo_s, hi_s;
+    const int t = static_cast<int>(threadIdx.x), c = static_cast<int>(blockIdx.x);
+    for (int b = c * 256 + t; b < kSliceBins; b += nchunks * 256) ghist[b] = 0u;
+    if (t == 0) {
+        lo_s = 0xFFFFFFFFu;
+        hi_s = 0u;
+    }
+    __syncthreads();
+    uint32_t lo = 0xFFFFFFFFu, hi = 0u;
+    const int q1 = min(nq, (c + 1) * kSliceChunk);
+    for (int q = c * kSliceChunk + t; q < q1; q += 256) {
+        const uint32_t k = keys[q];
+        if (k != kSliceDone) {
+            const uint32_t o = key_order_bits(k);
+            lo = min(lo, o);
+            hi = max(hi, o);
+        }
+    }
+    if (hi >= lo) {
+        atomicMin(&lo_s, lo);
+        atomicMax(&hi_s, hi);
+    }
+    __syncthreads();
+    if (t == 0) {
+        ext[2 * c] = lo_s;
+        ext[2 * c + 1] = hi_s;
+    }
+}
+
+__global__ __launch_bounds__(256) void fg_slice_hist_kernel(const uint32_t *keys, int nq, const uint32_t *ext,
+                                                            int nchunks, uint32_t *ghist, uint32_t *qbin) {
+    __shared__ uint32_t hist[kSliceBins];
+    __shared__ uint32_t lo_s, hi_s;
+    const int t = static_cast<int>(threadIdx.x), c = static_cast<int>(blockIdx.x);
+    for (int b = t; b < kSliceBins; b += 256) hist[b] = 0u;
+    if (t == 0) {
+        lo_s = 0xFFFFFFFFu;
+        hi_s = 0u;
+    }
+    __syncthreads();
+    uint32_t lo = 0xFFFFFFFFu, hi = 0u;
+    for (int j = t; j < nchunks; j += 256) {
+        lo = min(lo, ext[2 * j]);
+        hi = max(hi, ext[2 * j + 1]);
+    }
+    atomicMin(&lo_s, lo);
+    atomicMax(&hi_s, hi);
+    __syncthreads();
+    const float kmin = __uint_as_float(key_from_order_bits(lo_s));
+    const double scale = hi_s >= lo_s ? slice_scale(lo_s, hi_s) : 0.0;
+    const int q1 = min(nq, (c + 1) * kSliceChunk);
+    for (int q = c * kSliceChunk + t; q < q1; q += 256) {
+        const uint32_t k = keys[q];
+        uint32_t b = kSliceDone;
+        if (k != kSliceDone) {
+            b = slice_bin(k, kmin, scale);
+            atomicAdd(&hist[b], 1u);
+        }
+        qbin[q] = b;
+    }
+    __syncthreads();
+    for (int b = t; b < kSliceBins; b += 256)
+        if (hist[b]) atomicAdd(&ghist[b], hist[b]);
+}
+
+__global__ __launch_bounds__(1024) void fg_slice_scan_kernel(uint32_t *ghist, uint32_t *state) {
+    __shared__ uint32_t part[1024];
+    const int t = static_cast<int>(threadIdx.x);
+    constexpr int kPer = kSliceBins / 1024;
+    uint32_t loc[kPer], sum = 0u;
+    for (int j = 0; j < kPer; ++j) {
+        loc[j] = sum;
+        sum += ghist[t * kPer + j];
+    }
+    part[t] = sum;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {
+        const uint32_t x = t >= off ? part[t - off] : 0u;
+        __syncthreads();
+        part[t] += x;
+        __syncthreads();
+    }
+    const uint32_t base = part[t] - sum;
+    for (int j = 0; j < kPer; ++j) ghist[t * kPer + j] = base + loc[j];
+    if (t == 1023) state[0] = part[1023];
+}
+
+__global__ __launch_bounds__(256) void fg_slice_scatter_kernel(const uint32_t *qbin, int nq, uint32_t *goff,
+                                                               uint32_t *order) {
+    const int q = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+    if (q >= nq) return;
+    const uint32_t b = qbin[q];
+    if (b != kSliceDone) order[atomicAdd(&goff[b], 1u)] = static_cast<uint32_t>(q);
 }
 
 // ------------------------------------------------------------ test-hook kernels
@@ -478,15 +611,34 @@ int launch_t(const SearchParams &P, hipStream_t stream, int *waves_only = nullpt
 }
 
 // Whether a search may run as two launches (first slice, order, second
-// slice): the L2 metric, a batch the order kernel holds, and searches that
-// reach the suspension point.  slice_fits then asks for the one-wave form and
-// a batch larger than the device holds at once (the last queries to start
-// are the ones that make a launch's tail).  FLASHGANN_SLICE=0 / 1 forces one
-// launch / two launches wherever the form allows them (tests run both).
+// slice): searches that reach the suspension point, with suspended state of
+// at most kSliceMaxBytes (about 400,000 queries at d 128, beam 256).
+// slice_fits then asks for the one-wave form and a batch larger than the
+// device holds at once (the last queries to start are the ones that make a
+// launch's tail).  FLASHGANN_SLICE=0 / 1 forces one launch / two launches
+// wherever the form allows them (tests run both).
 constexpr int kSliceStop = 15;  // the top of the first iteration that rebuilds the visited table
+constexpr uint64_t kSliceMaxBytes = 1ull << 30;
+
+// Words of the two-launch search's buffer: the header, the per-query states,
+// the keys and the order, and above kSliceMaxQueries queries the order
+// step's work area (per-query bins, the histogram, two words per chunk).
+uint64_t slice_buffer_words(const SearchParams &P, uint64_t *states_out, uint64_t *pad_out) {
+    const uint64_t nq = static_cast<uint64_t>(P.nq), pad = (nq + 63u) & ~63ull;
+    const uint64_t states = nq * slice_words(static_cast<uint32_t>(P.pbeam), static_cast<uint32_t>(P.padded_dim));
+    uint64_t words = kSliceHeader + states + 2u * pad;
+    if (nq > static_cast<uint64_t>(kSliceMaxQueries)) {
+        const uint64_t chunks = (nq + kSliceChunk - 1) / kSliceChunk;
+        words += pad + kSliceBins + 2u * chunks;
+    }
+    if (states_out) *states_out = states;
+    if (pad_out) *pad_out = pad;
+    return words;
+}
+
 bool slice_wanted(const SearchParams &P) {
-    if (P.nq < 1 || P.nq > kSliceMaxQueries || P.max_iter <= kSliceStop || P.use_ip) return false;
-    return true;
+    if (P.nq < 1 || P.max_iter <= kSliceStop) return false;
+    return slice_buffer_words(P, nullptr, nullptr) * 4u <= kSliceMaxBytes;
 }
 
 // slice_wanted's answer for a batch whose form is known: the one-wave form,
@@ -513,11 +665,14 @@ int launch(fg_index *ix, const SearchParams &P0, hipStream_t stream, bool may_sl
         if (int rc = launch_t<false>(P0, stream, &waves, false, &resident)) return rc;
         if (slice_fits(P0, waves, resident)) {
             // one buffer: header (word 0: the count of suspended queries), the
-            // per-query states, the keys, the order
-            const uint64_t nq = static_cast<uint64_t>(P0.nq), pad = (nq + 63u) & ~63ull;
-            const uint64_t states = nq * slice_words(static_cast<uint32_t>(P0.pbeam));
-            const uint64_t words = kSliceHeader + states + 2u * pad;
-            if (int rc = ensure(reinterpret_cast<void **>(&ix->d_slice), &ix->slice_cap, words * 4u)) return rc;
+            // per-query states, the keys, the order (and the order step's work
+            // area).  If it cannot be allocated, the search makes one launch.
+            uint64_t states = 0, pad = 0;
+            const uint64_t words = slice_buffer_words(P0, &states, &pad);
+            if (ensure(reinterpret_cast<void **>(&ix->d_slice), &ix->slice_cap, words * 4u) != FG_OK) {
+                (void)hipGetLastError();
+                return launch_t<false>(P0, stream, nullptr, true);
+            }
             if (!ix->slice_done) FG_HIP(hipEventCreateWithFlags(&ix->slice_done, hipEventDisableTiming), "event");
             // a sliced search on another stream may still use the buffer
             if (ix->slice_pending && ix->slice_stream != stream)
@@ -532,7 +687,19 @@ int launch(fg_index *ix, const SearchParams &P0, hipStream_t stream, bool may_sl
             P.slice_suspend = kSliceStop;
             P.slice_resume = 0;
             if (int rc = launch_t<false>(P, stream, nullptr, true)) return rc;
-            hipLaunchKernelGGL(fg_slice_order_kernel, dim3(1), dim3(1024), 0, stream, state, keys, P0.nq, order);
+            if (P0.nq <= kSliceMaxQueries) {
+                hipLaunchKernelGGL(fg_slice_order_kernel, dim3(1), dim3(1024), 0, stream, state, keys, P0.nq, order);
+            } else {
+                const int chunks = (P0.nq + kSliceChunk - 1) / kSliceChunk;
+                uint32_t *qbin = order + pad, *ghist = qbin + pad, *ext = ghist + kSliceBins;
+                hipLaunchKernelGGL(fg_slice_minmax_kernel, dim3(chunks), dim3(256), 0, stream, keys, P0.nq, ext, ghist,
+                                   chunks);
+                hipLaunchKernelGGL(fg_slice_hist_kernel, dim3(chunks), dim3(256), 0, stream, keys, P0.nq, ext, chunks,
+                                   ghist, qbin);
+                hipLaunchKernelGGL(fg_slice_scan_kernel, dim3(1), dim3(1024), 0, stream, ghist, state);
+                hipLaunchKernelGGL(fg_slice_scatter_kernel, dim3((P0.nq + 255) / 256), dim3(256), 0, stream, qbin,
+                                   P0.nq, ghist, order);
+            }
             FG_HIP(hipGetLastError(), "order kernel launch");
             P.slice_resume = kSliceStop;
             P.slice_suspend = 0;

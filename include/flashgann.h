@@ -169,13 +169,15 @@ int fg_search_waves(fg_index *index, uint32_t nq, uint32_t K, uint32_t beam);
 /* Kernel launches (1 or 2) that fg_search / fg_search_device make for a
  * search of nq queries at this K and beam.  Two when the batch, in the
  * one-wave form, holds more queries than the device runs at once (6,144 at
- * d 128, degree 32, beam 256) and at most 16,384, with the L2 metric: every
- * query first runs to iteration 15 and an
- * unfinished one keeps its state in memory the index holds, then the
- * unfinished queries resume in a second launch, those with the largest best
- * distance so far first, so the longest searches start early.  Results are
- * identical either way; FLASHGANN_SLICE=0/1 in the environment forces one
- * launch / two wherever the form allows.  Device searches on one index that
+ * d 128, degree 32, beam 256), for either metric, while the suspended state
+ * stays within 1 GiB (about 400,000 queries at d 128, beam 256): every query
+ * first runs to iteration 15 and an unfinished one keeps its state (beam,
+ * candidates, controller, counters and prepared query) in memory the index
+ * holds, then the unfinished queries resume in a second launch, those with
+ * the largest best distance so far first, so the longest searches start
+ * early.  If that memory cannot be allocated the search makes one launch.
+ * Results are identical either way; FLASHGANN_SLICE=0/1 in the environment
+ * forces one launch / two wherever the form allows.  Device searches on one index that
  * overlap on different streams run one after another when they take two
  * launches.  fg_search_stream, fg_search_noalloc and a device search on a
  * stream that is being captured into a graph always make one.

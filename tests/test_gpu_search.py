@@ -348,20 +348,23 @@ def test_search_waves_reports_the_form(gpu_available, monkeypatch):
     ix.close()
 
 
-@pytest.mark.parametrize("dim,degree,kind,K,beam", [(128, 32, "int", 100, 256), (128, 32, "int", 10, 64),
-                                                    (96, 16, "unit", 100, 200), (96, 32, "unit", 10, 32),
-                                                    (40, 8, "int", 10, 128), (128, 32, "int", 100, 512),
-                                                    (96, 16, "unit", 100, 384), (128, 32, "int", 100, 1000),
-                                                    (960, 32, "box", 100, 384)])
-def test_two_launch_search_equals_one_launch(gpu_available, monkeypatch, dim, degree, kind, K, beam):
+@pytest.mark.parametrize("dim,degree,kind,K,beam,ip", [(128, 32, "int", 100, 256, False), (128, 32, "int", 10, 64, False),
+                                                       (96, 16, "unit", 100, 200, False), (96, 32, "unit", 10, 32, False),
+                                                       (40, 8, "int", 10, 128, False), (128, 32, "int", 100, 512, False),
+                                                       (96, 16, "unit", 100, 384, False), (128, 32, "int", 100, 1000, False),
+                                                       (960, 32, "box", 100, 384, False), (96, 32, "unit", 100, 256, True),
+                                                       (128, 32, "unit", 100, 512, True), (960, 32, "box", 100, 384, True)])
+def test_two_launch_search_equals_one_launch(gpu_available, monkeypatch, dim, degree, kind, K, beam, ip):
     """The two-launch search (every query suspended at the top of iteration
-    15 with its beam, candidates, controller and counters kept in HBM, then
-    resumed in an order of its own) returns the ids and work counters of the
-    one-launch search and of the oracle, with and without counters."""
+    15 with its beam, candidates, controller, counters and prepared query
+    kept in HBM, then resumed in an order of its own) returns the ids and
+    work counters of the one-launch search and of the oracle, with and
+    without counters, for both metrics (inner-product distances are
+    negative: the ordering key is the signed best distance)."""
     from flashgann_amd import Index
     from oracle import oracle as O
-    cb, q, _ = small_index(n=3000, nq=300, dim=dim, degree=degree, kind=kind, comps=16)
-    ix = Index.from_codebook(cb)
+    cb, q, _ = small_index(n=3000, nq=300, dim=dim, degree=degree, kind=kind, comps=16, use_ip=ip)
+    ix = Index.from_codebook(cb, metric=1 if ip else 0)
     monkeypatch.setenv("FLASHGANN_TEAM", "0")
     monkeypatch.setenv("FLASHGANN_SLICE", "0")
     ids1, _, cnt1 = ix.search(q, K, beam, counters=True)
@@ -372,7 +375,7 @@ def test_two_launch_search_equals_one_launch(gpu_available, monkeypatch, dim, de
     assert (cnt1[:, 0] > 15).any()  # some queries are suspended and resumed
     assert np.array_equal(ids2, ids1) and np.array_equal(cnt2, cnt1)
     assert np.array_equal(ids3, ids1)
-    rids, rcnt = O.OracleIndex.from_codebook(cb).search(q, K, beam)
+    rids, rcnt = O.OracleIndex.from_codebook(cb, use_ip=ip).search(q, K, beam)
     assert np.array_equal(ids2, rids)
     assert np.array_equal(cnt2, rcnt.view(np.uint32).reshape(-1, 6))
 
@@ -452,9 +455,10 @@ def test_search_launches_reports_the_schedule(gpu_available, monkeypatch):
         else:
             hi = mid
     assert lo % cus == 0 and 2 <= lo // cus <= 64, (lo, cus)
-    assert all(ix.search_launches(n, 100, 256) == 2 for n in (lo + 1, lo + 1000, 16384))
+    assert all(ix.search_launches(n, 100, 256) == 2 for n in (lo + 1, lo + 1000, 16384, 16385, 100000))
     assert ix.search_launches(16, 10, 64) == 1        # the team form
-    assert ix.search_launches(16385, 100, 256) == 1   # above the order kernel's 16,384
+    # 200,000 queries at beam 1024 would keep 1.7 GB of state: one launch
+    assert ix.search_launches(200000, 100, 1024) == 1
     monkeypatch.setenv("FLASHGANN_SLICE", "0")
     assert ix.search_launches(16384, 100, 256) == 1
     monkeypatch.setenv("FLASHGANN_SLICE", "1")
@@ -462,13 +466,16 @@ def test_search_launches_reports_the_schedule(gpu_available, monkeypatch):
     ix.close()
 
 
-@pytest.mark.parametrize("nq,beam", [(4000, 256), (4000, 384), (16384, 256), (16384, 512)])
+@pytest.mark.parametrize("nq,beam", [(4000, 256), (4000, 384), (16384, 256), (16384, 512), (16385, 256),
+                                     (30000, 384)])
 def test_two_launch_search_large_batches(gpu_available, monkeypatch, nq, beam):
     """Forced two-launch searches over batches that use every part of the
-    order kernel (queries past its first 1,024 slots, and its 16,384-query
-    maximum): ids and counters equal the one-launch search's, and on the
-    distinct queries the oracle's.  The batch repeats 300 queries, so each
-    distinct query is checked at many positions of the order."""
+    order step: queries past the one-workgroup kernel's first 1,024 slots and
+    at its 16,384-query maximum, then the multi-workgroup path (chunks of
+    4,096, a last partial chunk).  Ids and counters equal the one-launch
+    search's, and on the distinct queries the oracle's.  The batch repeats
+    300 queries, so each distinct query is checked at many positions of the
+    order."""
     from flashgann_amd import Index
     from oracle import oracle as O
     cb, q, _ = small_index(n=3000, nq=300)
