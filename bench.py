@@ -76,10 +76,11 @@ def main() -> int:
                          "beam of --beams for recall, QPS and oracle parity; the headline is the first beam that "
                          "reaches the target either way)")
     ap.add_argument("--full-sweep", action="store_true", help="(the default; kept for old command lines)")
-    ap.add_argument("--graph", type=str, default="mixed", choices=("mixed", "rng"),
+    ap.add_argument("--graph", type=str, default="mixed", choices=("mixed", "rng", "connected"),
                     help="mixed: RNG-pruned k-NN edges plus degree/4 seeded random long links, empty slots to "
                          "random targets (the default); rng: RNG-pruned k-NN edges only, empty slots backfilled "
-                         "from the k-NN candidates")
+                         "from the k-NN candidates; connected: rng plus the links that make every node reachable "
+                         "from the entry point (NSG-style repair, in backfilled or empty slots)")
     ap.add_argument("--alpha", type=float, default=1.0,
                     help="RNG prune slack: drop a candidate v when a kept w has alpha^2 d(w,v) < d(u,v)")
     ap.add_argument("--random-links", type=int, default=-1,
@@ -87,8 +88,9 @@ def main() -> int:
     ap.add_argument("--candidates", type=int, default=0, help="k-NN candidates per node before the prune "
                     "(default: 2*degree)")
     ap.add_argument("--no-rng-graph", action="store_true",
-                    help="skip the side measurement on the RNG-only graph (default: C2 with the mixed graph also "
-                         "sweeps the RNG-only graph and reports it in config.rng_graph)")
+                    help="skip the side measurements on the RNG-only and connected graphs (default: C2 with the "
+                         "mixed graph also sweeps them and reports them in config.rng_graph and "
+                         "config.connected_graph)")
     ap.add_argument("--parity-sample", type=int, default=500,
                     help="queries per swept beam whose GPU ids are compared with the CPU oracle's")
     ap.add_argument("--traffic", type=str, default=os.path.join(ROOT, "profiles", "search_c2_traffic.json"))
@@ -155,8 +157,11 @@ def main() -> int:
         graph_kw_large = {}
     use_ip = args.metric == "ip"
     tag = (f"{args.config}_{args.n}_{args.nq}_{args.components}_{args.degree}_{args.K}" + ("_ip" if use_ip else "")
-           + ("_rng" if args.graph == "rng" else ""))
-    graph_kw = dict(random_links=0, fill_random=False) if args.graph == "rng" else {}
+           + {"mixed": "", "rng": "_rng", "connected": "_conn"}[args.graph])
+    build_stats = {}
+    graph_kw = (dict(random_links=0, fill_random=False) if args.graph == "rng" else
+                dict(random_links=0, fill_random=False, connect=True, stats=build_stats)
+                if args.graph == "connected" else {})
     if args.random_links >= 0 and args.graph == "mixed":
         graph_kw["random_links"] = args.random_links
     graph_kw["alpha"] = args.alpha
@@ -424,49 +429,65 @@ def main() -> int:
         log(f"cpu oracle: {sample / cpu_s:.0f} QPS on {threads} threads; ids identical on {same * 100:.2f}% "
             f"of the sample")
 
-    # Side measurement (never `value`): the same data on an RNG-only graph
-    # (RNG-pruned k-NN edges, no random long links), swept over the same beams.
-    rng_graph = None
+    # Side measurements (never `value`): the same data and queries on the
+    # RNG-only graph (RNG-pruned k-NN edges, no random long links) and on the
+    # connected graph (the same edges plus the links that make every node
+    # reachable from the entry point), swept over the same beams.
+    side = {}
     if args.config == "c2" and args.graph == "mixed" and not args.no_rng_graph and not use_ip:
-        t0 = time.time()
-        cb_r = builder.build_codebook(base, args.degree, signs, device=dev, random_links=0, fill_random=False)
-        log(f"RNG-only graph built in {time.time() - t0:.1f}s")
-        ix_r = fg.Index.from_codebook(cb_r)
-        oix_r = O.OracleIndex.from_codebook(cb_r) if oix is not None else None
-        rows = []
-        for beam in beams:
-            ix_r.search_device(dq.data_ptr(), args.nq, args.K, beam, dres.data_ptr(), 0, stream.cuda_stream)
-            torch.cuda.synchronize()
-            ms = []
-            for _ in range(3):
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record(stream)
-                ix_r.search_device(dq.data_ptr(), args.nq, args.K, beam, dres.data_ptr(), 0, stream.cuda_stream)
-                e1.record(stream)
+        for sname, skw, sdesc in (
+                ("rng_graph", dict(random_links=0, fill_random=False),
+                 "RNG-pruned k-NN edges only (random_links=0, empty slots backfilled from the k-NN candidates)"),
+                ("connected_graph", dict(random_links=0, fill_random=False, connect=True),
+                 "RNG-pruned k-NN edges, empty slots backfilled from the k-NN candidates, then the links that make "
+                 "every node reachable from the entry point (the unreached node nearest the entry linked from its "
+                 "nearest reached node, into a backfilled or empty slot, repeated)")):
+            t0 = time.time()
+            sst = {}
+            cb_r = builder.build_codebook(base, args.degree, signs, device=dev, stats=sst, **skw)
+            log(f"{sname} built in {time.time() - t0:.1f}s" +
+                (f" ({sst['connect_links']} links added)" if "connect_links" in sst else ""))
+            ix_r = fg.Index.from_codebook(cb_r)
+            oix_r = O.OracleIndex.from_codebook(cb_r) if oix is not None else None
+            rows = []
+            for beam in beams:
+                for _ in range(4):
+                    ix_r.search_device(dq.data_ptr(), args.nq, args.K, beam, dres.data_ptr(), 0, stream.cuda_stream)
                 torch.cuda.synchronize()
-                ms.append(e0.elapsed_time(e1))
-            rids = dres.cpu().numpy().view(np.uint32)
-            row = {"beam": beam, "recall": round(float(recall_of(rids)), 5),
-                   "qps": round(args.nq / (min(ms) / 1e3), 1), "kernel_ms": round(min(ms), 4)}
-            if oix_r is not None and args.parity_sample > 0:
-                m = min(args.nq, args.parity_sample)
-                pids, _ = oix_r.search(queries[:m], args.K, beam, threads=threads)
-                row["oracle_ids_identical"] = float((pids == rids[:m]).all(1).mean())
-                row["oracle_sample"] = m
-            rows.append(row)
-            log(f"RNG-only graph, beam {beam}: recall@{args.K} {row['recall']:.4f}, {row['qps']:.0f} QPS"
-                + (f", ids identical to the oracle on {row['oracle_ids_identical'] * 100:.2f}% of "
-                   f"{row['oracle_sample']}" if "oracle_sample" in row else ""))
-        first = next((r["beam"] for r in rows if r["recall"] >= args.target_recall), None)
-        rng_graph = {"graph": "RNG-pruned k-NN edges only (random_links=0, empty slots backfilled from the "
-                              "k-NN candidates)", "beam_sweep": rows, "first_beam_reaching_target": first}
-        ix_r.close()
-        del cb_r, oix_r
+                ms = []
+                for _ in range(5):
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record(stream)
+                    ix_r.search_device(dq.data_ptr(), args.nq, args.K, beam, dres.data_ptr(), 0, stream.cuda_stream)
+                    e1.record(stream)
+                    torch.cuda.synchronize()
+                    ms.append(e0.elapsed_time(e1))
+                rids = dres.cpu().numpy().view(np.uint32)
+                row = {"beam": beam, "recall": round(float(recall_of(rids)), 5),
+                       "qps": round(args.nq / (float(np.median(ms)) / 1e3), 1), "kernel_ms": round(float(np.median(ms)), 4)}
+                if oix_r is not None and args.parity_sample > 0:
+                    m = min(args.nq, args.parity_sample)
+                    pids, _ = oix_r.search(queries[:m], args.K, beam, threads=threads)
+                    row["oracle_ids_identical"] = float((pids == rids[:m]).all(1).mean())
+                    row["oracle_sample"] = m
+                rows.append(row)
+                log(f"{sname}, beam {beam}: recall@{args.K} {row['recall']:.4f}, {row['qps']:.0f} QPS"
+                    + (f", ids identical to the oracle on {row['oracle_ids_identical'] * 100:.2f}% of "
+                       f"{row['oracle_sample']}" if "oracle_sample" in row else ""))
+            first = next((r["beam"] for r in rows if r["recall"] >= args.target_recall), None)
+            side[sname] = {"graph": sdesc, "beam_sweep": rows, "first_beam_reaching_target": first}
+            if "connect_links" in sst:
+                side[sname]["links_added"] = sst["connect_links"]
+            ix_r.close()
+            del cb_r, oix_r
 
     knn_desc = ("k-NN candidates searched in the 2 nearest of ~n/2500 k-means cells" if large
                 else "exact k-NN candidates")
     graph_desc = (f"RNG-pruned k-NN edges only ({knn_desc}), empty slots backfilled from the candidates"
-                  if args.graph == "rng"
+                  if args.graph == "rng" else
+                  f"RNG-pruned k-NN edges ({knn_desc}), empty slots backfilled from the candidates, plus "
+                  f"{build_stats.get('connect_links')} links that make every node reachable from the entry point"
+                  if args.graph == "connected"
                   else f"RNG-pruned k-NN edges ({knn_desc}, {args.candidates or 2 * args.degree} per node"
                        + (f", alpha {args.alpha}" if args.alpha != 1.0 else "")
                        + f") plus {args.random_links if args.random_links >= 0 else args.degree // 4} seeded "
@@ -495,7 +516,7 @@ def main() -> int:
                    "lds_bytes": fg.lds_bytes(dim, chosen, args.degree),
                    "waves_per_query": index.search_waves(args.nq, args.K, chosen),
                    "launches_per_search": index.search_launches(args.nq, args.K, chosen), "graph": graph_desc,
-                   "rng_graph": rng_graph},
+                   "rng_graph": side.get("rng_graph"), "connected_graph": side.get("connected_graph")},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_source,
                      "kernel": "fg_search_kernel", "kernel_ms": round(kernel_ms, 4),

@@ -270,15 +270,77 @@ def hadamard_rotation(signs: np.ndarray, device) -> torch.Tensor:
     return (h * torch.as_tensor(signs, dtype=torch.float64)[None, :]).to(device)
 
 
+def _reach(nbrs: torch.Tensor, reached: torch.Tensor, start: torch.Tensor) -> int:
+    """Marks every node reachable from the `start` ids over the out-edges of
+    nbrs (-1 = none) in `reached` (bool, in place; nodes already marked are
+    not expanded again).  Returns the number of newly marked nodes."""
+    frontier = start[~reached[start]]
+    reached[frontier] = True
+    added = int(frontier.numel())
+    while frontier.numel():
+        nb = nbrs[frontier].reshape(-1)
+        nb = nb[nb >= 0]
+        nb = torch.unique(nb[~reached[nb]])
+        reached[nb] = True
+        added += int(nb.numel())
+        frontier = nb
+    return added
+
+
+def connect_graph(x: torch.Tensor, nbrs: torch.Tensor, fixed: torch.Tensor, entry: int,
+                  verbose: bool = False) -> tuple[torch.Tensor, int]:
+    """Makes every node reachable from `entry` by adding the fewest links the
+    greedy repair finds, in the manner of NSG's spanning step (Fu et al.,
+    VLDB 2019): while some node is unreached, the unreached node nearest the
+    entry point is linked from its nearest reached node that has a free slot,
+    and everything reachable from it is marked.  A free slot is one that is
+    empty or holds an edge not in `fixed` (bool, same shape as nbrs: the
+    RNG-pruned edges, which are never replaced); the link takes the last such
+    slot.  Returns (nbrs with the links, number of links added)."""
+    n = x.shape[0]
+    dev = x.device
+    nbrs = nbrs.clone()
+    free = ~fixed | (nbrs < 0)
+    reached = torch.zeros(n, dtype=torch.bool, device=dev)
+    _reach(nbrs, reached, torch.tensor([entry], device=dev))
+    xn = _sqnorm(x)
+    de = _sqnorm(x - x[entry][None, :])  # distance of every node to the entry point
+    links = 0
+    t0 = time.time()
+    while not bool(reached.all()):
+        # the unreached node nearest the entry point
+        u = int(torch.argmin(torch.where(reached, torch.full_like(de, float("inf")), de)).item())
+        d = xn + xn[u] - 2.0 * (x @ x[u])
+        has_free = free.any(1)
+        d = torch.where(reached & has_free, d, torch.full_like(d, float("inf")))
+        v = int(torch.argmin(d).item())
+        if not bool(torch.isfinite(d[v])):
+            raise RuntimeError("connect_graph: no reached node has a free slot")
+        slot = int(torch.nonzero(free[v]).max().item())
+        nbrs[v, slot] = u
+        free[v, slot] = False
+        links += 1
+        _reach(nbrs, reached, torch.tensor([u], device=dev))
+        if verbose and links % 200 == 0:
+            print(f"[builder] connect: {links} links, {int(reached.sum())}/{n} reachable "
+                  f"({time.time() - t0:.1f}s)", flush=True)
+    return nbrs, links
+
+
 def build_graph(x: torch.Tensor, degree: int, random_links: int | None = None,
                 seed: int = 0x5EED, alpha: float = 1.0, candidates: int | None = None,
                 fill_random: bool = True, verbose: bool = False, dist_block_elems: int = 1 << 30,
-                knn_method: str = "exact") -> torch.Tensor:
+                knn_method: str = "exact", connect: bool = False, stats: dict | None = None) -> torch.Tensor:
     """Returns (n, degree) int64 neighbour ids (-1 = padding).  The final
     neighbour distances are gathered in row blocks of at most
     `dist_block_elems` floats.  knn_method "exact" takes the candidates from
     knn(), "partitioned" from knn_partitioned() (sets of millions of
-    high-dimensional points, where the exact search is out of reach)."""
+    high-dimensional points, where the exact search is out of reach).
+    connect=True (with random_links=0): the RNG-pruned k-NN edges are all
+    kept, the slots they leave are backfilled from the k-NN candidates, and
+    connect_graph() then replaces backfilled slots (or fills empty ones) with
+    the links that make every node reachable from the entry point (the node
+    nearest the mean); stats, if given, receives the number of links."""
     n = x.shape[0]
     dev = x.device
     kc = min(candidates or 2 * degree, n - 1)
@@ -312,6 +374,16 @@ def build_graph(x: torch.Tensor, degree: int, random_links: int | None = None,
         parts.append(_first_unique(r, nfill))
     parts.append(cand)
     merged = _first_unique(torch.cat(parts, 1), degree)
+    if connect:
+        if nr:
+            raise ValueError("connect=True builds on the RNG-pruned graph: use random_links=0")
+        # the RNG-kept edges are the first entries of each list (local is in
+        # candidate order and merged starts with it)
+        fixed = torch.arange(degree, device=dev)[None, :] < local_keep.sum(1, keepdim=True).clamp(max=local_cap)
+        fixed &= merged >= 0
+        merged, links = connect_graph(x, merged, fixed, entry_point(x), verbose=verbose)
+        if stats is not None:
+            stats["connect_links"] = links
     # sort each list by (distance, id)
     big = torch.iinfo(torch.int64).max
     valid = merged >= 0
@@ -421,13 +493,16 @@ def entry_point(x: torch.Tensor, chunk: int = 1 << 20) -> int:
 def build_codebook(base, degree: int, signs: np.ndarray, use_ip: bool = False,
                    device: str | torch.device = "cpu", random_links: int | None = None,
                    alpha: float = 1.0, candidates: int | None = None, fill_random: bool = True,
-                   store_entry: bool = True, verbose: bool = False, knn_method: str = "exact") -> Codebook:
+                   store_entry: bool = True, verbose: bool = False, knn_method: str = "exact",
+                   connect: bool = False, stats: dict | None = None) -> Codebook:
     """Builds a complete codebook in the reference layout.  `base` is a numpy
     array or a float32 tensor (already on `device` for sets too large to
-    hold twice)."""
+    hold twice).  connect=True: the RNG-pruned graph made reachable from the
+    entry point (build_graph)."""
     x = _as_device(base, device)
     nbrs = build_graph(x, degree, random_links=random_links, alpha=alpha, candidates=candidates,
-                       fill_random=fill_random, verbose=verbose, knn_method=knn_method)
+                       fill_random=fill_random, verbose=verbose, knn_method=knn_method, connect=connect,
+                       stats=stats)
     return codebook_from_graph(x, nbrs, signs, use_ip=use_ip, device=device, store_entry=store_entry,
                                verbose=verbose)
 

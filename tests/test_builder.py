@@ -225,3 +225,47 @@ def test_ground_truth_recheck():
         far = np.argsort(score, axis=1)[:, -20:]
         bad[::4] = far[::4]
         assert builder.check_ground_truth(base, q, bad, sample=40, use_ip=ip) == 10
+
+
+def test_connected_graph_keeps_rng_edges_and_reaches_every_node():
+    """The connect=True recipe on a 64-component integer mixture, where the
+    bare RNG-pruned k-NN graph reaches few nodes from the entry point: every
+    node becomes reachable (BFS over the out-edges), every RNG-kept edge of
+    every node is still in its list, the links added are few (one or a few
+    per component), lists stay sorted by distance, and the oracle's recall on
+    the repaired graph far exceeds the bare graph's (one link per component
+    makes each component reachable, not easy to reach: at beam 64 the search
+    finds the query's component about half the time)."""
+    import torch
+
+    from flashgann_amd import builder, datasets
+    base, q = datasets.integer_mixture(12000, 100, 128, 64, config=1)
+    x = torch.as_tensor(base)
+    n = base.shape[0]
+    entry = builder.entry_point(x)
+    bare = builder.build_graph(x, 32, random_links=0, fill_random=False)
+    st = {}
+    g = builder.build_graph(x, 32, random_links=0, fill_random=False, connect=True, stats=st)
+    reach = lambda gr: int(builder._reach(gr, torch.zeros(n, dtype=torch.bool), torch.tensor([entry])))
+    assert reach(bare) < n // 4
+    assert reach(g) == n
+    assert 0 < st["connect_links"] <= 3 * 64
+    # rows differ from the bare graph only by the links
+    assert int((bare != g).any(1).sum()) <= st["connect_links"]
+    # every RNG-kept candidate is still a neighbour
+    cand, cd = builder.knn(x, 64)
+    keep = builder._prune(cand, cd, x, 32)
+    for i in range(0, n, 7):
+        kept = set(cand[i][keep[i]].tolist())
+        assert kept <= set(g[i].tolist()), i
+    gn = g.numpy()
+    d = ((base[gn[:300]] - base[:300, None, :]) ** 2).sum(-1)
+    assert (np.diff(d, axis=1) >= 0).all()
+    sig = datasets.signs_for(128, 1)
+    gt = builder.ground_truth(base, q, 10)
+    rec = []
+    for gr in (bare, g):
+        cb = builder.codebook_from_graph(base, gr, sig)
+        ids, _ = O.OracleIndex.from_codebook(cb).search(q, 10, 64)
+        rec.append(O.recall(ids, gt, 10))
+    assert rec[0] < 0.1 and rec[1] > 0.4 and rec[1] > 5 * rec[0], rec
