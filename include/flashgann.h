@@ -175,7 +175,9 @@ int fg_search_waves(fg_index *index, uint32_t nq, uint32_t K, uint32_t beam);
  * candidates, controller, counters and prepared query) in memory the index
  * holds, then the unfinished queries resume in a second launch, those with
  * the largest best distance so far first, so the longest searches start
- * early.  If that memory cannot be allocated the search makes one launch.
+ * early.  The first such search of a larger batch allocates that memory,
+ * which synchronises the device; if it cannot be allocated the search makes
+ * one launch.
  * Results are identical either way; FLASHGANN_SLICE=0/1 in the environment
  * forces one launch / two wherever the form allows.  Device searches on one index that
  * overlap on different streams run one after another when they take two
