@@ -64,18 +64,57 @@ __device__ __forceinline__ double slice_scale(uint32_t omin, uint32_t omax) {
     return range > 0.0 ? static_cast<double>(kSliceBins - 1) / range : 0.0;
 }
 
+__device__ __forceinline__ uint32_t wave_umin(uint32_t v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = min(v, xshfl(v, m));
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = max(v, xshfl(v, m));
+    return v;
+}
+
+// Exclusive scan of the kSliceBins counts in[] into out[] (in == out allowed)
+// by a workgroup of 1024 threads, four consecutive bins per thread: a scan
+// within each wave by shuffles, then each wave adds the totals of the waves
+// before it (wsum: 16 words of LDS).  Returns the sum of all bins.
+__device__ __forceinline__ uint32_t block_scan_bins(const uint32_t *in, uint32_t *out, uint32_t *wsum) {
+    constexpr int kPer = kSliceBins / 1024;
+    const int t = static_cast<int>(threadIdx.x), lane = t & 63, w = t >> 6;
+    uint32_t loc[kPer], sum = 0u;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        loc[j] = sum;
+        sum += in[t * kPer + j];
+    }
+    uint32_t inc = sum;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t x = __shfl_up(inc, d);
+        if (lane >= d) inc += x;
+    }
+    if (lane == 63) wsum[w] = inc;
+    __syncthreads();
+    uint32_t base = inc - sum, total = 0u;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t x = wsum[i];
+        base += i < w ? x : 0u;
+        total += x;
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) out[t * kPer + j] = base + loc[j];
+    return total;
+}
+
 __global__ __launch_bounds__(1024) void fg_slice_order_kernel(uint32_t *state, const uint32_t *keys, int nq,
                                                              uint32_t *order) {
     constexpr int kPerThread = kSliceMaxQueries / 1024;
     __shared__ uint32_t hist[kSliceBins];
-    __shared__ uint32_t part[1024];
-    __shared__ uint32_t omin, omax;
-    const int t = static_cast<int>(threadIdx.x);
+    __shared__ uint32_t wlo[16], whi[16], wsum[16];
+    const int t = static_cast<int>(threadIdx.x), lane = t & 63, w = t >> 6;
     for (int b = t; b < kSliceBins; b += 1024) hist[b] = 0u;
-    if (t == 0) {
-        omin = 0xFFFFFFFFu;
-        omax = 0u;
-    }
     // every key this thread handles, loaded at once (query t + 1024 j)
     uint32_t v[kPerThread];
 #pragma unroll
@@ -91,12 +130,19 @@ __global__ __launch_bounds__(1024) void fg_slice_order_kernel(uint32_t *state, c
             lo = min(lo, o);
             hi = max(hi, o);
         }
-    __syncthreads();
-    if (hi >= lo) {
-        atomicMin(&omin, lo);
-        atomicMax(&omax, hi);
+    lo = wave_umin(lo);
+    hi = wave_umax(hi);
+    if (lane == 0) {
+        wlo[w] = lo;
+        whi[w] = hi;
     }
     __syncthreads();
+    uint32_t omin = wlo[0], omax = whi[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) {
+        omin = min(omin, wlo[i]);
+        omax = max(omax, whi[i]);
+    }
     const float kmin = __uint_as_float(key_from_order_bits(omin));
     const double scale = slice_scale(omin, omax);
 #pragma unroll
@@ -107,24 +153,8 @@ __global__ __launch_bounds__(1024) void fg_slice_order_kernel(uint32_t *state, c
         }
     }
     __syncthreads();
-    // exclusive scan: four bins per thread, then the 1024 partial sums
-    constexpr int kPer = kSliceBins / 1024;
-    uint32_t loc[kPer], sum = 0u;
-    for (int j = 0; j < kPer; ++j) {
-        loc[j] = sum;
-        sum += hist[t * kPer + j];
-    }
-    part[t] = sum;
-    __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {
-        const uint32_t x = t >= off ? part[t - off] : 0u;
-        __syncthreads();
-        part[t] += x;
-        __syncthreads();
-    }
-    const uint32_t base = part[t] - sum;
-    for (int j = 0; j < kPer; ++j) hist[t * kPer + j] = base + loc[j];
-    if (t == 1023) state[0] = part[1023];
+    const uint32_t total = block_scan_bins(hist, hist, wsum);
+    if (t == 0) state[0] = total;
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < kPerThread; ++j)
@@ -162,7 +192,9 @@ __global__ __launch_bounds__(256) void fg_slice_minmax_kernel(const uint32_t *ke
             hi = max(hi, o);
         }
     }
-    if (hi >= lo) {
+    lo = wave_umin(lo);
+    hi = wave_umax(hi);
+    if ((t & 63) == 0 && hi >= lo) {
         atomicMin(&lo_s, lo);
         atomicMax(&hi_s, hi);
     }
@@ -189,8 +221,12 @@ __global__ __launch_bounds__(256) void fg_slice_hist_kernel(const uint32_t *keys
         lo = min(lo, ext[2 * j]);
         hi = max(hi, ext[2 * j + 1]);
     }
-    atomicMin(&lo_s, lo);
-    atomicMax(&hi_s, hi);
+    lo = wave_umin(lo);
+    hi = wave_umax(hi);
+    if ((t & 63) == 0) {
+        atomicMin(&lo_s, lo);
+        atomicMax(&hi_s, hi);
+    }
     __syncthreads();
     const float kmin = __uint_as_float(key_from_order_bits(lo_s));
     const double scale = hi_s >= lo_s ? slice_scale(lo_s, hi_s) : 0.0;
@@ -210,25 +246,9 @@ __global__ __launch_bounds__(256) void fg_slice_hist_kernel(const uint32_t *keys
 }
 
 __global__ __launch_bounds__(1024) void fg_slice_scan_kernel(uint32_t *ghist, uint32_t *state) {
-    __shared__ uint32_t part[1024];
-    const int t = static_cast<int>(threadIdx.x);
-    constexpr int kPer = kSliceBins / 1024;
-    uint32_t loc[kPer], sum = 0u;
-    for (int j = 0; j < kPer; ++j) {
-        loc[j] = sum;
-        sum += ghist[t * kPer + j];
-    }
-    part[t] = sum;
-    __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {
-        const uint32_t x = t >= off ? part[t - off] : 0u;
-        __syncthreads();
-        part[t] += x;
-        __syncthreads();
-    }
-    const uint32_t base = part[t] - sum;
-    for (int j = 0; j < kPer; ++j) ghist[t * kPer + j] = base + loc[j];
-    if (t == 1023) state[0] = part[1023];
+    __shared__ uint32_t wsum[16];
+    const uint32_t total = block_scan_bins(ghist, ghist, wsum);
+    if (threadIdx.x == 0) state[0] = total;
 }
 
 __global__ __launch_bounds__(256) void fg_slice_scatter_kernel(const uint32_t *qbin, int nq, uint32_t *goff,
