@@ -20,19 +20,24 @@
  *                                raw = sum_i b_i q_i (minus the u8 wrap), and a
  *                                statistical check against exact L2
  *   warp distances               float64 textbook sum within 1e-5 relative;
- *                                exact on integer data
+ *                                exact on integer data; the shfl_down tree's
+ *                                order bit for bit at d = 32
  *   bitonic network              sortedness + permutation vs sorted() on
  *                                distinct keys; tie behaviour by brute force
  *                                of compare-exchange on tiny inputs
  *   merges                       vs heapq.merge / sorted() on distinct keys;
  *                                merge-path ties between beam and candidates
- *                                inside a segment: the stable merge, beam first
+ *                                inside a segment: the stable merge, beam first;
+ *                                ties across segment boundaries: a replay of
+ *                                the reference's thread segmentation
  *   hash                         set semantics vs a Python set
  *   pick / keep counts           hand-computed cases; the stage-II rank keeps
  *                                the lower lane of a tie (keep 1 over a tie)
  *   controller, K-th cutoff      hand-computed trajectories of the exported
  *                                fgo_controller_step / fgo_record_expander /
- *                                fgo_kth_cutoff (test_oracle_traces.py)
+ *                                fgo_kth_cutoff (test_oracle_traces.py),
+ *                                including the stage-I rate's cap and the
+ *                                fallbacks for unfinite expander distances
  *   loop order                   hand-traced searches over hand-built
  *                                codebooks (tests/crafted.py): cutoff and
  *                                `<=` near count in both stages, the switch
@@ -43,9 +48,12 @@
  *                                to the iteration limit); stage-II estimates
  *                                from each parent's own distance, the keep-all
  *                                shortcut at equality in both stages, the
- *                                8-slot second tile of a degree-40 parent, and
- *                                the result writer's empty slots (0x7FFFFFFF
- *                                inside the beam, the last id past it)
+ *                                8-slot second tile of a degree-40 parent, the
+ *                                parent-by-parent task order against the
+ *                                32-slot collect cap, out-of-range neighbour
+ *                                ids in both stages, and the result writer's
+ *                                empty slots (0x7FFFFFFF inside the beam, the
+ *                                last id past it)
  *   mutations                    each rule above planted wrong in a copy of
  *                                this file fails a pin (test_oracle_mutations)
  *   entry point / recall / I/O   the reference's own host headers compiled

@@ -76,7 +76,7 @@ def make(dist: dict[int, int], adj: dict[int, list[int]], est: dict[tuple[int, i
             if v is None:
                 continue
             ids[u, j] = v
-            e = est.get((u, v), dist[v])
+            e = est[(u, v)] if (u, v) in est else dist[v]
             f[u, 0, j] = e - dist[u]
     signs = np.ones(lay.padded_dim, np.float32)
     return Codebook(rows, signs, entry, lay), q[None, :]
@@ -326,3 +326,53 @@ def scenario_wide_degree():
         dist[i] = 5000
         adj[i] = [0]
     return make(dist, adj, {}, degree=40)
+
+
+def scenario_task_order():
+    """Degree 40, beam 64, K 44: stage II's tasks run parent by parent
+    (task t is tile t % 2 of parent t / 2, adaptive_search.cuh:354-356), eight
+    to a round, and the compaction keeps the first BUFFER_BOUND = 32 kept
+    children in (task, lane) order (:405-430); the ones past it are inserted
+    into the visited set but never scored.  The entry (distance 1) lists 1 ..
+    11; 1, 2, 3 are dead ends, so stage II starts at iteration 4 with parents
+    4 .. 11.  Parent p has four children in its first tile (slots 0-3) and
+    one in its second (slot 32), ids 20 + 5 (p - 4) + j, at distance
+    1000 + id; every child links back to its parent only."""
+    dist = {0: 1}
+    adj = {0: list(range(1, 12))}
+    for i in range(1, 12):
+        dist[i] = 10 * i
+        adj[i] = [0]
+    for p in range(4, 12):
+        kids = [20 + 5 * (p - 4) + j for j in range(5)]
+        adj[p] = kids[:4] + [None] * 28 + [kids[4]]
+        for k in kids:
+            dist[k] = 1000 + k
+            adj[k] = [p]
+    for i in range(12, 20):  # unused ids
+        dist[i] = 5000
+        adj[i] = [0]
+    return make(dist, adj, {}, degree=40)
+
+
+BAD_ID = 40  # an id past the last node of scenario_out_of_range_ids
+
+
+def scenario_out_of_range_ids():
+    """Degree 8, beam 64, K 10: a neighbour id that is neither a node nor
+    0xFFFFFFFF (BAD_ID, past the 15 nodes) is not a valid child in either
+    stage (adaptive_search.cuh:233, 372): it is read (ids counter) but never
+    estimated, inserted or scored.  The entry lists 1 .. 7 with BAD_ID in
+    slot 2; 1, 2, 3, 5, 6, 7 are dead ends, and parent 4 lists BAD_ID in slot
+    0 before its children 8 .. 14.  BAD_ID's edges carry the estimate 10^6."""
+    dist = {0: 1}
+    adj = {0: [1, 2, BAD_ID, 3, 4, 5, 6, 7]}
+    for i in range(1, 8):
+        dist[i] = 10 * i
+        adj[i] = [0]
+    adj[4] = [BAD_ID] + list(range(8, 15))
+    for k, r in zip(range(8, 15), (6, 2, 7, 1, 5, 3, 4)):  # estimate ranks of 8 .. 14
+        dist[k] = 100 + 10 * r
+        adj[k] = [4]
+    est = {(0, BAD_ID): 10 ** 6, (4, BAD_ID): 10 ** 6}
+    return make(dist, adj, est, degree=8)

@@ -1,5 +1,6 @@
 """The oracle's pins are strong enough to catch plausible mistakes in its
-controller, loop sequencing, merge, stage-II selection and result writer:
+controller, loop sequencing, merge, stage-II selection, task order, id
+validity, distance reduction and result writer:
 each mutation below is planted in a temporary copy of oracle/fg_oracle.c
 (compiled on the CPU, loaded through FG_ORACLE_LIB in a separate pytest
 process), and the pin tests (hand-traced searches, hand-computed primitives
@@ -58,6 +59,41 @@ MUTATIONS = {
     "no final merge after the loop": (
         "fgo_merge_candidates(bd, bi, cd, ci, cbs, pbeam, 0, ws->scratch_d, ws->scratch_i);  /* :449-451 */",
         "/* final merge dropped */"),
+    "per-parent budget rounded up": (
+        "(uint32_t)FGO_BUFFER_BOUND / (uint32_t)theta;",
+        "((uint32_t)FGO_BUFFER_BOUND + (uint32_t)theta - 1) / (uint32_t)theta;"),
+    "merge-path threads not rounded to a multiple of 32": ("    active = ((active + 31) / 32) * 32;\n", ""),
+    "stage-I rate capped at RHO_MAX instead of the phase-2 rate": (
+        "const float cap = phase2_rho > 0.25f ? phase2_rho : 0.99f;", "const float cap = 0.99f;"),
+    "unfinite current expander falls back to the entry": (
+        "*cur = finite_below_max(prev->current_expander_distance) ? prev->current_expander_distance : *last;",
+        "*cur = finite_below_max(prev->current_expander_distance) ? prev->current_expander_distance : entry;"),
+    "record falls back to the last distance": (
+        "? st->current_expander_distance : st->entry_distance;",
+        "? st->current_expander_distance : st->last_expander_distance;"),
+    "stage-II tasks tile by tile": (
+        """const uint32_t pidx = active ? (uint32_t)(task / tiles) : 0u;
+                    const int tile = active ? task - (int)pidx * tiles : 0;""",
+        """const uint32_t pidx = active ? (uint32_t)(task % (int)nexp) : 0u;
+                    const int tile = active ? task / (int)nexp : 0;"""),
+    "distance lanes summed in order instead of the shfl_down tree": (
+        """    for (int off = 16; off >= 1; off >>= 1)
+        for (int l = 0; l < off; ++l) v[l] = v[l] + v[l + off];
+    return v[0];
+}
+
+/* utils.cuh:286-300 */""",
+        """    for (int l = 1; l < 32; ++l) v[0] = v[0] + v[l];
+    return v[0];
+}
+
+/* utils.cuh:286-300 */"""),
+    "stage-I out-of-range ids valid": (
+        "if (child >= ix->npoints || fgo_hash_contains(hash, bitlen, child)) child = FGO_MAX_INDEX;",
+        "if (child == FGO_MAX_INDEX || fgo_hash_contains(hash, bitlen, child)) child = FGO_MAX_INDEX;"),
+    "stage-II out-of-range ids valid": (
+        "valid[l] = child[w][l] != FGO_MAX_INDEX && child[w][l] < ix->npoints &&",
+        "valid[l] = child[w][l] != FGO_MAX_INDEX &&"),
 }
 
 
@@ -77,7 +113,8 @@ def _build(tmp_path, name, mutation):
 
 
 PIN_TESTS = ["test_oracle_traces.py", "test_oracle_primitives.py",
-             "test_oracle_networks.py::test_merge_path_ties_inside_segments_keep_beam_first"]
+             "test_oracle_networks.py::test_merge_path_ties_inside_segments_keep_beam_first",
+             "test_oracle_networks.py::test_merge_path_segmentation_with_boundary_ties"]
 
 
 def _pins_pass(lib):

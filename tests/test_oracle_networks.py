@@ -356,6 +356,60 @@ def test_merge_path_partition_valid_split():
             assert left.max() <= right.min()
 
 
+
+def _ref_merge_path(bd, bi, cd, ci, pbeam, active):
+    """The output loop of topk_candidate_sort_and_merge (utils.cuh:637-669)
+    over `active` threads of a 256-thread block, candidates already sorted:
+    thread t writes outputs [t pbeam / active, (t + 1) pbeam / active), each
+    end located by the partition, the beam taken on `<=`."""
+    od, oi = [0.0] * pbeam, [0] * pbeam
+    for t in range(active):
+        ob, oe = min(pbeam, t * pbeam // active), min(pbeam, (t + 1) * pbeam // active)
+        tb, te = _ref_partition(bd, cd, ob), _ref_partition(bd, cd, oe)
+        ti, c, cend = tb, ob - tb, oe - te
+        for o in range(ob, oe):
+            if c >= cend or (ti < te and bd[ti] <= cd[c]):
+                od[o], oi[o] = bd[ti], bi[ti]
+                ti += 1
+            else:
+                od[o], oi[o] = cd[c], ci[c]
+                c += 1
+    return od, oi
+
+
+@pytest.mark.parametrize("pbeam", [129, 160, 200, 300, 513, 1000])
+def test_merge_path_segmentation_with_boundary_ties(pbeam):
+    """Keys tied between the beam and the candidates across segment
+    boundaries: which thread takes which tied entry depends on where the
+    segments start, so the ids' order pins the reference's segmentation,
+    ceil(pbeam / 4) threads rounded up to a multiple of 32 and at most 256
+    (utils.cuh:632-635).  Beam keys are integers with repeats, candidate keys
+    distinct integers (so the candidate sort has no ties to place); each case
+    is checked to come out differently with the unrounded thread count."""
+    L = O.lib()
+    rng = np.random.default_rng(pbeam)
+    active = min(256, ((pbeam + 3) // 4 + 31) // 32 * 32)
+    unrounded = (pbeam + 3) // 4
+    assert active != unrounded
+    differs = 0
+    for trial in range(8):
+        bd = np.sort(rng.integers(0, 60, pbeam)).astype(np.float32)
+        bi = np.arange(pbeam, dtype=np.uint32)
+        cs = np.sort(rng.choice(60, 32, replace=False)).astype(np.float32)
+        perm = rng.permutation(32)
+        cd = cs[perm].copy()
+        ci = (5000 + perm).astype(np.uint32)
+        want_d, want_i = _ref_merge_path(list(bd), list(bi), list(cs), list(range(5000, 5032)), pbeam, active)
+        _, other_i = _ref_merge_path(list(bd), list(bi), list(cs), list(range(5000, 5032)), pbeam, unrounded)
+        differs += other_i != want_i
+        sd = np.zeros(1024, np.float32)
+        si = np.zeros(1024, np.uint32)
+        L.fgo_merge_candidates(O.ptr(bd, C.c_float), O.ptr(bi, C.c_uint32), O.ptr(cd, C.c_float),
+                               O.ptr(ci, C.c_uint32), 32, pbeam, 0, O.ptr(sd, C.c_float), O.ptr(si, C.c_uint32))
+        assert bd.tolist() == want_d, trial
+        assert bi.tolist() == want_i, trial
+    assert differs >= 1
+
 @pytest.mark.parametrize("top", [8, 16])
 def test_short_candidate_sort_equals_full_network(top):
     """A 32-entry candidate buffer whose slots from `span` on hold the reset

@@ -64,6 +64,11 @@ def test_keep_counts_hand_computed():
     assert lib.fgo_keep_count_for_expander(32, 1, 0.25, 1, 99) == 24
     # a short tile (deg 40, second tile has 8) clamps to its active count
     assert lib.fgo_keep_count_for_expander(8, 8, 0.875, 0, 0) == 1
+    # the per-parent budget is BUFFER_BOUND / theta rounded down
+    # (adaptive_search_utils.cuh:126): 32 / 3 = 10, 32 / 5 = 6, 32 / 6 = 5
+    assert lib.fgo_keep_count_for_expander(32, 3, 0.0, 0, 0) == 10
+    assert lib.fgo_keep_count_for_expander(32, 5, 0.0, 0, 0) == 6
+    assert lib.fgo_keep_count_for_expander(32, 6, 0.0, 0, 0) == 5
 
 
 # ---------------------------------------------------------------- FWHT
@@ -220,6 +225,42 @@ def test_warp_distances():
         ai = rng.integers(0, 200, dim).astype(np.float32)
         bi = rng.integers(0, 200, dim).astype(np.float32)
         assert L().fgo_warp_l2(dim, O.ptr(ai, C.c_float), O.ptr(bi, C.c_float)) == float(((ai.astype(np.int64) - bi.astype(np.int64)) ** 2).sum())
+
+
+def _tree32(v):
+    """shfl_down tree of utils.cuh:277-281 / 292-296 over 32 float32 lane
+    sums: offsets 16, 8, 4, 2, 1, lane l adding lane l + offset."""
+    v = np.asarray(v, np.float32).copy()
+    off = 16
+    while off:
+        v[:off] = v[:off] + v[off:2 * off]
+        off //= 2
+    return v[0]
+
+
+def test_warp_distances_reduction_tree_bit_exact():
+    """At d = 32 each lane holds one product, rounded once to float32 (the
+    fmaf with a zero addend; float64 holds the product exactly), so the
+    distance is exactly the shfl_down tree over those 32 values in float32.
+    Random floats make the tree's sum differ in its last bits from other
+    orders (sequential, pairwise from the other end) in most trials, so the
+    order is pinned bit for bit."""
+    rng = np.random.default_rng(9)
+    differs = 0
+    for _ in range(50):
+        a = rng.standard_normal(32).astype(np.float32)
+        b = rng.standard_normal(32).astype(np.float32)
+        d = (a - b).astype(np.float32)
+        sq = (d.astype(np.float64) ** 2).astype(np.float32)
+        pr = (a.astype(np.float64) * b.astype(np.float64)).astype(np.float32)
+        want_l2, want_ip = _tree32(sq), -_tree32(pr)
+        assert np.float32(L().fgo_warp_l2(32, O.ptr(a, C.c_float), O.ptr(b, C.c_float))) == want_l2
+        assert np.float32(L().fgo_warp_ip(32, O.ptr(a, C.c_float), O.ptr(b, C.c_float))) == want_ip
+        seq = np.float32(0)
+        for x in sq:
+            seq = np.float32(seq + x)
+        differs += seq != want_l2
+    assert differs >= 10
 
 
 # ---------------------------------------------------------------- hash / pick

@@ -359,3 +359,93 @@ def test_trace_wide_degree_tiles():
     assert tr[0]["cand"] == [1, 2, 3, 4, 5, 6, 7, 8]
     assert tr[4]["cand"] == [21] and tr[4]["cdist"] == [150]
     assert np.allclose([t["rho"] for t in tr[4:]], [0.9, 0.9])
+
+
+def test_trace_task_order_and_collect_cap():
+    """Degree 40, beam 64, K 44 (crafted.scenario_task_order).
+      it 0: the entry's 11 neighbours (keep ceil(32 * 0.75) = 24 >= 11: all).
+      it 1-3: 1, 2, 3 are dead ends; top-1 0 stalls 1, 2, 3 times.
+      it 4: stage II (rate 1 - 4/40 = 0.9), parents 4 .. 11, two tiles each:
+            16 tasks, parent by parent, in two rounds of 8.  A first tile
+            keeps min(ceil(32 * 0.1), 32 / 8) = 4 >= its 4 children and the
+            8-slot second tile min(ceil(8 * 0.1), 4) = 1 >= its 1: every child
+            is kept, 40 in all.  Round 1 (parents 4-7, both tiles) collects
+            20 .. 39, round 2 continues with 40 .. 49 (parents 8, 9) and the
+            first two of parent 10's first tile, 50 and 51; there the 32-slot
+            buffer is full and 52 .. 59 are inserted but never scored.  (Tasks
+            taken tile by tile would fill the buffer with the eight first
+            tiles in round 1.)
+      it 5-8: the 32 children, eight per iteration, all dead ends; it 9
+            finds nothing to expand.
+    Counters: 9 iterations, 1+1+1+1+8+32 = 44 expansions, 4 x 32 + 40 x 40
+    = 1,728 ids, no estimates, 1 + 11 + 32 = 44 exact distances, stage II
+    from iteration 4."""
+    cb, q = crafted.scenario_task_order()
+    out, cnt, tr = _trace(cb, q, 44, 64)
+    assert out == [0] + list(range(1, 12)) + list(range(20, 52))
+    assert cnt == (9, 44, 1728, 0, 44, 4)
+    assert [t["parents"] for t in tr[:5]] == [[0], [1], [2], [3], list(range(4, 12))]
+    assert [t["theta"] for t in tr] == [1, 1, 1, 1, 8, 8, 8, 8, 8]
+    assert tr[4]["cand"] == list(range(20, 52))
+    assert [t["parents"] for t in tr[5:]] == [list(range(20 + 8 * i, 28 + 8 * i)) for i in range(4)]
+
+
+def test_controller_stage1_rate_capped_at_phase2_rate():
+    """Degree 32 (phase-2 rate 0.875, span 0.625), entry 100, expanders 10,
+    50, 10 (not monotone, as in a real search): progress 0.9 takes the rate to
+    0.25 + 0.5625 = 0.8125, the rise to 50 adds nothing, the drop back to 10
+    adds 0.625 * 0.4 = 0.25, and 1.0625 is clamped to the phase-2 rate 0.875
+    (adaptive_search_utils.cuh:104-107), not to RHO_MAX 0.99."""
+    st = _ctl(100.0)
+    _step(st, 1, 0.875)
+    _record(st, [10])
+    assert _step(st, 2, 0.875)[1] == pytest.approx(0.8125, abs=1e-6)
+    _record(st, [50])
+    assert _step(st, 3, 0.875)[1] == pytest.approx(0.8125, abs=1e-6)
+    _record(st, [10])
+    th, rho, stall = _step(st, 4, 0.875)
+    assert (th, stall) == (1, 0) and rho == np.float32(0.875)
+
+
+def test_controller_unfinite_expander_distances_fall_back():
+    """expander_progress (adaptive_search_utils.cuh:51-72): a current
+    expander distance that is not finite (or FLT_MAX) falls back to the last
+    one, and a last one that is not falls back to the entry distance;
+    record_selected_expander_dist (:41-49) moves the current distance into
+    `last`, or the entry distance when the current one is not finite.
+    Entry 10, expanders 40 then FLT_MAX: at step 3 last = 40 and current
+    falls back to 40, so progress is 0 and the rate stays 0.25 (falling back
+    to the entry 10 would give progress 3 -> 1 and the rate 0.875)."""
+    st = _ctl(10.0)
+    _step(st, 1, 0.875)
+    assert _record(st, [40]) == (10.0, 40.0)
+    assert _step(st, 2, 0.875)[1] == 0.25
+    assert _record(st, [FLT_MAX]) == (40.0, FLT_MAX)
+    assert _step(st, 3, 0.875)[1] == 0.25
+    assert (st.last_expander_distance, st.current_expander_distance) == (40.0, 40.0)
+    fresh = _ctl(7.0)  # current is FLT_MAX before any step: last becomes the entry
+    assert _record(fresh, [3]) == (7.0, 3.0)
+
+
+def test_trace_out_of_range_ids_are_not_children():
+    """Degree 8, beam 64, K 10 (crafted.scenario_out_of_range_ids; BAD_ID =
+    40 with 15 nodes).
+      it 0: the entry's 8 slots are read; 7 valid (BAD_ID is not: child_id
+            >= npoints, adaptive_search.cuh:233), keep min(ceil(8 * 0.75),
+            8) = 6 < 7: 7 estimates, 1 .. 6 kept (7 at 70 is not).
+      it 1-3: 1, 2, 3 are dead ends; top-1 0 stalls 1, 2, 3 times.
+      it 4: stage II, rate 1 - 4/8 = 0.5, parents 4, 5, 6.  Parent 4 lists
+            BAD_ID (not valid, :372) and 8 .. 14: keep min(ceil(8 * 0.5),
+            32 / 8) = 4 < 7: 7 estimates, the four smallest 11 (110), 9
+            (120), 13 (130), 14 (140), listed in lane order 9, 11, 13, 14.
+      it 5: parents 11, 9, 13, 14 (dead ends); it 6 finds nothing.
+    Counters: 6 iterations, 1+1+1+1+3+4 = 11 expansions, 8 + 3 x 8 + 3 x 8 +
+    4 x 8 = 88 ids, 7 + 7 = 14 estimates, 1 + 6 + 4 = 11 exact distances."""
+    cb, q = crafted.scenario_out_of_range_ids()
+    assert cb.rows.shape[0] < crafted.BAD_ID
+    out, cnt, tr = _trace(cb, q, 10, 64)
+    assert out == [0, 1, 2, 3, 4, 5, 6, 11, 9, 13]
+    assert cnt == (6, 11, 88, 14, 11, 4)
+    assert [t["parents"] for t in tr] == [[0], [1], [2], [3], [4, 5, 6], [11, 9, 13, 14]]
+    assert tr[0]["cand"] == [1, 2, 3, 4, 5, 6]
+    assert tr[4]["cand"] == [9, 11, 13, 14] and tr[4]["cdist"] == [120, 110, 130, 140]
