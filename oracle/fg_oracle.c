@@ -70,8 +70,9 @@
  *     test_oracle_fma rebuilds this file with all six sites unfused and
  *     requires the same ids on >= 98% of queries and recall within 0.2 pp;
  *   - the speculative round's visibility rule (every task of a round sees the
- *     visited set as it stood at the round's start; inserts resolve in
- *     (task, lane) order) and theta = 1 duplicates resolving by slot order;
+ *     visited set as it stood at the round's start; inserts and the 32
+ *     candidate slots go in (task, lane) order, where the reference's warps
+ *     race) and theta = 1 duplicates resolving by slot order;
  *   - a query whose rotated vector is constant (width == 0): the reference
  *     computes lroundf(NaN); here every level is 0;
  *   - the codebook factors, whose builder (SymphonyQG) is not in the

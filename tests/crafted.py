@@ -330,10 +330,12 @@ def scenario_wide_degree():
 
 def scenario_task_order():
     """Degree 40, beam 64, K 44: stage II's tasks run parent by parent
-    (task t is tile t % 2 of parent t / 2, adaptive_search.cuh:354-356), eight
-    to a round, and the compaction keeps the first BUFFER_BOUND = 32 kept
-    children in (task, lane) order (:405-430); the ones past it are inserted
-    into the visited set but never scored.  The entry (distance 1) lists 1 ..
+    (task t is tile t % 2 of parent t / 2, adaptive_search.cuh:351-354), eight
+    to a round, and the compaction keeps at most BUFFER_BOUND = 32 kept
+    children (:413-430); the ones past it are inserted into the visited set
+    but never scored.  Which of a round's children take the last free slots
+    is a race between the reference's warps; the oracle (and the kernel)
+    take them in (task, lane) order.  The entry (distance 1) lists 1 ..
     11; 1, 2, 3 are dead ends, so stage II starts at iteration 4 with parents
     4 .. 11.  Parent p has four children in its first tile (slots 0-3) and
     one in its second (slot 32), ids 20 + 5 (p - 4) + j, at distance
