@@ -15,7 +15,8 @@
  *   FWHT (fgo_rotate)            O(B^2) Sylvester-Hadamard product, exact on
  *                                integer inputs
  *   quantizer / LUT              closed form: LUT[m] = sum of q over bits of m
- *                                (mod 256); q in [1, 64]; sum_q = sum q
+ *                                (mod 256); q in [1, 64]; sum_q = sum q; the
+ *                                range over all B rotated entries (d < B too)
  *   estimators                   closed form vs the bit-plane identity
  *                                raw = sum_i b_i q_i (minus the u8 wrap), and a
  *                                statistical check against exact L2
@@ -48,7 +49,9 @@
  *                                to the iteration limit); stage-II estimates
  *                                from each parent's own distance, the keep-all
  *                                shortcut at equality in both stages, the
- *                                8-slot second tile of a degree-40 parent, the
+ *                                8-slot second tile of a degree-40 parent and
+ *                                its estimates read from the neighbour's own
+ *                                code slot, the
  *                                parent-by-parent task order against the
  *                                32-slot collect cap, out-of-range neighbour
  *                                ids in both stages, and the result writer's

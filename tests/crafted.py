@@ -378,3 +378,28 @@ def scenario_out_of_range_ids():
         adj[k] = [4]
     est = {(0, BAD_ID): 10 ** 6, (4, BAD_ID): 10 ** 6}
     return make(dist, adj, est, degree=8)
+
+
+def scenario_wide_degree_codes():
+    """scenario_wide_degree with parent 4's second-tile estimates made by
+    their codes: the edges 4 -> 20, 21, 22 (slots 32-34) carry triple_x 160
+    (so triple_x + d(q, 4) = 200), factor_dq 1 and factor_vq 0, and the codes
+    at slots 32, 33, 34 are all ones, all zeros and every other chunk set.
+    The query (10, 3, 0, ...) rotates to 13 on even and 7 on odd dimensions
+    of 64 (low 7, width 6/63), so it quantizes to q = 1 (odd) and 63 (even:
+    6 / fl(6/63) + 0.5 falls a hair below 63.5 in float), sum_q = 2048: raw
+    is 2048, 0 and 1024, and the estimates 200 + (6/63)(2 raw - 2048) =
+    395.0, 5.0 and 200.  Slots 0-2 of the first tile (ids 0 and two
+    empty slots) hold the codes zeros, ones, ones, so an estimate read from
+    slot l of the tile instead of slot 32 + l would rank 20 first."""
+    cb, q = scenario_wide_degree()
+    lay = cb.layout
+    codes = cb.rows[:, lay.code_offset:lay.factor_offset].view(np.uint8).reshape(cb.rows.shape[0], lay.degree, -1)
+    f = cb.rows[:, lay.factor_offset:lay.neighbor_offset].reshape(cb.rows.shape[0], 3, lay.degree)
+    for slot, byte in ((32, 0xFF), (33, 0x00), (34, 0x0F), (0, 0x00), (1, 0xFF), (2, 0xFF)):
+        codes[4, slot, :] = byte
+    for slot in (32, 33, 34):
+        f[4, 0, slot] = 160.0
+        f[4, 1, slot] = 1.0
+        f[4, 2, slot] = 0.0
+    return cb, q

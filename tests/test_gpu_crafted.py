@@ -52,6 +52,7 @@ def test_line_search_at_max_iter(gpu_available, beam):
     ("scenario_short_graph", 4, 2, [1, 2, 2, 2]),
     ("scenario_stage2_parents", 8, 8, [0, 1, 31, 2, 41, 3, 50, 51]),
     ("scenario_wide_degree", 12, 64, [0, 1, 2, 3, 4, 5, 6, 7, 8, 21, 0x7FFFFFFF, 0x7FFFFFFF]),
+    ("scenario_wide_degree_codes", 12, 64, [0, 1, 2, 3, 4, 5, 6, 7, 8, 21, 0x7FFFFFFF, 0x7FFFFFFF]),
     ("scenario_task_order", 44, 64, [0] + list(range(1, 12)) + list(range(20, 52))),
     ("scenario_out_of_range_ids", 10, 64, [0, 1, 2, 3, 4, 5, 6, 11, 9, 13]),
 ])

@@ -91,6 +91,12 @@ MUTATIONS = {
     "stage-I out-of-range ids valid": (
         "if (child >= ix->npoints || fgo_hash_contains(hash, bitlen, child)) child = FGO_MAX_INDEX;",
         "if (child == FGO_MAX_INDEX || fgo_hash_contains(hash, bitlen, child)) child = FGO_MAX_INDEX;"),
+    "stage-II estimate from the tile's slot l instead of neighbour slot nidx": (
+        "est[l] = fgo_estimate_seq(qf, codes + (size_t)nidx * bytes_per_nbr, tx[l], fdq[l],",
+        "est[l] = fgo_estimate_seq(qf, codes + (size_t)l * bytes_per_nbr, tx[l], fdq[l],"),
+    "query range over the d input dimensions only": (
+        "    for (int i = 0; i < padded_dim; ++i) {\n        lo = fminf(lo, qf->rotated[i]);",
+        "    for (int i = 0; i < dim; ++i) {\n        lo = fminf(lo, qf->rotated[i]);"),
     "stage-II out-of-range ids valid": (
         "valid[l] = child[w][l] != FGO_MAX_INDEX && child[w][l] < ix->npoints &&",
         "valid[l] = child[w][l] != FGO_MAX_INDEX &&"),

@@ -114,9 +114,11 @@ def _prep(x, s, dim, B):
 
 
 @pytest.mark.parametrize("seed", range(5))
-def test_quantizer_closed_form(seed):
+@pytest.mark.parametrize("dim,B", [(128, 128), (96, 128), (40, 64)])
+def test_quantizer_closed_form(seed, dim, B):
+    """Range, width, levels and LUT over all B rotated entries (utils.cuh:
+    840-939; the zero-padded dimensions of a d < B query are rotated too)."""
     rng = np.random.default_rng(seed)
-    dim, B = 128, 128
     x = rng.integers(0, 150, dim).astype(np.float32)
     s = np.where(rng.random(B) < 0.5, -1.0, 1.0).astype(np.float32)
     qf = _prep(x, s, dim, B)

@@ -453,3 +453,26 @@ def test_trace_out_of_range_ids_are_not_children():
     assert [t["parents"] for t in tr] == [[0], [1], [2], [3], [4, 5, 6], [11, 9, 13, 14]]
     assert tr[0]["cand"] == [1, 2, 3, 4, 5, 6]
     assert tr[4]["cand"] == [9, 11, 13, 14] and tr[4]["cdist"] == [120, 110, 130, 140]
+
+
+def test_trace_wide_degree_estimates_read_their_own_slot():
+    """crafted.scenario_wide_degree_codes: as test_trace_wide_degree_tiles,
+    but parent 4's second-tile estimates come from the codes at slots 32-34
+    (the code of neighbour slot nidx, adaptive_search.cuh:392-394).  By hand
+    (the docstring of the scenario) they are 395.0, 5.0 and 200 for 20, 21
+    and 22, so 21 is kept; an estimate read from slot l of the tile would
+    give 20 the smallest (slot 0's zero code) and keep 20."""
+    cb, q = crafted.scenario_wide_degree_codes()
+    qf = O.query_prepare(q[0], cb.signs, 40, 64)
+    assert (qf.sum_q, qf.low, qf.high) == (2048, 7.0, 13.0)
+    assert list(qf.q[:4]) == [63, 1, 63, 1]
+    lay = cb.layout
+    codes = cb.rows[4, lay.code_offset:lay.factor_offset].view(np.uint8).reshape(lay.degree, -1)
+    est = [O.lib().fgo_estimate_seq(O.C.byref(qf), O.ptr(np.ascontiguousarray(codes[s]), O.C.c_uint8),
+                                     160.0, 1.0, 0.0, 40.0, 64) for s in (32, 33, 34)]
+    w = np.float32(6.0) / np.float32(63.0)
+    assert est == pytest.approx([200 + w * 2048, 200 - w * 2048, 200], abs=1e-3)
+    out, cnt, tr = _trace(cb, q, 12, 64)
+    assert out == [0, 1, 2, 3, 4, 5, 6, 7, 8, 21, 0x7FFFFFFF, 0x7FFFFFFF]
+    assert cnt == (6, 10, 368, 3, 10, 4)
+    assert tr[4]["cand"] == [21] and tr[4]["cdist"] == [150]
