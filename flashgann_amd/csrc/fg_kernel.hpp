@@ -1844,6 +1844,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
     uint32_t c_iters = 0, c_exp = 0, c_ids = 0, c_est = 0, c_exact = 1, c_st2 = kMaxIndex;
     const int beam_sz = P.beam, pbeam = P.pbeam;
     const int cbs = P.cbs;
+    // ranges the host guarantees (make_params), stated so that the compiler
+    // keeps no guard on them live across the search loop: each such guard is
+    // a 64-bit lane mask, and the loop is short of scalar registers
+    __builtin_assume(beam_sz >= 1 && beam_sz <= kMaxBeam && pbeam >= beam_sz && pbeam <= kMaxBeam);
+    __builtin_assume(cbs >= 1 && cbs <= kBufferBound && nbk >= 1u && P.K >= 1);
+    // the node count as a 32-bit bound: ids are 32-bit and MAX_INDEX is tested
+    // apart wherever an id is checked, so min(npoints, MAX_INDEX) decides
+    // the same and is one scalar register and a 32-bit compare
+    const uint32_t np32 = uni(P.npoints > 0xFFFFFFFFull ? 0xFFFFFFFFu : static_cast<uint32_t>(P.npoints));
     // candidate slots the next merge may find filled (the rest hold the
     // reset pair): the entry point's slot 0 first, then what each stage fills
     int cand_span = 1;
@@ -2065,7 +2074,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
                 if constexpr (WT > 0)
                     load_code<WT>(reinterpret_cast<const uint32_t *>(prow + g.code) + static_cast<uint64_t>(nsafe) * WT,
                                   vec_ok, c1[0]);
-                bool fresh[1] = {nl < cwc && ck[0] < P.npoints};
+                bool fresh[1] = {nl < cwc && ck[0] < np32};
                 hash_contains_n<1>(H, nbk, ck, fresh);
                 uint32_t child = fresh[0] ? ck[0] : kMaxIndex;
                 const uint32_t vmask = half_bits(ballot(child != kMaxIndex), 0);
@@ -2231,7 +2240,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
                     if (!lact[sr]) cid[sr] = kMaxIndex;
                 // (b) visited test against the table as it stood at the round's start
 #pragma unroll
-                for (int sr = 0; sr < SRN; ++sr) val[sr] = cid[sr] != kMaxIndex && cid[sr] < P.npoints;
+                for (int sr = 0; sr < SRN; ++sr) val[sr] = cid[sr] != kMaxIndex && cid[sr] < np32;
                 hash_contains_n<SRN>(H, nbk, cid, val);
                 // (c) which tasks need estimates.  Lane predicates from here on
                 // are masks taken straight from compares.  A task without

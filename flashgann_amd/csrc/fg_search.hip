@@ -64,15 +64,22 @@ __device__ __forceinline__ double slice_scale(uint32_t omin, uint32_t omax) {
     return range > 0.0 ? static_cast<double>(kSliceBins - 1) / range : 0.0;
 }
 
+// (xor distances 32 .. 1 written out: each is a different cross-lane move)
 __device__ __forceinline__ uint32_t wave_umin(uint32_t v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = min(v, xshfl(v, m));
-    return v;
+    v = min(v, xshfl(v, 32));
+    v = min(v, xshfl(v, 16));
+    v = min(v, xshfl(v, 8));
+    v = min(v, xshfl(v, 4));
+    v = min(v, xshfl(v, 2));
+    return min(v, xshfl(v, 1));
 }
 __device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = max(v, xshfl(v, m));
-    return v;
+    v = max(v, xshfl(v, 32));
+    v = max(v, xshfl(v, 16));
+    v = max(v, xshfl(v, 8));
+    v = max(v, xshfl(v, 4));
+    v = max(v, xshfl(v, 2));
+    return max(v, xshfl(v, 1));
 }
 
 // Exclusive scan of the kSliceBins counts in[] into out[] (in == out allowed)
