@@ -341,6 +341,26 @@ def main() -> int:
     single_ms = float(np.median(single))
     log(f"beam {chosen}: one synchronous search {single_ms:.3f} ms (median of 11; {args.nq / single_ms * 1e3:.0f} QPS)")
 
+    # The device's measured copy bandwidth, the second yardstick for the
+    # roofline fraction: ten 1 GiB device-to-device copies (1 GiB read and
+    # 1 GiB written each) timed with events on torch's stream.
+    src = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    cstream = torch.cuda.current_stream()
+    c0.record(cstream)
+    for _ in range(10):
+        dst.copy_(src)
+    c1.record(cstream)
+    torch.cuda.synchronize()
+    copy_gbs = 10 * 2 * src.numel() * 4 / (c0.elapsed_time(c1) / 1e3) / 1e9
+    del src, dst
+    torch.cuda.empty_cache()
+    log(f"device copy: {copy_gbs:.1f} GB/s (read + write); the search's algorithmic rate is "
+        f"{achieved / copy_gbs:.3f} of it")
+
     # the same search through the host-buffer entry point (queries copied in,
     # ids copied out, PCIe included) -- reported beside, never as, `value`
     host_q = np.ascontiguousarray(queries, dtype=np.float32)
@@ -519,6 +539,7 @@ def main() -> int:
                    "rng_graph": side.get("rng_graph"), "connected_graph": side.get("connected_graph")},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_source,
+                     "measured_copy_gbs": round(copy_gbs, 1), "frac_of_measured_copy": round(achieved / copy_gbs, 4),
                      "kernel": "fg_search_kernel", "kernel_ms": round(kernel_ms, 4),
                      "algorithmic_bytes_per_launch": alg_bytes},
         "cpu_baseline": cpu,
