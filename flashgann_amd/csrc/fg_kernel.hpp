@@ -498,6 +498,17 @@ __device__ __forceinline__ int wave_sum(int v) {
 
 // uniform value -> scalar register
 __device__ __forceinline__ uint32_t uni(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// A flag that stays the same through the search loop, kept as a 32-bit
+// scalar and tested where it is used (one scalar compare).  Held as a bool it
+// becomes a 64-bit lane mask live across the whole loop, and the loop is
+// short of scalar registers (such masks are spilled to vector-register lanes
+// and reloaded with v_readlane, a vector instruction).
+__device__ __forceinline__ bool sflag(uint32_t v) {
+    uint32_t u = __builtin_amdgcn_readfirstlane(v);
+    asm volatile("" : "+s"(u));
+    return u != 0u;
+}
 __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 __device__ __forceinline__ float uni(float v) {
     return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
@@ -1303,7 +1314,12 @@ struct Controller {
     int stall;
     bool warm;
     float entry_d, last_e, cur_e;
+    uint32_t entry_ok;  // 1 while entry_d is finite and |entry_d| > 1e-20 (set with entry_d)
 };
+
+__device__ __forceinline__ uint32_t entry_guard(float e) {
+    return (isfinite(e) && fabsf(e) > 1.0e-20f) ? 1u : 0u;
+}
 
 // src/adaptive_search.cuh:166-190 + adaptive_search_utils.cuh:32-39, 51-119
 // (CHECK_INTERVAL = 1): every lane computes the same values.
@@ -1316,7 +1332,7 @@ __device__ __forceinline__ void controller_step(Controller &c, uint32_t beam0, f
     const float cur = finite_below_max(c.cur_e) ? c.cur_e : last;
     float rate = 0.0f;  // only read while the search stays in stage I
     const float denom = fabsf(entry);
-    if (!phase_changed && isfinite(last) && isfinite(cur) && isfinite(entry) && denom > 1.0e-20f) {
+    if (!phase_changed && isfinite(last) && isfinite(cur) && sflag(c.entry_ok)) {
         const float pr = (last - cur) / denom;
         if (isfinite(pr) && pr > 0.0f) rate = pr < 1.0f ? pr : 1.0f;
     }
@@ -1555,7 +1571,7 @@ __device__ __forceinline__ void exact_batch_range(const SearchParams &P, const G
                                                   const float (&qr)[DPL > 0 ? DPL : 1], const float *qv) {
     const int lane = lane_id();
     const int h = lane >> 5, nl = lane & 31;
-    const bool ip = P.use_ip != 0;
+    const bool ip = sflag(static_cast<uint32_t>(P.use_ip));
     if constexpr (DPL > 0) {
         int e0 = lo;
         for (; n - e0 > 8; e0 += 16) exact_pass<8, DPL>(P, g, e0, n, slot_list, cd, ci, qr, ip);
@@ -1772,7 +1788,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
     constexpr int WTR = WT > 0 ? WT : 1;
     // whether any chunk of the quantized query wraps the reference's uint8
     // LUT entry (then the estimates subtract the wrapped chunks)
-    bool any_wrap = false, any_zero = false;
+    uint32_t any_wrap = 0u, any_zero = 0u;  // 0 / 1 (sflag at each use)
     if (lead) {
         if constexpr (WT > 0) {
             uint32_t wor = 0, zor = 0;
@@ -1781,16 +1797,16 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
                 wor |= planes[kWrapPlane * WT + w];
                 zor |= planes[kZeroPlane * WT + w];
             }
-            any_wrap = uni(wor) != 0u;
-            any_zero = uni(zor) != 0u;
+            any_wrap = uni(wor) != 0u ? 1u : 0u;
+            any_zero = uni(zor) != 0u ? 1u : 0u;
         } else {
             uint32_t wor = 0, zor = 0;
             for (int w = lane; w < W; w += 64) {
                 wor |= planes[kWrapPlane * W + w];
                 zor |= planes[kZeroPlane * W + w];
             }
-            any_wrap = any_lane(wor != 0u);
-            any_zero = any_lane(zor != 0u);
+            any_wrap = any_lane(wor != 0u) ? 1u : 0u;
+            any_zero = any_lane(zor != 0u) ? 1u : 0u;
         }
     }
     constexpr int DPLR = DPL > 0 ? DPL : 1;
@@ -1827,20 +1843,20 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
             tb->sum_q = static_cast<uint32_t>(sum_q);
             tb->qwidth_bits = __float_as_uint(qwidth);
             tb->qlow_bits = __float_as_uint(qlow);
-            tb->any_wrap = any_wrap ? 1u : 0u;
-            tb->any_zero = any_zero ? 1u : 0u;
+            tb->any_wrap = any_wrap;
+            tb->any_zero = any_zero;
         }
         __syncthreads();
         if (!lead) {
             sum_q = static_cast<int>(uni(tb->sum_q));
             qwidth = __uint_as_float(uni(tb->qwidth_bits));
             qlow = __uint_as_float(uni(tb->qlow_bits));
-            any_wrap = uni(tb->any_wrap) != 0u;
-            any_zero = uni(tb->any_zero) != 0u;
+            any_wrap = uni(tb->any_wrap) != 0u ? 1u : 0u;
+            any_zero = uni(tb->any_zero) != 0u ? 1u : 0u;
         }
     }
 
-    Controller ctl{1, kPhase1Rho, 0, kMaxIndex, 0, false, entry_d, FLT_MAX, FLT_MAX};
+    Controller ctl{1, kPhase1Rho, 0, kMaxIndex, 0, false, entry_d, FLT_MAX, FLT_MAX, uni(entry_guard(entry_d))};
     uint32_t c_iters = 0, c_exp = 0, c_ids = 0, c_est = 0, c_exact = 1, c_st2 = kMaxIndex;
     const int beam_sz = P.beam, pbeam = P.pbeam;
     const int cbs = P.cbs;
@@ -1864,6 +1880,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
 
     int iter = 0;
     bool suspended = false;
+    // the iteration at whose top an unfinished query suspends (-1: never)
+    const int suspend_at = (kSliceable && P.slice_suspend > 0) ? P.slice_suspend : -1;
     if constexpr (kSliceable) {
         if (P.slice_resume > 0) {
             // resume at the top of iteration slice_resume (before its visited-table
@@ -1887,6 +1905,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
             ctl.stall = static_cast<int>(uni(st[6]));
             ctl.warm = uni(st[7]) != 0u;
             ctl.entry_d = __uint_as_float(uni(st[8]));
+            ctl.entry_ok = uni(entry_guard(ctl.entry_d));
             ctl.last_e = __uint_as_float(uni(st[9]));
             ctl.cur_e = __uint_as_float(uni(st[10]));
             c_iters = uni(st[11]);
@@ -1906,7 +1925,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
     FG_PHASE(0);
     for (; iter < kMaxIterations; ++iter) {
         if constexpr (kSliceable) {
-            if (P.slice_suspend > 0 && iter == P.slice_suspend) {
+            if (iter == suspend_at) {
                 suspended = true;
                 break;
             }
@@ -2091,10 +2110,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
                     int32_t r1[1] = {0};
                     if constexpr (WT > 0) {
                         // computed on every lane, selected for the valid ones
-                        raw_batch<1, WT>(c1, planes, any_wrap, any_zero, r1);
+                        raw_batch<1, WT>(c1, planes, sflag(any_wrap), sflag(any_zero), r1);
                         est = tx == FLT_MAX ? 0.0f : estimate_formula(r1[0], sum_q, qwidth, qlow, tx, fdq, fvq, pd0);
                     } else if (valid) {
-                        const int32_t raw = raw_words(codes + static_cast<uint64_t>(nsafe) * W, planes, W, vec_ok, any_wrap, any_zero);
+                        const int32_t raw = raw_words(codes + static_cast<uint64_t>(nsafe) * W, planes, W, vec_ok,
+                                                      sflag(any_wrap), sflag(any_zero));
                         est = tx == FLT_MAX ? 0.0f : estimate_formula(raw, sum_q, qwidth, qlow, tx, fdq, fvq, pd0);
                     }
                     const bool fin = isfinite(est);
@@ -2122,7 +2142,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
                 const bool want = ((admit_mask >> nl) & 1u) && child != kMaxIndex && dist < FLT_MAX;
                 const uint32_t want_mask = half_bits(ballot(want), 0);
                 bool ins = want;
-                if (!P.dup_free) ins = want && !dup_of_earlier(child, want_mask, nl, 0);
+                if (!sflag(static_cast<uint32_t>(P.dup_free))) ins = want && !dup_of_earlier(child, want_mask, nl, 0);
                 if (h == 0 && ins) hash_insert(H, nbk, child);
                 if (!ins) {
                     if ((admit_mask >> nl) & 1u) {
@@ -2260,7 +2280,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
                 // (d) estimates, kth-near counts, keep decisions
                 uint64_t klm[SRN];
                 int32_t rawb[SRN];
-                if constexpr (WT > 0) raw_batch<SRN, WT>(code, planes, any_wrap, any_zero, rawb);
+                if constexpr (WT > 0) raw_batch<SRN, WT>(code, planes, sflag(any_wrap), sflag(any_zero), rawb);
 #pragma unroll
                 for (int sr = 0; sr < SRN; ++sr) {
                     float est = FLT_MAX;
@@ -2275,7 +2295,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WT == 0
                         const int nidx = tsk[sr] + nlg;
                         const int32_t raw = raw_words(reinterpret_cast<const uint32_t *>(prw[sr] + g.code) +
                                                           static_cast<uint64_t>(nidx) * W,
-                                                      planes, W, vec_ok, any_wrap, any_zero);
+                                                      planes, W, vec_ok, sflag(any_wrap), sflag(any_zero));
                         est = estimate_formula(raw, sum_q, qwidth, qlow, tx[sr], fdq[sr], fvq[sr], pdist[pix[sr]]);
                     }
                     // a scored child with a non-finite estimate is dropped
