@@ -875,20 +875,20 @@ int fg_index_load(const char *path, uint64_t npoints, uint32_t dim, uint32_t deg
 
 void fg_index_destroy(fg_index *ix) {
     if (!ix) return;
+    // searches still running on the index's own streams (serving batches, a
+    // two-launch search) end before any of its memory is released
+    if (ix->slice_done) (void)hipEventSynchronize(ix->slice_done);
+    for (int i = 0; i < ix->serve_count; ++i) (void)hipStreamSynchronize(ix->serve[i]);
     if (ix->d_rows) (void)hipFree(ix->d_rows);
     if (ix->d_signs) (void)hipFree(ix->d_signs);
     if (ix->d_q) (void)hipFree(ix->d_q);
     if (ix->d_res) (void)hipFree(ix->d_res);
     if (ix->d_cnt) (void)hipFree(ix->d_cnt);
-    if (ix->slice_done) {
-        (void)hipEventSynchronize(ix->slice_done);
-        (void)hipEventDestroy(ix->slice_done);
-    }
+    if (ix->slice_done) (void)hipEventDestroy(ix->slice_done);
     if (ix->d_slice) (void)hipFree(ix->d_slice);
     if (ix->ev0) (void)hipEventDestroy(ix->ev0);
     if (ix->ev1) (void)hipEventDestroy(ix->ev1);
     for (int i = 0; i < ix->serve_count; ++i) {
-        (void)hipStreamSynchronize(ix->serve[i]);
         (void)hipStreamDestroy(ix->serve[i]);
         (void)hipEventDestroy(ix->serve_done[i]);
     }

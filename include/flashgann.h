@@ -91,6 +91,10 @@ int fg_index_create(const float *rows, uint64_t npoints, uint32_t dim, uint32_t 
 int fg_index_load(const char *codebook_path, uint64_t npoints, uint32_t dim, uint32_t degree,
                   int metric, fg_index **out);
 
+/* Releases the index (the destructor, include/qg.hpp:44-47).  The searches
+ * the index keeps track of (fg_search_stream's batches on its internal
+ * streams, the last two-launch search) are waited for first; any other search
+ * the caller queued with fg_search_device must have ended. */
 void fg_index_destroy(fg_index *index);
 
 int fg_index_get_info(const fg_index *index, fg_index_info *info);
