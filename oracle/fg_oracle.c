@@ -60,7 +60,10 @@
  *   mutations                    each rule above planted wrong in a copy of
  *                                this file fails a pin (test_oracle_mutations)
  *   entry point / recall / I/O   the reference's own host headers compiled
- *                                from /root/reference (oracle/_ref)
+ *                                from /root/reference (oracle/_ref), and
+ *                                their recorded outputs
+ *                                (tests/golden/ref_host_golden.npz: ties
+ *                                and centroid rounding included)
  *   whole search                 recall vs brute-force ground truth; a
  *                                complete graph with beam >= n returns the
  *                                brute-force top-K exactly; internal

@@ -1,6 +1,6 @@
 """The oracle's pins are strong enough to catch plausible mistakes in its
 controller, loop sequencing, merge, stage-II selection, task order, id
-validity, distance reduction and result writer:
+validity, distance reduction, result writer, entry point and recall:
 each mutation below is planted in a temporary copy of oracle/fg_oracle.c
 (compiled on the CPU, loaded through FG_ORACLE_LIB in a separate pytest
 process), and the pin tests (hand-traced searches, hand-computed primitives
@@ -97,6 +97,16 @@ MUTATIONS = {
     "query range over the d input dimensions only": (
         "    for (int i = 0; i < padded_dim; ++i) {\n        lo = fminf(lo, qf->rotated[i]);",
         "    for (int i = 0; i < dim; ++i) {\n        lo = fminf(lo, qf->rotated[i]);"),
+    "entry point keeps the last of equal distances": (
+        "        if (dd < best_dist) { best_dist = dd; best = (uint32_t)i; }",
+        "        if (dd <= best_dist) { best_dist = dd; best = (uint32_t)i; }"),
+    "entry-point centroid divides instead of scaling by fl(1/n)": (
+        "            float t = row[d] * inv;", "            float t = row[d] / (float)npoints;"),
+    "recall over all ground-truth columns": (
+        "    const int eval_k = topk < gt_k ? topk : gt_k;", "    const int eval_k = gt_k;"),
+    "recall counts a prediction once per matching column": (
+        "                if (p == gt[i * (uint64_t)gt_k + k]) { ++correct; break; }",
+        "                if (p == gt[i * (uint64_t)gt_k + k]) { ++correct; }"),
     "stage-II out-of-range ids valid": (
         "valid[l] = child[w][l] != FGO_MAX_INDEX && child[w][l] < ix->npoints &&",
         "valid[l] = child[w][l] != FGO_MAX_INDEX &&"),
@@ -120,7 +130,8 @@ def _build(tmp_path, name, mutation):
 
 PIN_TESTS = ["test_oracle_traces.py", "test_oracle_primitives.py",
              "test_oracle_networks.py::test_merge_path_ties_inside_segments_keep_beam_first",
-             "test_oracle_networks.py::test_merge_path_segmentation_with_boundary_ties"]
+             "test_oracle_networks.py::test_merge_path_segmentation_with_boundary_ties",
+             "test_golden_ref_host.py"]
 
 
 def _pins_pass(lib):
