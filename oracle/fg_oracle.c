@@ -53,7 +53,8 @@
  *                                its estimates read from the neighbour's own
  *                                code slot, the
  *                                parent-by-parent task order against the
- *                                32-slot collect cap, out-of-range neighbour
+ *                                32-slot collect cap, a child shared by two
+ *                                parents of a round, out-of-range neighbour
  *                                ids in both stages, and the result writer's
  *                                empty slots (0x7FFFFFFF inside the beam, the
  *                                last id past it)

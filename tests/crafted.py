@@ -403,3 +403,34 @@ def scenario_wide_degree_codes():
         f[4, 1, slot] = 1.0
         f[4, 2, slot] = 0.0
     return cb, q
+
+
+def scenario_shared_child():
+    """Degree 8, beam 64, K 10: two parents of one stage-II round list the
+    same child (node 30).  The entry lists 1 .. 6; 1, 2, 3 are dead ends, so
+    stage II starts at iteration 4 with parents 4, 5, 6.  Parent 4 lists
+    20, 21, 22, 23, 30, 24, 25, 26 and parent 5 lists 31, 30, 32 .. 37; 6 is a
+    dead end.  Both parents see 30 as unvisited (the visited set as it stood
+    at the round's start) and both keep it among their four best; the
+    inserts go in (task, lane) order, so parent 4's copy is the one kept and
+    parent 5's is dropped, leaving parent 5 three children (the reference's
+    warps race here: this is the rule the oracle and the kernel fix)."""
+    dist = {0: 1}
+    adj = {0: [1, 2, 3, 4, 5, 6, None, None]}
+    for i in range(1, 7):
+        dist[i] = 10 * i
+        adj[i] = [0]
+    adj[4] = [20, 21, 22, 23, 30, 24, 25, 26]
+    adj[5] = [31, 30, 32, 33, 34, 35, 36, 37]
+    for k, d in zip((20, 21, 22, 23, 24, 25, 26), (200, 210, 220, 230, 240, 250, 260)):
+        dist[k] = d
+        adj[k] = [4]
+    for k, d in zip((31, 32, 33, 34, 35, 36, 37), (170, 180, 190, 300, 310, 320, 330)):
+        dist[k] = d
+        adj[k] = [5]
+    dist[30] = 150
+    adj[30] = [4]
+    for i in list(range(7, 20)) + [27, 28, 29]:  # unused ids
+        dist[i] = 5000
+        adj[i] = [0]
+    return make(dist, adj, {}, degree=8)

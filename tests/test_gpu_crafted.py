@@ -55,6 +55,7 @@ def test_line_search_at_max_iter(gpu_available, beam):
     ("scenario_wide_degree_codes", 12, 64, [0, 1, 2, 3, 4, 5, 6, 7, 8, 21, 0x7FFFFFFF, 0x7FFFFFFF]),
     ("scenario_task_order", 44, 64, [0] + list(range(1, 12)) + list(range(20, 52))),
     ("scenario_out_of_range_ids", 10, 64, [0, 1, 2, 3, 4, 5, 6, 11, 9, 13]),
+    ("scenario_shared_child", 10, 64, [0, 1, 2, 3, 4, 5, 6, 30, 31, 32]),
 ])
 def test_hand_traced_scenarios(gpu_available, name, K, beam, want):
     cb, q = getattr(crafted, name)()

@@ -107,6 +107,33 @@ MUTATIONS = {
     "recall counts a prediction once per matching column": (
         "                if (p == gt[i * (uint64_t)gt_k + k]) { ++correct; break; }",
         "                if (p == gt[i * (uint64_t)gt_k + k]) { ++correct; }"),
+    "stage-II inserts of a round in reverse task order": (
+        """                for (int w = 0; w < FGO_SEARCH_WIDTH; ++w)
+                    for (int l = 0; l < 32; ++l) {
+                        if (!keepl[w][l]) continue;""",
+        """                for (int w = FGO_SEARCH_WIDTH - 1; w >= 0; --w)
+                    for (int l = 0; l < 32; ++l) {
+                        if (!keepl[w][l]) continue;"""),
+    "stage-II tests see the round's earlier inserts": (
+        """                    if (keep_all) {
+                        for (int l = 0; l < 32; ++l) keepl[w][l] = valid[l];
+                    } else {
+                        fgo_warp_keep_topk(est, valid, eff, keepl[w]);
+                    }
+                }""",
+        """                    if (keep_all) {
+                        for (int l = 0; l < 32; ++l) keepl[w][l] = valid[l];
+                    } else {
+                        fgo_warp_keep_topk(est, valid, eff, keepl[w]);
+                    }
+                    for (int l = 0; l < 32; ++l) {
+                        if (!keepl[w][l]) continue;
+                        keepl[w][l] = 0;
+                        if (!fgo_hash_insert(hash, bitlen, child[w][l])) continue;
+                        const uint32_t slot = compact_count++;
+                        if (slot < collect_cap) { ci[slot] = child[w][l]; cd[slot] = FLT_MAX; }
+                    }
+                }"""),
     "stage-II out-of-range ids valid": (
         "valid[l] = child[w][l] != FGO_MAX_INDEX && child[w][l] < ix->npoints &&",
         "valid[l] = child[w][l] != FGO_MAX_INDEX &&"),

@@ -476,3 +476,29 @@ def test_trace_wide_degree_estimates_read_their_own_slot():
     assert out == [0, 1, 2, 3, 4, 5, 6, 7, 8, 21, 0x7FFFFFFF, 0x7FFFFFFF]
     assert cnt == (6, 10, 368, 3, 10, 4)
     assert tr[4]["cand"] == [21] and tr[4]["cdist"] == [150]
+
+
+def test_trace_shared_child_first_task_keeps_it():
+    """Degree 8, beam 64, K 10 (crafted.scenario_shared_child).
+      it 0: the entry's 6 neighbours (keep ceil(8 * 0.75) = 6 >= 6: all).
+      it 1-3: 1, 2, 3 are dead ends; top-1 0 stalls 1, 2, 3 times.
+      it 4: stage II (rate 1 - 4/8 = 0.5), parents 4, 5, 6, one round.  Each
+            task keeps min(ceil(8 * 0.5), 32 / 8) = 4 of its 8 valid
+            children by estimate: parent 4 keeps 30 (150), 20, 21, 22, in
+            lane order 20, 21, 22, 30; parent 5, which also sees 30 as
+            unvisited (the set as it stood at the round's start), keeps 30,
+            31 (170), 32, 33, in lane order 31, 30, 32, 33.  Inserts in
+            (task, lane) order: parent 4's 30 goes in, parent 5's is a
+            repeat and is dropped: candidates 20, 21, 22, 30, 31, 32, 33.
+            (Seeing parent 4's inserts already would have kept 34 for
+            parent 5; the later task winning would list 31, 30, ... first.)
+      it 5: the seven children (dead ends); it 6 finds nothing.
+    Counters: 6 iterations, 1+1+1+1+3+7 = 14 expansions, 4 x 8 + 3 x 8 +
+    7 x 8 = 112 ids, 8 + 8 = 16 estimates, 1 + 6 + 7 = 14 exact distances."""
+    cb, q = crafted.scenario_shared_child()
+    out, cnt, tr = _trace(cb, q, 10, 64)
+    assert out == [0, 1, 2, 3, 4, 5, 6, 30, 31, 32]
+    assert cnt == (6, 14, 112, 16, 14, 4)
+    assert [t["parents"] for t in tr[:5]] == [[0], [1], [2], [3], [4, 5, 6]]
+    assert tr[4]["cand"] == [20, 21, 22, 30, 31, 32, 33]
+    assert tr[5]["parents"] == [30, 31, 32, 33, 20, 21, 22]
