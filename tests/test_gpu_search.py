@@ -494,3 +494,29 @@ def test_two_launch_search_large_batches(gpu_available, monkeypatch, nq, beam):
     rep = np.arange(nq) % q.shape[0]
     assert np.array_equal(ids2, rids[rep])
     assert np.array_equal(cnt2, rcnt.view(np.uint32).reshape(-1, 6)[rep])
+
+
+@pytest.mark.parametrize("team", ["0", "1"])
+@pytest.mark.parametrize("beam", [64, 512])
+def test_profiling_build_same_ids(gpu_available, monkeypatch, team, beam):
+    """fg_search_profile (the phase-timer instantiation of the kernel, the
+    one-wave and team forms) returns the ids of the ordinary search, and its
+    per-query timers are sane: phase cycle sums >= 0 and start <= end."""
+    import torch
+    import flashgann_amd as fg
+    from flashgann_amd import Index
+    monkeypatch.setenv("FLASHGANN_TEAM", team)
+    cb, q, _ = small_index(n=3000, nq=24, dim=128, comps=16, degree=32)
+    ix = Index.from_codebook(cb)
+    K = 10
+    ids = ix.search(q, K, beam)[0]
+    dq = torch.as_tensor(np.ascontiguousarray(q, np.float32), device="cuda")
+    dres = torch.zeros((len(q), K), dtype=torch.int32, device="cuda")
+    dph = torch.zeros((len(q), fg.FG_PROFILE_SLOTS), dtype=torch.int64, device="cuda")
+    ix.search_profile(dq.data_ptr(), len(q), K, beam, dres.data_ptr(), dph.data_ptr(), 0)
+    torch.cuda.synchronize()
+    ix.close()
+    assert np.array_equal(dres.cpu().numpy().view(np.uint32), ids)
+    ph = dph.cpu().numpy()
+    assert (ph[:, :10] >= 0).all() and (ph[:, :10].sum(1) > 0).all()
+    assert (ph[:, 10] <= ph[:, 11]).all() and (ph[:, 10] > 0).all()
