@@ -369,11 +369,11 @@ def test_trace_task_order_and_collect_cap():
             16 tasks, parent by parent (adaptive_search.cuh:351-354), in
             two rounds of 8.  A first tile keeps min(ceil(32 * 0.1), 32 / 8)
             = 4 >= its 4 children and the 8-slot second tile min(ceil(8 *
-            0.1), 4) = 1 >= its 1: every child is kept, 40 in all.  Round 1
-            (parents 4-7, both tiles) collects 20 .. 39, including the second
+            0.1), 4) = 1 >= its 1: every child is kept, 40 in all.  The first
+            task round (parents 4-7, both tiles) collects 20 .. 39, including the second
             tiles' 24, 29, 34, 39, whatever order its warps take (20 <= 32
             slots); tasks taken tile by tile would fill all 32 slots with
-            first tiles in round 1 instead.  Round 2 (parents 8-11) has 12
+            first tiles in the first task round instead.  The second (parents 8-11) has 12
             slots for its 20 children: in the reference its warps race for
             them, here they go in (task, lane) order, the oracle's stated
             rule: 40 .. 49 (parents 8, 9) and the first two of parent 10's
@@ -389,8 +389,8 @@ def test_trace_task_order_and_collect_cap():
     assert cnt == (9, 44, 1728, 0, 44, 4)
     assert [t["parents"] for t in tr[:5]] == [[0], [1], [2], [3], list(range(4, 12))]
     assert [t["theta"] for t in tr] == [1, 1, 1, 1, 8, 8, 8, 8, 8]
-    assert set(range(20, 40)) <= set(tr[4]["cand"])  # round 1, in any order of its warps
-    assert tr[4]["cand"] == list(range(20, 52))  # round 2 in (task, lane) order
+    assert set(range(20, 40)) <= set(tr[4]["cand"])  # first task round, in any order of its warps
+    assert tr[4]["cand"] == list(range(20, 52))  # second task round in (task, lane) order
     assert [t["parents"] for t in tr[5:]] == [list(range(20 + 8 * i, 28 + 8 * i)) for i in range(4)]
 
 
